@@ -1,0 +1,126 @@
+/*
+ * wdrz_attn.h — C ABI of libwdrz_attn.so, the MI355X (gfx950) attention hot path of
+ * WhisperDRZ.
+ *
+ * Two entry points replace the reference's two attention seams:
+ *
+ *   wdrz_attn_fwd      replaces F.scaled_dot_product_attention as called from
+ *                      MultiHeadAttention.qkv_attention (src/whisperdrz/model.py:276-298,
+ *                      the SDPA call itself at model.py:288-296): encoder self-attention
+ *                      (non-causal, L=1500) and the uncached decoder (causal, top-left).
+ *
+ *   wdrz_attn_kvcache  replaces flash_attn_with_kvcache / its torch fallback
+ *                      _sdpa_attn_with_kvcache (src/whisperdrz/model.py:20-95), as called from
+ *                      MultiHeadAttention.forward_flash (model.py:336-344 cross, 349-359 self):
+ *                      decoder cached self-attention with fused in-place K/V append, decoder
+ *                      cross-attention, and multi-token (prefill / draft-verify) queries.
+ *
+ * Conventions
+ *   - All pointers are device pointers owned by the caller. The library never allocates,
+ *     frees or synchronises, and never reads device memory from the host, so every call is
+ *     safe inside hipGraph stream capture.
+ *   - Strides are in ELEMENTS (not bytes). The last (head_dim) dimension must be contiguous
+ *     (stride 1); every other stride and every base pointer must be 16-byte aligned.
+ *   - head_dim must be 64 (every Whisper size uses 64).
+ *   - `stream` is a hipStream_t (0 = the null stream).
+ *   - Every function returns 0 on success or a WDRZ_E* code; wdrz_last_error() then returns a
+ *     thread-local message naming the offending argument.
+ */
+#ifndef WDRZ_ATTN_H
+#define WDRZ_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Element types (the reference runs fp16 on GPU, model.py:769-770; fp32 on CPU,
+ * transcriber.py:662-663; bf16 is the build's headline type). */
+#define WDRZ_F32 0
+#define WDRZ_F16 1
+#define WDRZ_BF16 2
+
+/* Status codes. */
+#define WDRZ_OK 0
+#define WDRZ_EINVAL 1       /* bad argument (shape, stride, alignment, null pointer) */
+#define WDRZ_EUNSUPPORTED 2 /* valid for the reference but not implemented (e.g. D != 64) */
+#define WDRZ_ELAUNCH 3      /* the HIP launch itself failed */
+#define WDRZ_EWORKSPACE 4   /* workspace missing or too small */
+
+/* Thread-local message for the last failing call on this thread ("" if none). */
+const char* wdrz_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int wdrz_abi_version(void);
+
+/*
+ * Dense scaled-dot-product attention, O = softmax(scale * Q K^T [+ causal mask]) V, per (b, h).
+ *
+ * Replaces: F.scaled_dot_product_attention(q, k, v, is_causal=..., attn_mask=None,
+ *           scale=1/8, dropout_p=0) at src/whisperdrz/model.py:288-296.
+ *
+ * q: [B, H, Lq, D], k, v: [B, H, Lk, D], o: [B, H, Lq, D], each described by 4 strides in
+ * [B, H, L, D] order (the reference passes rearranged, non-contiguous views of the
+ * [B, T, H*D] projection output, model.py:282-284, so strides are honoured).
+ * causal != 0 applies torch's is_causal mask (top-left aligned: query i sees keys j <= i).
+ * dtype: WDRZ_BF16 / WDRZ_F16 use the MFMA kernel; WDRZ_F32 uses an fp32 kernel.
+ */
+int wdrz_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* o, int64_t B,
+                  int64_t H, int64_t Lq, int64_t Lk, int64_t D, const int64_t* q_strides,
+                  const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+                  float scale, int causal, void* stream);
+
+/*
+ * Workspace (bytes) that wdrz_attn_kvcache needs for these sizes. 0 means none is needed.
+ * No counterpart in the reference: flash-attn allocates its split-KV scratch internally; this
+ * library leaves allocation to the caller so calls can be captured into a hipGraph.
+ */
+size_t wdrz_attn_kvcache_workspace_size(int64_t B, int64_t sq, int64_t H, int64_t D,
+                                        int64_t Lmax);
+
+/*
+ * Attention against a slot KV cache.
+ *
+ * Replaces: flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, cache_seqlens=None,
+ *           cache_batch_idx=None, softmax_scale=None, causal=False)
+ *           (dispatcher src/whisperdrz/model.py:88-95; semantics of the torch fallback
+ *           _sdpa_attn_with_kvcache, model.py:20-76).
+ *
+ * q:        [B, sq, H, D]                      strides q_strides[4]
+ * k_cache,  [n_slots, Lmax, H, D]              strides kc_strides[4], vc_strides[4]
+ * v_cache
+ * k_new,    [B, sq, H, D] or both NULL         strides kn_strides[4], vn_strides[4]
+ * v_new
+ * cache_seqlens   int32 [B]: pre-append length per batch row (required iff k_new given)
+ * cache_batch_idx int32 [B]: batch row -> slot (NULL = identity; must be < n_slots)
+ * o:        [B, sq, H, D], same dtype as q     strides o_strides[4]
+ *
+ * Self-attention (k_new != NULL), model.py:49-63:
+ *   k_new[b, t], v_new[b, t] are written IN PLACE to cache row cache_seqlens[b] + t of slot
+ *   cache_batch_idx[b]; query t attends keys j <= cache_seqlens[b] + t (bottom-right causal).
+ *   cache_seqlens itself is NOT modified (the caller bumps it, model.py:602-607).
+ * Cross-attention (k_new == NULL), model.py:64-67: non-causal attention over all Lmax rows
+ *   (cache_seqlens is ignored, as in the fallback).
+ * `causal` is accepted for signature parity; as in the fallback, the mask is decided by
+ *   whether k_new is given.
+ * Duplicate cache_batch_idx entries with k_new given write the same cache rows from several
+ *   batch rows; which write lands is unspecified (as with flash-attn).
+ * workspace: device buffer of at least wdrz_attn_kvcache_workspace_size(...) bytes (may be
+ *   NULL when that is 0). Concurrent calls must not share a workspace.
+ */
+int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, const void* k_new,
+                      const void* v_new, const int32_t* cache_seqlens,
+                      const int32_t* cache_batch_idx, void* o, int64_t B, int64_t sq, int64_t H,
+                      int64_t D, int64_t n_slots, int64_t Lmax, const int64_t* q_strides,
+                      const int64_t* kc_strides, const int64_t* vc_strides,
+                      const int64_t* kn_strides, const int64_t* vn_strides,
+                      const int64_t* o_strides, float softmax_scale, int causal, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WDRZ_ATTN_H */

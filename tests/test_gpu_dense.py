@@ -1,0 +1,113 @@
+"""Parity of the dense SDPA kernels (encoder / uncached decoder) with the float64 oracle.
+
+Reference seam: F.scaled_dot_product_attention at src/whisperdrz/model.py:288-296.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention_oracle import sdpa_ref
+from tests._util import assert_close, randn, to_np
+
+pytestmark = pytest.mark.gpu
+
+SHAPES = [
+    # (B, H, Lq, Lk, causal)
+    (1, 1, 1, 1, False),
+    (2, 3, 37, 100, False),
+    (1, 2, 64, 64, False),
+    (2, 2, 65, 130, False),
+    (1, 2, 300, 1500, False),
+    (1, 2, 1500, 1500, False),
+    (2, 2, 200, 200, True),
+    (1, 3, 448, 448, True),
+    (1, 2, 100, 300, True),
+    (1, 2, 300, 100, True),
+    (1, 1, 257, 257, True),
+]
+
+
+def _run(cuda, dtype, B, H, Lq, Lk, causal, seed, layout="btHd"):
+    D = 64
+    if layout == "btHd":
+        # the reference's layout: [B, T, H*D] projections viewed as [B, H, T, D]
+        q = randn((B, Lq, H, D), seed, dtype).to(cuda).permute(0, 2, 1, 3)
+        k = randn((B, Lk, H, D), seed + 1, dtype).to(cuda).permute(0, 2, 1, 3)
+        v = randn((B, Lk, H, D), seed + 2, dtype).to(cuda).permute(0, 2, 1, 3)
+    else:
+        q = randn((B, H, Lq, D), seed, dtype).to(cuda)
+        k = randn((B, H, Lk, D), seed + 1, dtype).to(cuda)
+        v = randn((B, H, Lk, D), seed + 2, dtype).to(cuda)
+    from whisperdrz_amd import scaled_dot_product_attention
+
+    out = scaled_dot_product_attention(q, k, v, is_causal=causal, scale=0.125)
+    torch.cuda.synchronize()
+    ref = sdpa_ref(to_np(q), to_np(k), to_np(v), scale=0.125, causal=causal)
+    return out, ref
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("B,H,Lq,Lk,causal", SHAPES)
+def test_dense_parity(cuda, dtype, B, H, Lq, Lk, causal):
+    print(f"dense dtype={dtype} B={B} H={H} Lq={Lq} Lk={Lk} causal={causal}", flush=True)
+    out, ref = _run(cuda, dtype, B, H, Lq, Lk, causal, seed=1000 + Lq + Lk)
+    assert out.shape == (B, H, Lq, 64)
+    assert_close(out, ref, dtype, "dense")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_dense_contiguous_bhld(cuda, dtype):
+    out, ref = _run(cuda, dtype, 2, 2, 129, 77, False, seed=7, layout="bhld")
+    assert_close(out, ref, dtype, "dense bhld")
+
+
+def test_config1_fp32_full_shape(cuda):
+    """Config 1: B=1, H=20, L=1500, D=64, fp32, scale 1/8 — max|diff| <= 1e-5 * max|ref|."""
+    out, ref = _run(cuda, torch.float32, 1, 20, 1500, 1500, False, seed=2024, layout="bhld")
+    err = assert_close(out, ref, torch.float32, "config1")
+    # elementwise report (rtol=1e-5, atol=1e-6)
+    got = to_np(out)
+    frac = float(np.mean(np.abs(got - ref) <= 1e-6 + 1e-5 * np.abs(ref)))
+    print(f"config1 max|diff|={err:.3e} elementwise-within(rtol=1e-5, atol=1e-6)={frac:.6f}")
+
+
+def test_config2_layer_bf16_sample(cuda):
+    """Config 2 shape (B=16, H=20, L=1500, bf16): whole-batch run, two (b, h) pairs checked."""
+    B, H, L, D = 16, 20, 1500, 64
+    q = randn((B, L, H, D), 11, torch.bfloat16).to(cuda)
+    k = randn((B, L, H, D), 12, torch.bfloat16).to(cuda)
+    v = randn((B, L, H, D), 13, torch.bfloat16).to(cuda)
+    from whisperdrz_amd import scaled_dot_product_attention
+
+    out = scaled_dot_product_attention(
+        q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3), scale=0.125
+    )
+    torch.cuda.synchronize()
+    for b, h in ((0, 0), (15, 19), (7, 11)):
+        ref = sdpa_ref(
+            to_np(q[b : b + 1, :, h : h + 1].permute(0, 2, 1, 3)),
+            to_np(k[b : b + 1, :, h : h + 1].permute(0, 2, 1, 3)),
+            to_np(v[b : b + 1, :, h : h + 1].permute(0, 2, 1, 3)),
+            scale=0.125,
+        )
+        assert_close(out[b : b + 1, h : h + 1], ref, torch.bfloat16, f"config2 b={b} h={h}")
+
+
+def test_qkv_attention_helper(cuda):
+    """qkv_attention on [B, T, H*D] projections == oracle (model.py:276-298, causal n_ctx>1)."""
+    from whisperdrz_amd import qkv_attention
+
+    B, T, H, D = 2, 33, 4, 64
+    q = randn((B, T, H * D), 1, torch.float32).to(cuda)
+    k = randn((B, T, H * D), 2, torch.float32).to(cuda)
+    v = randn((B, T, H * D), 3, torch.float32).to(cuda)
+    out = qkv_attention(q, k, v, H, causal=True)
+    ref = sdpa_ref(
+        to_np(q.view(B, T, H, D).permute(0, 2, 1, 3)),
+        to_np(k.view(B, T, H, D).permute(0, 2, 1, 3)),
+        to_np(v.view(B, T, H, D).permute(0, 2, 1, 3)),
+        scale=0.125,
+        causal=True,
+    )
+    ref = ref.transpose(0, 2, 1, 3).reshape(B, T, H * D)
+    assert_close(out, ref, torch.float32, "qkv_attention")

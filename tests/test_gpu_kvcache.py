@@ -1,0 +1,143 @@
+"""Parity of the cached decoder kernels with the float64 restatement of the reference fallback.
+
+Reference seam: flash_attn_with_kvcache / _sdpa_attn_with_kvcache, src/whisperdrz/model.py:20-95.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.attention_oracle import kvcache_ref
+from tests._util import assert_close, make_cache, randn, to_np
+
+pytestmark = pytest.mark.gpu
+
+D = 64
+
+
+def _case(cuda, dtype, B, sq, H, n_slots, Lmax, layout, seed, self_attn=True, bidx_mode="perm", cs=None):
+    from whisperdrz_amd import flash_attn_with_kvcache
+
+    rng = np.random.default_rng(seed)
+    kc, vc = make_cache(n_slots, Lmax, H, D, dtype, cuda, layout, seed)
+    kc0, vc0 = to_np(kc), to_np(vc)
+    q = randn((B, sq, H, D), seed + 10, dtype).to(cuda)
+    if bidx_mode == "perm":
+        bidx_np = rng.permutation(n_slots)[:B].astype(np.int32)
+        bidx = torch.from_numpy(bidx_np).to(cuda)
+    else:
+        bidx_np, bidx = None, None
+    if self_attn:
+        k = randn((B, sq, H, D), seed + 11, dtype).to(cuda)
+        v = randn((B, sq, H, D), seed + 12, dtype).to(cuda)
+        if cs is None:
+            cs = rng.integers(0, Lmax - sq + 1, size=B)
+            cs[0] = 0
+            if B > 1:
+                cs[-1] = Lmax - sq
+        cs = np.asarray(cs, dtype=np.int32)
+        seqlens = torch.from_numpy(cs).to(cuda)
+        seqlens_before = seqlens.clone()
+        out = flash_attn_with_kvcache(q, kc, vc, k=k, v=v, cache_seqlens=seqlens, cache_batch_idx=bidx,
+                                      softmax_scale=0.125, causal=True)
+        torch.cuda.synchronize()
+        assert torch.equal(seqlens, seqlens_before), "cache_seqlens must not be modified"
+        ref, kref, vref = kvcache_ref(to_np(q), kc0, vc0, to_np(k), to_np(v), cs, bidx_np, 0.125)
+    else:
+        out = flash_attn_with_kvcache(q, kc, vc, cache_batch_idx=bidx, softmax_scale=0.125, causal=False)
+        torch.cuda.synchronize()
+        ref, kref, vref = kvcache_ref(to_np(q), kc0, vc0, None, None, None, bidx_np, 0.125)
+    assert out.shape == (B, sq, H, D) and out.dtype == dtype
+    assert_close(out, ref, dtype, f"kvcache self={self_attn}")
+    # the post-append cache is bit-identical to the reference's (untouched rows/slots included)
+    assert np.array_equal(to_np(kc), kref), "k_cache differs from the reference after append"
+    assert np.array_equal(to_np(vc), vref), "v_cache differs from the reference after append"
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("sq", [1, 2, 5, 7, 8, 9, 17])
+@pytest.mark.parametrize("layout", ["slot_major", "head_major"])
+def test_self_attention(cuda, dtype, sq, layout):
+    print(f"self dtype={dtype} sq={sq} layout={layout}", flush=True)
+    _case(cuda, dtype, B=6, sq=sq, H=4, n_slots=9, Lmax=448, layout=layout, seed=100 + sq)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("Lmax", [1, 63, 100, 1500])
+@pytest.mark.parametrize("sq", [1, 5])
+def test_cross_attention(cuda, dtype, Lmax, sq):
+    print(f"cross dtype={dtype} Lmax={Lmax} sq={sq}", flush=True)
+    _case(cuda, dtype, B=5, sq=sq, H=3, n_slots=7, Lmax=Lmax, layout="head_major", seed=200 + Lmax,
+          self_attn=False)
+
+
+@pytest.mark.parametrize("self_attn", [True, False])
+def test_identity_batch_idx(cuda, self_attn):
+    _case(cuda, torch.bfloat16, B=4, sq=1, H=2, n_slots=4, Lmax=200, layout="slot_major", seed=5,
+          self_attn=self_attn, bidx_mode="none")
+
+
+@pytest.mark.parametrize("B,H,Lmax", [(1, 20, 448), (2, 20, 1500), (1, 1, 1500), (3, 5, 448)])
+@pytest.mark.parametrize("self_attn", [True, False])
+def test_split_kv_paths(cuda, B, H, Lmax, self_attn):
+    """Small batches split the keys over several workgroups (workspace + combine pass)."""
+    from whisperdrz_amd import kvcache_workspace_size
+
+    assert kvcache_workspace_size(B, 1, H, D, Lmax) > 0
+    _case(cuda, torch.bfloat16, B=B, sq=1, H=H, n_slots=B + 2, Lmax=Lmax, layout="head_major", seed=300 + B,
+          self_attn=self_attn)
+
+
+def test_config3_shape_fp32_tolerance(cuda):
+    """Config 3 shape at fp32: 64 streams, H=20, L_i ~ U[1,448], capacity 448."""
+    from oracle.attention_oracle import decode_lengths
+
+    L = decode_lengths(3, 64, 1, 448)
+    _case(cuda, torch.float32, B=64, sq=1, H=20, n_slots=64, Lmax=448, layout="head_major", seed=3,
+          cs=L - 1)
+
+
+def test_verify_equals_sequential_steps(cuda):
+    """A 5-token causal draft == 5 sequential 1-token steps (config 5's check)."""
+    from whisperdrz_amd import flash_attn_with_kvcache
+
+    B, H, Lmax, sq = 8, 20, 448, 5
+    for dtype in (torch.bfloat16, torch.float32):
+        rng = np.random.default_rng(9)
+        cs = rng.integers(0, Lmax - sq + 1, size=B).astype(np.int32)
+        kc, vc = make_cache(B, Lmax, H, D, dtype, cuda, "head_major", 9)
+        kc2, vc2 = kc.clone(), vc.clone()
+        q = randn((B, sq, H, D), 91, dtype).to(cuda)
+        k = randn((B, sq, H, D), 92, dtype).to(cuda)
+        v = randn((B, sq, H, D), 93, dtype).to(cuda)
+        seq = torch.from_numpy(cs).to(cuda)
+        bidx = torch.arange(B, dtype=torch.int32, device=cuda)
+        out = flash_attn_with_kvcache(q, kc, vc, k=k, v=v, cache_seqlens=seq, cache_batch_idx=bidx, softmax_scale=0.125)
+        steps = []
+        for t in range(sq):
+            o = flash_attn_with_kvcache(q[:, t : t + 1].contiguous(), kc2, vc2, k=k[:, t : t + 1].contiguous(),
+                                        v=v[:, t : t + 1].contiguous(), cache_seqlens=seq + t, cache_batch_idx=bidx,
+                                        softmax_scale=0.125)
+            steps.append(o)
+        seqout = torch.cat(steps, dim=1)
+        torch.cuda.synchronize()
+        assert torch.equal(kc, kc2) and torch.equal(vc, vc2)
+        assert_close(out, to_np(seqout), dtype, "verify vs sequential")
+
+
+def test_bad_slot_gives_nan_not_fault(cuda):
+    """An out-of-range slot id (which the host cannot see) yields NaN rows and no memory access."""
+    from whisperdrz_amd import flash_attn_with_kvcache
+
+    kc, vc = make_cache(3, 64, 2, D, torch.bfloat16, cuda, "slot_major", 1)
+    snap_k = kc.clone()
+    q = randn((2, 1, 2, D), 2, torch.bfloat16).to(cuda)
+    k = randn((2, 1, 2, D), 3, torch.bfloat16).to(cuda)
+    bidx = torch.tensor([1, 3], dtype=torch.int32, device=cuda)
+    seq = torch.tensor([5, 5], dtype=torch.int32, device=cuda)
+    out = flash_attn_with_kvcache(q, kc, vc, k=k, v=k, cache_seqlens=seq, cache_batch_idx=bidx)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out[0].float()).all()
+    assert torch.isnan(out[1].float()).all()
+    snap_k[1, 5] = k[0, 0]
+    assert torch.equal(kc, snap_k)

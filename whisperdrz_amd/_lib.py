@@ -1,0 +1,103 @@
+"""ctypes binding of libwdrz_attn.so (the C ABI declared in include/wdrz_attn.h).
+
+The library is loaded lazily and exactly once. There is no fallback: if the shared object is
+missing or fails to load, every compute entry point raises ``RuntimeError``.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libwdrz_attn.so"
+
+WDRZ_F32, WDRZ_F16, WDRZ_BF16 = 0, 1, 2
+WDRZ_OK, WDRZ_EINVAL, WDRZ_EUNSUPPORTED, WDRZ_ELAUNCH, WDRZ_EWORKSPACE = 0, 1, 2, 3, 4
+
+# Every symbol include/wdrz_attn.h declares (tests check the .so exports all of them).
+EXPORTED_SYMBOLS = (
+    "wdrz_last_error",
+    "wdrz_abi_version",
+    "wdrz_attn_fwd",
+    "wdrz_attn_kvcache_workspace_size",
+    "wdrz_attn_kvcache",
+)
+ABI_VERSION = 1
+
+_lock = threading.Lock()
+_lib = None
+_load_error: str | None = None
+
+_i64 = ctypes.c_int64
+_p = ctypes.c_void_p
+_i64p = ctypes.POINTER(ctypes.c_int64)
+_i32p = ctypes.c_void_p
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    lib.wdrz_last_error.restype = ctypes.c_char_p
+    lib.wdrz_last_error.argtypes = []
+    lib.wdrz_abi_version.restype = ctypes.c_int
+    lib.wdrz_abi_version.argtypes = []
+    lib.wdrz_attn_fwd.restype = ctypes.c_int
+    lib.wdrz_attn_fwd.argtypes = [
+        ctypes.c_int, _p, _p, _p, _p,  # dtype, q, k, v, o
+        _i64, _i64, _i64, _i64, _i64,  # B, H, Lq, Lk, D
+        _i64p, _i64p, _i64p, _i64p,  # strides
+        ctypes.c_float, ctypes.c_int, _p,  # scale, causal, stream
+    ]
+    lib.wdrz_attn_kvcache_workspace_size.restype = ctypes.c_size_t
+    lib.wdrz_attn_kvcache_workspace_size.argtypes = [_i64, _i64, _i64, _i64, _i64]
+    lib.wdrz_attn_kvcache.restype = ctypes.c_int
+    lib.wdrz_attn_kvcache.argtypes = [
+        ctypes.c_int, _p, _p, _p, _p, _p,  # dtype, q, k_cache, v_cache, k_new, v_new
+        _i32p, _i32p, _p,  # cache_seqlens, cache_batch_idx, out
+        _i64, _i64, _i64, _i64, _i64, _i64,  # B, sq, H, D, n_slots, Lmax
+        _i64p, _i64p, _i64p, _i64p, _i64p, _i64p,  # strides
+        ctypes.c_float, ctypes.c_int,  # softmax_scale, causal
+        _p, ctypes.c_size_t, _p,  # workspace, bytes, stream
+    ]
+
+
+def load() -> ctypes.CDLL:
+    """Return the loaded library, raising RuntimeError when it cannot be loaded."""
+    global _lib, _load_error
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is not None:
+            return _lib
+        if not LIB_PATH.exists():
+            _load_error = (
+                f"{LIB_PATH} is not built; run `python -m whisperdrz_amd.build` "
+                "(or __graft_entry__.build())"
+            )
+            raise RuntimeError(_load_error)
+        try:
+            lib = ctypes.CDLL(str(LIB_PATH))
+        except OSError as exc:  # pragma: no cover - depends on the environment
+            _load_error = f"failed to load {LIB_PATH}: {exc}"
+            raise RuntimeError(_load_error) from exc
+        _declare(lib)
+        if lib.wdrz_abi_version() != ABI_VERSION:
+            raise RuntimeError(
+                f"{LIB_PATH} has ABI {lib.wdrz_abi_version()}, expected {ABI_VERSION}; rebuild it"
+            )
+        _lib = lib
+        return lib
+
+
+def available() -> bool:
+    try:
+        load()
+        return True
+    except RuntimeError:
+        return False
+
+
+def last_error() -> str:
+    return load().wdrz_last_error().decode()
+
+
+def strides4(s) -> ctypes.Array:
+    return (ctypes.c_int64 * 4)(*[int(x) for x in s])

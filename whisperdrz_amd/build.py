@@ -1,0 +1,72 @@
+"""Build libwdrz_attn.so in-tree with hipcc for gfx950.
+
+Usage: python -m whisperdrz_amd.build [--debug]
+
+The library is a plain shared object (no torch / pybind dependency); the Python side loads it
+with ctypes. ``--debug`` builds with -O1 -g and device-side bounds assertions off, for host
+debugging only.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+CSRC = PKG_DIR / "csrc"
+LIB_NAME = "libwdrz_attn.so"
+LIB_PATH = PKG_DIR / LIB_NAME
+SOURCES = ["attn_kvcache.hip", "attn_dense.hip", "wdrz_capi.cpp"]
+ARCH = "gfx950"
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (ROCm toolchain required to build libwdrz_attn.so)")
+
+
+def build_library(debug: bool = False, verbose: bool = False) -> Path:
+    """Compile every source for gfx950 and link libwdrz_attn.so next to this file."""
+    out_dir = PKG_DIR / "_build"
+    out_dir.mkdir(exist_ok=True)
+    opt = ["-O1", "-g"] if debug else ["-O3"]
+    common = [
+        f"--offload-arch={ARCH}",
+        "-fPIC",
+        "-std=c++17",
+        "-Wall",
+        "-Wno-unused-function",
+        *opt,
+    ]
+    # Packed-fp32 instructions are disabled for all device code (they have returned wrong
+    # results on these boxes); the flag is device-only, hipcc's host pass merely warns.
+    device_flags = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
+    objs = []
+    for src in SOURCES:
+        obj = out_dir / (src + ".o")
+        cmd = [hipcc(), *common, "-c", str(CSRC / src), "-o", str(obj)]
+        if src.endswith(".hip"):
+            cmd[1:1] = ["-x", "hip"]
+            cmd += device_flags
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"hipcc failed for {src}:\n{proc.stderr}")
+        objs.append(str(obj))
+    tmp = out_dir / (LIB_NAME + ".tmp")
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{proc.stderr}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    p = build_library(debug="--debug" in sys.argv, verbose=True)
+    print(p)

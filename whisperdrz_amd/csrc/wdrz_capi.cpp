@@ -1,0 +1,223 @@
+// wdrz_capi.cpp — the extern "C" boundary of libwdrz_attn.so (declared in include/wdrz_attn.h).
+//
+// Host-side only: validates every argument that can be checked without reading device memory,
+// converts element strides to byte strides, and forwards to the kernel launchers. Nothing here
+// allocates, frees, synchronises or reads device memory, so the entry points may be called
+// during hipGraph stream capture.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <string>
+
+#include "../../include/wdrz_attn.h"
+#include "wdrz_launch.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int elem_bytes(int dtype) {
+  switch (dtype) {
+    case WDRZ_F32:
+      return 4;
+    case WDRZ_F16:
+    case WDRZ_BF16:
+      return 2;
+    default:
+      return 0;
+  }
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Checks a 4-stride tensor description (element strides): last stride 1, others 16-B aligned.
+int check_strides(const char* name, const int64_t* s, int eb) {
+  if (!s) return fail(WDRZ_EINVAL, "%s: strides pointer is NULL", name);
+  if (s[3] != 1) return fail(WDRZ_EINVAL, "%s: head_dim stride must be 1 (got %lld)", name, (long long)s[3]);
+  for (int i = 0; i < 3; ++i) {
+    if (((s[i] * eb) & 15) != 0)
+      return fail(WDRZ_EINVAL, "%s: stride[%d]=%lld elements is not 16-byte aligned", name, i, (long long)s[i]);
+  }
+  return WDRZ_OK;
+}
+
+int check_ptr(const char* name, const void* p) {
+  if (!p) return fail(WDRZ_EINVAL, "%s is NULL", name);
+  if (!aligned16(p)) return fail(WDRZ_EINVAL, "%s is not 16-byte aligned", name);
+  return WDRZ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* wdrz_last_error(void) { return g_last_error.c_str(); }
+
+int wdrz_abi_version(void) { return 1; }
+
+int wdrz_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* o, int64_t B, int64_t H,
+                  int64_t Lq, int64_t Lk, int64_t D, const int64_t* q_strides, const int64_t* k_strides,
+                  const int64_t* v_strides, const int64_t* o_strides, float scale, int causal, void* stream) {
+  g_last_error.clear();
+  const int eb = elem_bytes(dtype);
+  if (!eb) return fail(WDRZ_EINVAL, "dtype %d is not one of WDRZ_F32/F16/BF16", dtype);
+  if (D != 64) return fail(WDRZ_EUNSUPPORTED, "head_dim %lld is not supported (only 64)", (long long)D);
+  if (B < 0 || H <= 0 || Lq < 0 || Lk <= 0)
+    return fail(WDRZ_EINVAL, "bad sizes B=%lld H=%lld Lq=%lld Lk=%lld", (long long)B, (long long)H,
+                (long long)Lq, (long long)Lk);
+  if (B > 65535 || H > 65535 || Lq > (1 << 24) || Lk > (1 << 24))
+    return fail(WDRZ_EUNSUPPORTED, "sizes too large");
+  if (!(scale > 0.f) || scale != scale) return fail(WDRZ_EINVAL, "scale must be a positive finite number");
+  int rc;
+  if ((rc = check_ptr("q", q)) || (rc = check_ptr("k", k)) || (rc = check_ptr("v", v)) || (rc = check_ptr("o", o)))
+    return rc;
+  if ((rc = check_strides("q", q_strides, eb)) || (rc = check_strides("k", k_strides, eb)) ||
+      (rc = check_strides("v", v_strides, eb)) || (rc = check_strides("o", o_strides, eb)))
+    return rc;
+  if (B == 0 || Lq == 0) return WDRZ_OK;
+  const float c = scale * 1.4426950408889634f;
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipError_t err;
+  if (dtype == WDRZ_F32) {
+    // fp32: the split-KV kernel with the query axis blocked by 8 (dense view of the cache:
+    // "slot" = b, position = l, head = h).
+    wdrz::KvArgs a{};
+    a.q = static_cast<const char*>(q);
+    a.kc = static_cast<char*>(const_cast<void*>(k));
+    a.vc = static_cast<char*>(const_cast<void*>(v));
+    a.o = static_cast<char*>(o);
+    a.B = (int)B;
+    a.sq = (int)Lq;
+    a.H = (int)H;
+    a.Lk = (int)Lk;
+    a.n_slots = (int)B;
+    a.n_qblocks = (int)((Lq + 7) / 8);
+    a.causal = causal ? 1 : 0;
+    // [B, H, L, D] strides -> (batch, position, head) byte strides.
+    const int64_t* S[4] = {q_strides, k_strides, v_strides, o_strides};
+    int64_t* Dst[4] = {a.qs, a.kcs, a.vcs, a.os};
+    for (int i = 0; i < 4; ++i) {
+      Dst[i][0] = S[i][0] * eb;
+      Dst[i][1] = S[i][2] * eb;
+      Dst[i][2] = S[i][1] * eb;
+    }
+    a.c = c;
+    a.n_splits = 1;
+    a.split_len = (int)Lk;  // the query blocks already fill the GPU; no workspace needed
+    err = wdrz::launch_kv_attn(dtype, a, st);
+  } else {
+    wdrz::DenseArgs a{};
+    a.q = q;
+    a.k = k;
+    a.v = v;
+    a.o = o;
+    a.B = (int)B;
+    a.H = (int)H;
+    a.Lq = (int)Lq;
+    a.Lk = (int)Lk;
+    a.causal = causal ? 1 : 0;
+    const int64_t* S[4] = {q_strides, k_strides, v_strides, o_strides};
+    int64_t* Dst[4] = {a.qs, a.ks, a.vs, a.os};
+    for (int i = 0; i < 4; ++i)
+      for (int j = 0; j < 3; ++j) Dst[i][j] = S[i][j];
+    a.c = c;
+    err = wdrz::launch_dense_mfma(dtype, a, st);
+  }
+  if (err != hipSuccess) return fail(WDRZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  return WDRZ_OK;
+}
+
+size_t wdrz_attn_kvcache_workspace_size(int64_t B, int64_t sq, int64_t H, int64_t D, int64_t Lmax) {
+  (void)D;
+  if (B <= 0 || sq <= 0 || H <= 0 || Lmax <= 0) return 0;
+  int n_splits, split_len;
+  wdrz::kv_split_plan(B * H * ((sq + 7) / 8), Lmax, &n_splits, &split_len);
+  return wdrz::kv_workspace_bytes(B, sq, H, n_splits);
+}
+
+int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, const void* k_new, const void* v_new,
+                      const int32_t* cache_seqlens, const int32_t* cache_batch_idx, void* o, int64_t B, int64_t sq,
+                      int64_t H, int64_t D, int64_t n_slots, int64_t Lmax, const int64_t* q_strides,
+                      const int64_t* kc_strides, const int64_t* vc_strides, const int64_t* kn_strides,
+                      const int64_t* vn_strides, const int64_t* o_strides, float softmax_scale, int causal,
+                      void* workspace, size_t workspace_bytes, void* stream) {
+  (void)causal;
+  g_last_error.clear();
+  const int eb = elem_bytes(dtype);
+  if (!eb) return fail(WDRZ_EINVAL, "dtype %d is not one of WDRZ_F32/F16/BF16", dtype);
+  if (D != 64) return fail(WDRZ_EUNSUPPORTED, "head_dim %lld is not supported (only 64)", (long long)D);
+  if (B < 0 || sq <= 0 || H <= 0 || n_slots <= 0 || Lmax <= 0)
+    return fail(WDRZ_EINVAL, "bad sizes B=%lld sq=%lld H=%lld n_slots=%lld Lmax=%lld", (long long)B,
+                (long long)sq, (long long)H, (long long)n_slots, (long long)Lmax);
+  if (B > (1 << 20) || H > 65535 || sq > 4096 || Lmax > (1 << 24) || n_slots > (1 << 24))
+    return fail(WDRZ_EUNSUPPORTED, "sizes too large");
+  if (!(softmax_scale > 0.f) || softmax_scale != softmax_scale)
+    return fail(WDRZ_EINVAL, "softmax_scale must be a positive finite number");
+  const bool has_new = k_new != nullptr || v_new != nullptr;
+  if (has_new && (!k_new || !v_new)) return fail(WDRZ_EINVAL, "k and v must be given together");
+  if (has_new && !cache_seqlens) return fail(WDRZ_EINVAL, "cache_seqlens is required when k/v are given");
+  if (has_new && sq > Lmax) return fail(WDRZ_EINVAL, "sq=%lld exceeds cache length %lld", (long long)sq, (long long)Lmax);
+  int rc;
+  if ((rc = check_ptr("q", q)) || (rc = check_ptr("k_cache", k_cache)) || (rc = check_ptr("v_cache", v_cache)) ||
+      (rc = check_ptr("out", o)))
+    return rc;
+  if ((rc = check_strides("q", q_strides, eb)) || (rc = check_strides("k_cache", kc_strides, eb)) ||
+      (rc = check_strides("v_cache", vc_strides, eb)) || (rc = check_strides("out", o_strides, eb)))
+    return rc;
+  if (has_new) {
+    if ((rc = check_ptr("k", k_new)) || (rc = check_ptr("v", v_new))) return rc;
+    if ((rc = check_strides("k", kn_strides, eb)) || (rc = check_strides("v", vn_strides, eb))) return rc;
+  }
+  if (B == 0) return WDRZ_OK;
+
+  wdrz::KvArgs a{};
+  a.q = static_cast<const char*>(q);
+  a.kc = static_cast<char*>(k_cache);
+  a.vc = static_cast<char*>(v_cache);
+  a.kn = has_new ? static_cast<const char*>(k_new) : nullptr;
+  a.vn = has_new ? static_cast<const char*>(v_new) : nullptr;
+  a.seqlens = has_new ? cache_seqlens : nullptr;
+  a.bidx = cache_batch_idx;
+  a.o = static_cast<char*>(o);
+  a.B = (int)B;
+  a.sq = (int)sq;
+  a.H = (int)H;
+  a.Lk = (int)Lmax;
+  a.n_slots = (int)n_slots;
+  a.n_qblocks = (int)((sq + 7) / 8);
+  a.causal = 0;
+  const int64_t* S[4] = {q_strides, kc_strides, vc_strides, o_strides};
+  int64_t* Dst[4] = {a.qs, a.kcs, a.vcs, a.os};
+  for (int i = 0; i < 4; ++i)
+    for (int j = 0; j < 3; ++j) Dst[i][j] = S[i][j] * eb;
+  if (has_new)
+    for (int j = 0; j < 3; ++j) {
+      a.kns[j] = kn_strides[j] * eb;
+      a.vns[j] = vn_strides[j] * eb;
+    }
+  a.c = softmax_scale * 1.4426950408889634f;
+  wdrz::kv_split_plan(B * H * a.n_qblocks, Lmax, &a.n_splits, &a.split_len);
+  const size_t need = wdrz::kv_workspace_bytes(B, sq, H, a.n_splits);
+  if (need > 0) {
+    if (!workspace || workspace_bytes < need)
+      return fail(WDRZ_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace ? workspace_bytes : 0);
+    if (!aligned16(workspace)) return fail(WDRZ_EINVAL, "workspace is not 16-byte aligned");
+    a.ws = static_cast<float*>(workspace);
+  }
+  hipError_t err = wdrz::launch_kv_attn(dtype, a, reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(WDRZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  return WDRZ_OK;
+}
+
+}  // extern "C"

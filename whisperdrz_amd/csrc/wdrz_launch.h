@@ -1,0 +1,51 @@
+// wdrz_launch.h — internal (C++) launch interface between the C-ABI layer and the kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace wdrz {
+
+// Split-KV attention over a key/value store, used both for the cached decoder paths and for
+// the fp32 dense path. Strides are in BYTES; the last (head_dim) dimension is contiguous.
+//
+// Query row (b, t, h) lives at q + b*qs[0] + t*qs[1] + h*qs[2] (same for o, k_new, v_new).
+// Key j of batch row b, head h lives at kv + slot(b)*kvs[0] + j*kvs[1] + h*kvs[2].
+struct KvArgs {
+  const char* q;
+  char* kc;
+  char* vc;
+  const char* kn;  // k_new (nullptr: no append)
+  const char* vn;
+  const int32_t* seqlens;  // pre-append lengths (required with k_new)
+  const int32_t* bidx;     // batch row -> slot (nullptr: identity)
+  char* o;
+  float* ws;  // split partials, nullptr when n_splits == 1
+  int B, sq, H, Lk, n_slots, n_qblocks, n_splits, split_len;
+  int causal;  // top-left causal mask (dense path only; the append path is always causal)
+  int64_t qs[3], kcs[3], vcs[3], kns[3], vns[3], os[3];
+  float c;  // softmax scale * log2(e)
+};
+
+// Split count and keys per split for B*H*n_qblocks work units over Lk keys. Depends only on
+// sizes, so the workspace size can be queried without data.
+void kv_split_plan(int64_t units, int64_t Lk, int* n_splits, int* split_len);
+size_t kv_workspace_bytes(int64_t B, int64_t sq, int64_t H, int n_splits);
+
+// Launch the split-KV kernel (+ the combine pass when n_splits > 1). dtype: 0 f32, 1 f16,
+// 2 bf16. Returns hipSuccess or the launch error.
+hipError_t launch_kv_attn(int dtype, const KvArgs& a, hipStream_t stream);
+
+// Dense MFMA attention (bf16 / fp16). Strides in ELEMENTS in [B, H, L, D] order.
+struct DenseArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int B, H, Lq, Lk, causal;
+  int64_t qs[3], ks[3], vs[3], os[3];  // b, h, l strides
+  float c;                             // softmax scale * log2(e)
+};
+hipError_t launch_dense_mfma(int dtype, const DenseArgs& a, hipStream_t stream);
+
+}  // namespace wdrz
