@@ -1,0 +1,334 @@
+"""Benchmark of the WhisperDRZ attention hot path on one MI355X.
+
+Headline (the JSON line's ``value``): BASELINE config 2 — encoder self-attention at
+Whisper-large-v3 shape, B=16 x H=20 x L=1500 x D=64, bf16, 32 sequential layers each with its
+own seeded inputs resident in HBM. One "step" = the 32 layers. Reported in TFLOP/s of
+algorithmic work (4*B*H*L^2*D per layer) and as a fraction of the bf16 dense MFMA peak.
+
+The same line carries, under ``decode``, the decoder paths (configs 3, 4, 5) in GB/s of
+algorithmic HBM bytes (only valid K/V rows are counted), each with 32 distinct per-layer caches
+captured into one hipGraph and replayed, and under ``cpu_baseline`` the reference's CPU torch
+path (torch SDPA, fp32) timed on this host's cores on a bounded sample.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only enc|dec]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+METRIC = "enc-attn TFLOP/s + decode-attn HBM GB/s at large-v3 shape, % of MI355X roofline"
+# MI355X published peaks (dense, no sparsity).
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+
+H, D = 20, 64
+E = 2  # bytes per bf16 element
+N_LAYERS = 32
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def timed_events(fn, iters: int, stream: torch.cuda.Stream) -> float:
+    """Milliseconds per call of fn() over `iters` calls, timed with HIP events on `stream`."""
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+# --------------------------------------------------------------------------------------------
+# config 2: encoder self-attention
+# --------------------------------------------------------------------------------------------
+
+
+def bench_encoder(dev, steps: int, warmup: int) -> dict:
+    from whisperdrz_amd import scaled_dot_product_attention
+
+    B, L = 16, 1500
+    flop_layer = 4.0 * B * H * L * L * D
+    log(f"[bench] encoder: generating {N_LAYERS} layers of B={B} H={H} L={L} bf16 inputs")
+    layers = []
+    for i in range(N_LAYERS):
+        g = torch.Generator(device=dev).manual_seed(2000 + i)
+        qkv = torch.randn((3, B, L, H, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        layers.append(tuple(x.permute(0, 2, 1, 3) for x in qkv))  # [B, H, L, D] views of [B, L, H, D]
+    outs = [None] * N_LAYERS
+
+    def step():
+        for i, (q, k, v) in enumerate(layers):
+            outs[i] = scaled_dot_product_attention(q, k, v, scale=0.125)
+
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        step()
+    ms_step = timed_events(step, steps, stream)
+    ms_launch = ms_step / N_LAYERS
+    tflops = flop_layer * N_LAYERS / (ms_step * 1e-3) / 1e12
+    achieved = flop_layer / (ms_launch * 1e-3) / 1e12
+    log(f"[bench] encoder: {ms_step:.3f} ms/step, {tflops:.1f} TFLOP/s ({100 * tflops / PEAK_BF16_TFLOPS:.1f}% of bf16 peak)")
+    del layers, outs
+    torch.cuda.empty_cache()
+    return {
+        "ms_per_step": ms_step,
+        "tflops": tflops,
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(achieved, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+            "kernel": "dense_mfma_kernel<Bf16,false>",
+            "flop_per_launch": flop_layer,
+            "ms_per_launch": ms_launch,
+        },
+    }
+
+
+# --------------------------------------------------------------------------------------------
+# configs 3, 4, 5: decoder cached self-attention, cross-attention, draft verify
+# --------------------------------------------------------------------------------------------
+
+
+def _lengths(seed, n, lo, hi):
+    from oracle.attention_oracle import decode_lengths  # seeded draw only; not timed
+
+    return decode_lengths(seed, n, lo, hi)
+
+
+def _head_major_cache(n_slots, Lmax, dev, seed):
+    """K and V caches stored head-major [n_slots, H, Lmax, D], viewed as [n_slots, Lmax, H, D]."""
+    g = torch.Generator(device=dev).manual_seed(seed)
+    kv = torch.randn((2, n_slots, H, Lmax, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    return kv[0].permute(0, 2, 1, 3), kv[1].permute(0, 2, 1, 3)
+
+
+def bench_decode(dev, steps: int, warmup: int) -> dict:
+    from whisperdrz_amd import flash_attn_with_kvcache, kvcache_workspace_size
+    from whisperdrz_amd.attention import _WORKSPACES
+
+    Bs, Lself, Lcross = 64, 448, 1500
+    res = {}
+    slots = torch.arange(Bs, dtype=torch.int32, device=dev)
+
+    def q_new(seed, sq):
+        g = torch.Generator(device=dev).manual_seed(seed)
+        t = torch.randn((3, Bs, sq, H, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        return t[0], t[1], t[2]
+
+    def run_graph(name, body, bytes_per_layer, extra=None):
+        torch.cuda.synchronize()
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(3):
+                body()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            body()
+        stream = torch.cuda.current_stream()
+        for _ in range(warmup):
+            graph.replay()
+        ms = timed_events(graph.replay, steps, stream)
+        gbs = bytes_per_layer * N_LAYERS / (ms * 1e-3) / 1e9
+        log(f"[bench] {name}: {ms * 1e3 / N_LAYERS:.2f} us/layer, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM)")
+        out = {
+            "us_per_layer": round(ms * 1e3 / N_LAYERS, 3),
+            "GB_per_s": round(gbs, 1),
+            "roofline": {
+                "bound": "hbm",
+                "achieved": round(gbs, 1),
+                "peak": PEAK_HBM_GBS,
+                "unit": "GB/s",
+                "frac": round(gbs / PEAK_HBM_GBS, 4),
+                "traffic": None,
+                "bytes_per_layer": bytes_per_layer,
+            },
+            "graph": f"{N_LAYERS} layers in one hipGraph",
+        }
+        if extra:
+            out.update(extra)
+        del graph
+        return out
+
+    # shared per-layer caches: 32 distinct self caches (capacity 448) and cross caches (1500)
+    log("[bench] decode: generating 32 self caches (64 x 448) and 32 cross caches (64 x 1500), head-major bf16")
+    self_kv = [_head_major_cache(Bs, Lself, dev, 3000 + i) for i in range(N_LAYERS)]
+    cross_kv = [_head_major_cache(Bs, Lcross, dev, 4000 + i) for i in range(N_LAYERS)]
+    for sq in (1, 5):
+        _WORKSPACES.reserve(dev, max(kvcache_workspace_size(Bs, sq, H, D, Lself),
+                                     kvcache_workspace_size(Bs, sq, H, D, Lcross)))
+
+    # ---- config 3: self-attention decode, sq=1, L_i ~ U[1,448] including the new token ----
+    L3 = _lengths(3, Bs, 1, Lself)
+    cs3 = torch.from_numpy((L3 - 1).astype(np.int32)).to(dev)
+    q3 = [q_new(5000 + i, 1) for i in range(N_LAYERS)]
+    o3 = [torch.empty((Bs, 1, H, D), dtype=torch.bfloat16, device=dev) for _ in range(N_LAYERS)]
+
+    def body3():
+        for i in range(N_LAYERS):
+            q, k, v = q3[i]
+            flash_attn_with_kvcache(q, self_kv[i][0], self_kv[i][1], k=k, v=v, cache_seqlens=cs3,
+                                    cache_batch_idx=slots, softmax_scale=0.125, causal=True, out=o3[i])
+
+    sumL3 = int(L3.sum())
+    bytes3 = 2 * H * D * E * sumL3 + 2 * H * D * E * Bs + 2 * H * D * E * Bs + 8 * Bs
+    res["config3_self_decode"] = run_graph("config3 self sq=1", body3, bytes3, {"sum_L": sumL3})
+
+    # ---- config 4: cross-attention decode, sq=1, 1500 keys per stream ----
+    q4 = [q_new(6000 + i, 1)[0] for i in range(N_LAYERS)]
+    o4 = [torch.empty((Bs, 1, H, D), dtype=torch.bfloat16, device=dev) for _ in range(N_LAYERS)]
+
+    def body4():
+        for i in range(N_LAYERS):
+            flash_attn_with_kvcache(q4[i], cross_kv[i][0], cross_kv[i][1], cache_batch_idx=slots,
+                                    softmax_scale=0.125, causal=False, out=o4[i])
+
+    bytes4 = 2 * Bs * Lcross * H * D * E + 2 * H * D * E * Bs + 4 * Bs
+    res["config4_cross_decode"] = run_graph("config4 cross sq=1", body4, bytes4)
+
+    # ---- config 5: 5-token draft verify (self, causal within the draft) + cross ----
+    sq = 5
+    L5 = _lengths(5, Bs, sq, Lself)
+    cs5 = torch.from_numpy((L5 - sq).astype(np.int32)).to(dev)
+    q5 = [q_new(7000 + i, sq) for i in range(N_LAYERS)]
+    qx5 = [q_new(8000 + i, sq)[0] for i in range(N_LAYERS)]
+    o5 = [torch.empty((Bs, sq, H, D), dtype=torch.bfloat16, device=dev) for _ in range(N_LAYERS)]
+    ox5 = [torch.empty((Bs, sq, H, D), dtype=torch.bfloat16, device=dev) for _ in range(N_LAYERS)]
+
+    def body5():
+        for i in range(N_LAYERS):
+            q, k, v = q5[i]
+            flash_attn_with_kvcache(q, self_kv[i][0], self_kv[i][1], k=k, v=v, cache_seqlens=cs5,
+                                    cache_batch_idx=slots, softmax_scale=0.125, causal=True, out=o5[i])
+            flash_attn_with_kvcache(qx5[i], cross_kv[i][0], cross_kv[i][1], cache_batch_idx=slots,
+                                    softmax_scale=0.125, causal=False, out=ox5[i])
+
+    sumL5 = int(L5.sum())
+    bytes5_self = 2 * H * D * E * sumL5 + 4 * H * D * E * Bs * sq + 8 * Bs
+    bytes5_cross = 2 * Bs * Lcross * H * D * E + 2 * H * D * E * Bs * sq + 4 * Bs
+    res["config5_verify_self_plus_cross"] = run_graph(
+        "config5 verify sq=5 (self+cross)", body5, bytes5_self + bytes5_cross,
+        {"sum_L": sumL5, "bytes_self_per_layer": bytes5_self, "bytes_cross_per_layer": bytes5_cross},
+    )
+    del self_kv, cross_kv
+    torch.cuda.empty_cache()
+    return res
+
+
+# --------------------------------------------------------------------------------------------
+# CPU baseline: the reference's CPU torch path (torch SDPA, fp32), bounded sample
+# --------------------------------------------------------------------------------------------
+
+
+def cpu_baseline(budget_s: float = 12.0) -> dict:
+    from oracle.attention_oracle import sdpa_torch
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    B, L = 1, 1500
+    g = torch.Generator().manual_seed(1)
+    q, k, v = (torch.randn((B, H, L, D), generator=g) for _ in range(3))
+    flop = 4.0 * B * H * L * L * D
+    sdpa_torch(q, k, v, scale=0.125)  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 5 or (time.perf_counter() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        sdpa_torch(q, k, v, scale=0.125)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    tflops = flop / med / 1e12
+    log(f"[bench] cpu baseline: torch SDPA fp32 {med * 1e3:.1f} ms per (B=1,H=20,L=1500) layer on {cores} threads -> {tflops:.3f} TFLOP/s")
+    return {
+        "value": round(tflops, 4),
+        "unit": "TFLOP/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"torch CPU F.scaled_dot_product_attention fp32 (the reference's CPU path, model.py:288-296) on "
+        f"one 30-s window layer B=1 H=20 L=1500 D=64, median of {len(times)} runs "
+        f"({med * 1e3:.1f} ms each); config 2 is 16 such windows x 32 layers",
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--only", choices=["enc", "dec"], default=None)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print(
+            "bench.py measures one GPU: the attention hot path shards by independent windows/slots "
+            "with no collective, and this build runs on single-GPU boxes only (use --gpus 1).",
+            file=sys.stderr,
+        )
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU (torch.cuda.is_available() is False)", file=sys.stderr)
+        return 2
+    from whisperdrz_amd import _lib
+
+    _lib.load()  # fail loudly if the HIP library is missing
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+
+    enc = bench_encoder(dev, args.steps, args.warmup) if args.only in (None, "enc") else None
+    dec = bench_decode(dev, args.steps, args.warmup) if args.only in (None, "dec") else None
+    cpu = None if args.no_cpu else cpu_baseline()
+
+    line = {
+        "metric": METRIC,
+        "value": round(enc["tflops"], 2) if enc else None,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(enc["ms_per_step"], 4) if enc else None,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) Q/K/V and K/V caches generated on the GPU)",
+        "config": {
+            "workload": "config2: encoder self-attention B=16 H=20 L=1500 D=64 bf16, non-causal, scale 1/8, "
+            "32 sequential layers with distinct inputs; one step = 32 layers",
+            "batch": 16,
+            "heads": H,
+            "seq_len": 1500,
+            "head_dim": D,
+            "layers_per_step": N_LAYERS,
+            "parallelism": "single GPU",
+        },
+        "roofline": enc["roofline"] if enc else None,
+        "cpu_baseline": cpu,
+        "decode": dec,
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
