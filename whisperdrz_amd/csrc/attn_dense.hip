@@ -2,23 +2,35 @@
 //
 // Replaces F.scaled_dot_product_attention at reference src/whisperdrz/model.py:288-296
 // (encoder self-attention, [B, 20, 1500, 64], non-causal, scale 1/8; and the uncached decoder,
-// top-left causal). O = softmax(c' * Q K^T) V per (b, h), computed with an online softmax in
-// the log2 domain (c = scale * log2 e).
+// top-left causal). O = softmax(scale * Q K^T) V per (b, h), with an online softmax in the
+// log2 domain.
 //
-// Tiling. A workgroup of 4 wavefronts owns 256 query rows of one (b, h); each wavefront owns
-// 64 of them (two 32-row blocks). Key/value tiles of 64 rows are staged through LDS (double
-// buffered, register prefetch of the next tile while the current one is in the MFMAs).
+// Layout of the work. A workgroup of 4 wavefronts owns 256 query rows of one (b, h); each
+// wavefront owns 64 of them (two 32-row blocks). Key/value tiles of 64 rows are staged through
+// LDS (triple buffered: the global loads of tile t+1 are in flight while tile t is computed, and
+// one barrier per tile suffices). Each tile is consumed as two 32-key sub-steps.
 //
-// The wavefront computes S^T = K Q^T with v_mfma_f32_32x32x16 (A = K from LDS, B = Q held in
-// registers for the whole kernel), so every lane owns whole query COLUMNS of S: the row max
-// and row sum of the softmax are in-lane work plus one exchange with lane ^ 32, and the
-// rescale of the output accumulator is per-lane. The output is produced transposed as well,
-// O^T = V^T P^T (A = V^T from LDS, B = P straight from the S accumulators after exp2 and
-// conversion to 16 bits). For P to be usable as the B operand without any shuffle, the K rows
-// feeding S^T are loaded in a permuted order pi(m) chosen so that accumulator a of lane l
-// holds key 16*(a>>3) + 8*(l>>5) + (a&7) of its 32-key block; accumulators 8c..8c+7 of a lane
-// are then exactly the eight consecutive keys that lane must supply for the 16-key chunk c of
-// the PV product, and the matching V^T operand is one 16-byte LDS read.
+// Transposed products. The wavefront computes S^T = K Q^T with v_mfma_f32_32x32x16 (A = K from
+// LDS, B = Q kept in registers), so a lane owns whole query COLUMNS of S: the row max and row
+// sum are in-lane work plus one exchange between the two 32-lane halves, and the output rescale
+// is per lane. The output is produced transposed too, O^T = V^T P^T (A = V^T from LDS, B = P
+// straight from the S accumulators). For P to serve as the B operand without shuffles, the K
+// rows feeding S^T are loaded in a permuted order so that accumulator a of lane l holds key
+// 16*(a>>3) + 8*(l>>5) + (a&7) of its 32-key block: accumulators 8c..8c+7 are then the eight
+// consecutive keys the lane supplies for 16-key chunk c of the PV product, and the matching
+// V^T operand is one 16-byte LDS read. V is transposed into LDS at staging time.
+//
+// VALU diet (the kernel is bounded by VALU issue, not MFMA, at head_dim 64):
+//   * Q is pre-scaled by scale*log2(e) once, and the S accumulation starts from a register
+//     block holding -m (the running max) instead of zero, so exp2 applies directly to the MFMA
+//     output: no per-score multiply/subtract.
+//   * Lazy rescaling: the running max only moves when a score exceeds it by more than 2^kTau
+//     (P values up to 2^8 are exact enough in bf16 and harmless in fp32 sums); in steady state
+//     the output accumulator is never rescaled.
+//   * Row sums use v_dot2_f32_{bf16,f16} on the packed 16-bit P against (1, 1): one
+//     instruction per two scores, summing exactly the P that feeds the MFMA.
+// Software pipelining: sub-step s issues the S_s MFMAs, then the PV_{s-1} MFMAs, then the
+// softmax of S_s, so the VALU softmax runs while the matrix pipe works on PV_{s-1}.
 //
 // Grid. One workgroup per (b, h, 256-query block), flattened and remapped so that the query
 // blocks of one (b, h) land on the same XCD (work-group ids are dealt round-robin over the
@@ -32,10 +44,13 @@ namespace {
 
 constexpr int kWavesD = 4;
 constexpr int kThreadsD = kWavesD * 64;
-constexpr int kBM = 64 * kWavesD;  // query rows per workgroup
-constexpr int kBN = 64;            // key rows per tile
+constexpr int kBM = 64 * kWavesD;     // query rows per workgroup
+constexpr int kBN = 64;               // key rows per LDS tile
+constexpr int kBS = 32;               // key rows per sub-step
 constexpr int kPitch = kHeadDim + 8;  // LDS row pitch in elements (16-byte pad)
+constexpr int kNumBuf = 3;
 constexpr int kNumXcd = 8;
+constexpr float kTau = 8.0f;  // lazy-rescale threshold (log2 units)
 
 template <typename T> struct Mfma;
 template <> struct Mfma<Bf16> {
@@ -44,6 +59,14 @@ template <> struct Mfma<Bf16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return pack_bf16x2(lo, hi); }
+  static __device__ __forceinline__ float widen_lo(uint32_t w) { return bf16_lo(w); }
+  static __device__ __forceinline__ float widen_hi(uint32_t w) { return bf16_hi(w); }
+  // sum of the two packed values, accumulated into acc
+  static __device__ __forceinline__ float dot_ones(uint32_t w, float acc) {
+    typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+    const v2 one = {(__bf16)1.0f, (__bf16)1.0f};
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, w), one, acc, false);
+  }
 };
 template <> struct Mfma<F16> {
   typedef f16x8 op_t;
@@ -51,6 +74,13 @@ template <> struct Mfma<F16> {
     return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
   }
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return pack_f16x2(lo, hi); }
+  static __device__ __forceinline__ float widen_lo(uint32_t w) { return f16_lo(w); }
+  static __device__ __forceinline__ float widen_hi(uint32_t w) { return f16_hi(w); }
+  static __device__ __forceinline__ float dot_ones(uint32_t w, float acc) {
+    typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+    const v2 one = {(_Float16)1.0f, (_Float16)1.0f};
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, w), one, acc, false);
+  }
 };
 
 __device__ __forceinline__ int remap_xcd(int id, int n) {
@@ -59,12 +89,18 @@ __device__ __forceinline__ int remap_xcd(int id, int n) {
   return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
 }
 
+// max of x over the two 32-lane halves of the wavefront (every lane gets the result)
+__device__ __forceinline__ float half_swap_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
 template <typename T, bool CAUSAL>
 __global__ __launch_bounds__(kThreadsD, 2) void dense_mfma_kernel(DenseArgs a) {
   typedef typename Mfma<T>::op_t op_t;
   typedef uint16_t e_t;
-  __shared__ __attribute__((aligned(16))) e_t sK[2][kBN * kPitch];
-  __shared__ __attribute__((aligned(16))) e_t sVt[2][kHeadDim * kPitch];
+  __shared__ __attribute__((aligned(16))) e_t sK[kNumBuf][kBN * kPitch];
+  __shared__ __attribute__((aligned(16))) e_t sVt[kNumBuf][kHeadDim * kPitch];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -73,9 +109,9 @@ __global__ __launch_bounds__(kThreadsD, 2) void dense_mfma_kernel(DenseArgs a) {
   const int l32 = lane & 31;
 
   const int n_qblk = (a.Lq + kBM - 1) / kBM;
-  const int tile = remap_xcd(blockIdx.x, gridDim.x);
-  const int qblk = tile % n_qblk;
-  const int bh = tile / n_qblk;
+  const int tile_id = remap_xcd(blockIdx.x, gridDim.x);
+  const int qblk = tile_id % n_qblk;
+  const int bh = tile_id / n_qblk;
   const int b = bh / a.H, h = bh % a.H;
 
   const e_t* Q = reinterpret_cast<const e_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
@@ -85,21 +121,35 @@ __global__ __launch_bounds__(kThreadsD, 2) void dense_mfma_kernel(DenseArgs a) {
 
   const int q_wg = qblk * kBM;
   const int q_wave = q_wg + wave * 64;
+  const float c = a.c;
 
-  // Q operand (B of S^T = K Q^T): lane holds query q_wave + qb*32 + l32, dims ks*16 + hl*8 + 0..7.
+  // Q operand (B of S^T = K Q^T), pre-scaled by c: lane holds query q_wave + qb*32 + l32,
+  // dims ks*16 + hl*8 + 0..7.
   op_t qreg[2][4];
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const int qi = min(q_wave + qb * 32 + l32, a.Lq - 1);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
-      qreg[qb][ks] = __builtin_bit_cast(op_t, load16(Q + qi * a.qs[2] + ks * 16 + hl * 8));
+    for (int ks = 0; ks < 4; ++ks) {
+      const u32x4 raw = load16(Q + qi * a.qs[2] + ks * 16 + hl * 8);
+      u32x4 sc;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        sc[e] = Mfma<T>::pack(Mfma<T>::widen_lo(raw[e]) * c, Mfma<T>::widen_hi(raw[e]) * c);
+      // Opaque to the optimiser: keeps the scaled Q resident instead of being recomputed
+      // from the raw load in every sub-step.
+      asm volatile("" : "+v"(sc));
+      qreg[qb][ks] = __builtin_bit_cast(op_t, sc);
+    }
   }
 
-  // Keys needed by this workgroup.
+  // Keys needed by the workgroup and by this wavefront.
   int k_lim = a.Lk;
   if (CAUSAL) k_lim = min(a.Lk, q_wg + kBM);
   const int n_tiles = (k_lim + kBN - 1) / kBN;
+  const int n_sub = (k_lim + kBS - 1) / kBS;
+  int n_sub_w = n_sub;  // sub-steps this wavefront computes (causal: fewer for early rows)
+  if (CAUSAL) n_sub_w = min(n_sub, (min(a.Lk, q_wave + 64) + kBS - 1) / kBS);
 
   // Tile loader: thread owns key pair (2*kp, 2*kp+1) and dims d0..d0+7 of each.
   const int kp = tid >> 3;
@@ -127,20 +177,24 @@ __global__ __launch_bounds__(kThreadsD, 2) void dense_mfma_kernel(DenseArgs a) {
     }
   };
 
-  // Permuted key row this lane feeds as the A operand of S^T (see header comment).
+  // Permuted key row this lane feeds as the A operand of S^T.
   const int pm = l32;
   const int pi_row = 16 * ((pm >> 3) >> 1) + 8 * ((pm >> 2) & 1) + 4 * ((pm >> 3) & 1) + (pm & 3);
 
   f32x16 acc_o[2][2];  // [db][qb]: O^T rows d = db*32 + ..., column = query
+  f32x16 cinit[2];     // [qb]: -m_run broadcast, the starting value of each S accumulation
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < 2; ++i) {
+#pragma unroll
+    for (int x = 0; x < 16; ++x) cinit[i][x] = 0.f;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int x = 0; x < 16; ++x) acc_o[i][j][x] = 0.f;
-  float m_run[2] = {kNegBig, kNegBig};
-  float l_run[2] = {0.f, 0.f};
-  const float c = a.c;
+  }
+  float m_run[2] = {0.f, 0.f};  // running max (scaled units); scores are kept relative to it
+  float l_run[2] = {0.f, 0.f};  // partial row sum of this lane's half of the keys
+  op_t pprev[2][2];             // [qb][chunk] P of the previous sub-step
 
   if (n_tiles > 0) {
     gload(0);
@@ -148,101 +202,109 @@ __global__ __launch_bounds__(kThreadsD, 2) void dense_mfma_kernel(DenseArgs a) {
   }
   __syncthreads();
 
-  for (int kt = 0; kt < n_tiles; ++kt) {
-    const int buf = kt & 1;
-    if (kt + 1 < n_tiles) gload(kt + 1);
-    const int k0 = kt * kBN;
-    bool active = true;
-    if (CAUSAL) active = k0 <= q_wave + 63;
-    if (active) {
-      // ---- S^T = K Q^T ----
-      f32x16 s[2][2];  // [kb][qb]
+  for (int s = 0; s <= n_sub; ++s) {
+    const int t = s >> 1;       // tile of this sub-step
+    const int kb = s & 1;       // 32-key half of the tile
+    const int buf = t % kNumBuf;
+    if (kb == 0 && t + 1 < n_tiles) gload(t + 1);
+
+    const bool do_s = s < n_sub_w;
+    const bool do_pv = s >= 1 && s - 1 < n_sub_w;
+    f32x16 sacc[2];
+    if (do_s) {
+      // ---- S^T - m = K (cQ)^T + cinit ----
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+      for (int ks = 0; ks < 4; ++ks) {
+        const op_t ka = __builtin_bit_cast(
+            op_t, *reinterpret_cast<const u32x4*>(&sK[buf][(kb * 32 + pi_row) * kPitch + ks * 16 + hl * 8]));
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-          for (int x = 0; x < 16; ++x) s[kb][qb][x] = 0.f;
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          const op_t ka = __builtin_bit_cast(
-              op_t, *reinterpret_cast<const u32x4*>(&sK[buf][(kb * 32 + pi_row) * kPitch + ks * 16 + hl * 8]));
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) s[kb][qb] = Mfma<T>::run(ka, qreg[qb][ks], s[kb][qb]);
-        }
+          sacc[qb] = Mfma<T>::run(ka, qreg[qb][ks], ks == 0 ? cinit[qb] : sacc[qb]);
       }
-      // ---- mask (tail tile, causal diagonal) ----
-      const bool need_mask = (k0 + kBN > a.Lk) || (CAUSAL && k0 + kBN - 1 > q_wave);
-      if (need_mask) {
+    }
+    if (do_pv) {
+      // ---- O^T += V^T P_{s-1}^T ----
+      const int sp = s - 1;
+      const int bufp = (sp >> 1) % kNumBuf;
+      const int kbp = sp & 1;
 #pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) {
-            const int qi = q_wave + qb * 32 + l32;
-#pragma unroll
-            for (int x = 0; x < 16; ++x) {
-              const int key = k0 + kb * 32 + 16 * (x >> 3) + 8 * hl + (x & 7);
-              bool ok = key < a.Lk;
-              if (CAUSAL) ok = ok && key <= qi;
-              if (!ok) s[kb][qb][x] = -INFINITY;
-            }
-          }
-      }
-      // ---- online softmax per query column ----
-      op_t pop[2][4];  // [qb][chunk]: B operand of O^T = V^T P^T
-#pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        float mx = s[0][qb][0];
-#pragma unroll
-        for (int x = 1; x < 16; ++x) mx = fmaxf(mx, s[0][qb][x]);
-#pragma unroll
-        for (int x = 0; x < 16; ++x) mx = fmaxf(mx, s[1][qb][x]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run[qb], mx);
-        const float alpha = fast_exp2((m_run[qb] - m_new) * c);
-        m_run[qb] = m_new;
-        const float mc = m_new * c;
-        float ps = 0.f;
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-          for (int half = 0; half < 2; ++half) {
-            u32x4 w;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float p0 = fast_exp2(__builtin_fmaf(s[kb][qb][half * 8 + 2 * e], c, -mc));
-              const float p1 = fast_exp2(__builtin_fmaf(s[kb][qb][half * 8 + 2 * e + 1], c, -mc));
-              ps += p0 + p1;
-              w[e] = Mfma<T>::pack(p0, p1);
-            }
-            pop[qb][kb * 2 + half] = __builtin_bit_cast(op_t, w);
-          }
-        }
-        l_run[qb] = __builtin_fmaf(l_run[qb], alpha, ps);
-#pragma unroll
-        for (int db = 0; db < 2; ++db)
-#pragma unroll
-          for (int x = 0; x < 16; ++x) acc_o[db][qb][x] *= alpha;
-      }
-      // ---- O^T += V^T P^T ----
-#pragma unroll
-      for (int kc = 0; kc < 4; ++kc) {
+      for (int ch = 0; ch < 2; ++ch) {
 #pragma unroll
         for (int db = 0; db < 2; ++db) {
           const op_t va = __builtin_bit_cast(
-              op_t, *reinterpret_cast<const u32x4*>(&sVt[buf][(db * 32 + l32) * kPitch + kc * 16 + hl * 8]));
+              op_t, *reinterpret_cast<const u32x4*>(
+                        &sVt[bufp][(db * 32 + l32) * kPitch + kbp * 32 + ch * 16 + hl * 8]));
 #pragma unroll
-          for (int qb = 0; qb < 2; ++qb) acc_o[db][qb] = Mfma<T>::run(va, pop[qb][kc], acc_o[db][qb]);
+          for (int qb = 0; qb < 2; ++qb) acc_o[db][qb] = Mfma<T>::run(va, pprev[qb][ch], acc_o[db][qb]);
         }
       }
     }
-    if (kt + 1 < n_tiles) lstore(buf ^ 1);
-    __syncthreads();
+    if (do_s) {
+      // ---- mask (tail keys, causal diagonal) ----
+      const int k0 = s * kBS;
+      const bool need_mask = (k0 + kBS > a.Lk) || (CAUSAL && k0 + kBS - 1 > q_wave);
+      if (need_mask) {
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+          const int qi = q_wave + qb * 32 + l32;
+#pragma unroll
+          for (int x = 0; x < 16; ++x) {
+            const int key = k0 + 16 * (x >> 3) + 8 * hl + (x & 7);
+            bool ok = key < a.Lk;
+            if (CAUSAL) ok = ok && key <= qi;
+            if (!ok) sacc[qb][x] = -INFINITY;
+          }
+        }
+      }
+      // ---- online softmax per query column ----
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        float mx = fmaxf(sacc[qb][0], sacc[qb][1]);
+#pragma unroll
+        for (int x = 2; x < 16; x += 2) mx = fmaxf(mx, fmaxf(sacc[qb][x], sacc[qb][x + 1]));
+        mx = half_swap_max(mx);
+        // First sub-step: adopt the true max. Later: move the max only when it grew by > kTau.
+        const bool first = s == 0;
+        if (__any(first || mx > kTau)) {
+          const float delta = first ? mx : fmaxf(mx, 0.f);
+          m_run[qb] += delta;
+          if (!first) {
+            const float alpha = fast_exp2(-delta);
+            l_run[qb] *= alpha;
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+              for (int x = 0; x < 16; ++x) acc_o[db][qb][x] *= alpha;
+          }
+#pragma unroll
+          for (int x = 0; x < 16; ++x) {
+            sacc[qb][x] -= delta;
+            cinit[qb][x] = -m_run[qb];
+          }
+        }
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch) {
+          u32x4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float p0 = fast_exp2(sacc[qb][ch * 8 + 2 * e]);
+            const float p1 = fast_exp2(sacc[qb][ch * 8 + 2 * e + 1]);
+            w[e] = Mfma<T>::pack(p0, p1);
+            l_run[qb] = Mfma<T>::dot_ones(w[e], l_run[qb]);
+          }
+          pprev[qb][ch] = __builtin_bit_cast(op_t, w);
+        }
+      }
+    }
+    // Stage the prefetched tile t+1 after the second sub-step of tile t. Its buffer last held
+    // tile t-2, whose final PV ran in sub-step 2t-2, before the previous barrier.
+    if (kb == 1 && t + 1 < n_tiles) {
+      lstore((t + 1) % kNumBuf);
+      __syncthreads();
+    }
   }
 
-  // ---- normalise and store: lane holds query column, 4 consecutive dims per (db, i) ----
+  // ---- normalise and store: lane holds a query column, 4 consecutive dims per (db, i) ----
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
     const float lt = l_run[qb] + __shfl_xor(l_run[qb], 32);
