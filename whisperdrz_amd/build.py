@@ -45,9 +45,9 @@ def build_library(debug: bool = False, verbose: bool = False) -> Path:
     # Packed-fp32 instructions are disabled for all device code (they have returned wrong
     # results on these boxes); the flag is device-only, hipcc's host pass merely warns.
     device_flags = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
-    # Per-file device flags. The dense kernel assumes no NaNs (masking uses -inf): without
-    # this, every fmaxf on an MFMA result pays an extra canonicalising max.
-    per_file = {"attn_dense.hip": ["-fno-honor-nans"]}
+    # Per-file device flags. The kernels assume no NaN inputs (masking uses -inf): without
+    # this, every fmaxf on a computed score pays an extra canonicalising max.
+    per_file = {"attn_dense.hip": ["-fno-honor-nans"], "attn_kvcache.hip": ["-fno-honor-nans"]}
     objs = []
     for src in SOURCES:
         obj = out_dir / (src + ".o")

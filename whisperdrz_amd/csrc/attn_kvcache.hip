@@ -30,7 +30,27 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kMaxSQ = 8;  // query rows per workgroup
-constexpr int kUnroll = 4; // keys per lane group per batch
+constexpr int kUnroll = 4; // keys per lane group per batch (even: P V runs on key pairs)
+constexpr float kTau = 8.0f;  // lazy-rescale threshold (log2 units)
+
+// v_dot2 on packed 16-bit pairs with fp32 accumulation.
+template <typename T> struct Dot2;
+template <> struct Dot2<Bf16> {
+  typedef __bf16 v2 __attribute__((ext_vector_type(2)));
+  static constexpr uint32_t kOnes = 0x3f803f80u;  // (1.0, 1.0)
+  static __device__ __forceinline__ float run(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+  }
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return pack_bf16x2(lo, hi); }
+};
+template <> struct Dot2<F16> {
+  typedef _Float16 v2 __attribute__((ext_vector_type(2)));
+  static constexpr uint32_t kOnes = 0x3c003c00u;  // (1.0, 1.0)
+  static __device__ __forceinline__ float run(uint32_t a, uint32_t b, float c) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(v2, a), __builtin_bit_cast(v2, b), c, false);
+  }
+  static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return pack_f16x2(lo, hi); }
+};
 
 template <typename T, int SQ, bool HAS_NEW>
 __global__ __launch_bounds__(kThreads) void kv_attn_kernel(KvArgs a) {
@@ -72,17 +92,23 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(KvArgs a) {
   const int k_begin = split * a.split_len;
   const int k_end = bad ? k_begin : min(key_lim, k_begin + a.split_len);
 
-  // Queries, pre-scaled into the log2 domain.
+  // Queries. 16-bit types keep the raw packed pairs for v_dot2 (the scale is applied to the
+  // reduced score); fp32 keeps floats pre-scaled into the log2 domain.
+  u32x4 qraw[SQ];
   float qf[SQ][EPL];
 #pragma unroll
   for (int t = 0; t < SQ; ++t) {
     const int tt = t0 + min(t, nq - 1);
-    Slice<T> s;
-    s.from_raw(load16(a.q + b * a.qs[0] + tt * a.qs[1] + h * a.qs[2] + r * 16));
+    qraw[t] = load16(a.q + b * a.qs[0] + tt * a.qs[1] + h * a.qs[2] + r * 16);
+    if constexpr (EB == 4) {
+      Slice<T> sl;
+      sl.from_raw(qraw[t]);
 #pragma unroll
-    for (int e = 0; e < EPL; ++e) qf[t][e] = s.v[e] * a.c;
+      for (int e = 0; e < EPL; ++e) qf[t][e] = sl.v[e] * a.c;
+    }
   }
 
+  // Per query: running max (log2 units), partial row sum and output slice of this lane group.
   float m[SQ], l[SQ], acc[SQ][EPL];
 #pragma unroll
   for (int t = 0; t < SQ; ++t) {
@@ -90,6 +116,14 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(KvArgs a) {
     l[t] = 0.f;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) acc[t][e] = 0.f;
+  }
+  // Last key each query may see inside this split (inclusive).
+  int lim[SQ];
+#pragma unroll
+  for (int t = 0; t < SQ; ++t) {
+    lim[t] = k_end - 1;
+    if (HAS_NEW) lim[t] = min(lim[t], cs + t0 + t);
+    else if (a.causal) lim[t] = min(lim[t], t0 + t);
   }
 
   const int safe_slot = bad ? 0 : slot;
@@ -100,11 +134,9 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(KvArgs a) {
 
   for (int base = k_begin + g; base < k_end; base += G * kUnroll) {
     u32x4 kr[kUnroll], vr[kUnroll];
-    int key[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      key[u] = base + u * G;
-      const int kk = min(key[u], k_end - 1);
+      const int kk = min(base + u * G, k_end - 1);
       const char* kp;
       const char* vp;
       if (HAS_NEW && kk >= cs) {
@@ -117,46 +149,89 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(KvArgs a) {
       kr[u] = load16(kp);
       vr[u] = load16(vp);
     }
-    float s[SQ][kUnroll];
+    // ---- scores (log2 units), masked to -inf outside each query's key range ----
+    float sc[SQ][kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      Slice<T> ks;
-      ks.from_raw(kr[u]);
+      if constexpr (EB == 2) {
 #pragma unroll
-      for (int t = 0; t < SQ; ++t) {
-        float d = 0.f;
+        for (int t = 0; t < SQ; ++t) {
+          float d = 0.f;
 #pragma unroll
-        for (int e = 0; e < EPL; ++e) d = __builtin_fmaf(qf[t][e], ks.v[e], d);
-        d = group_sum<LPK>(d);
-        bool ok = key[u] < k_end;
-        if (HAS_NEW) ok = ok && key[u] <= cs + t0 + t;
-        else if (a.causal) ok = ok && key[u] <= t0 + t;
-        s[t][u] = ok ? d : -INFINITY;
+          for (int i = 0; i < 4; ++i) d = Dot2<T>::run(qraw[t][i], kr[u][i], d);
+          sc[t][u] = group_sum<LPK>(d) * a.c;
+        }
+      } else {
+        Slice<T> ks;
+        ks.from_raw(kr[u]);
+#pragma unroll
+        for (int t = 0; t < SQ; ++t) {
+          float d = 0.f;
+#pragma unroll
+          for (int e = 0; e < EPL; ++e) d = __builtin_fmaf(qf[t][e], ks.v[e], d);
+          sc[t][u] = group_sum<LPK>(d);
+        }
       }
-    }
-    Slice<T> vs[kUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) vs[u].from_raw(vr[u]);
+      for (int t = 0; t < SQ; ++t)
+        if (base + u * G > lim[t]) sc[t][u] = -INFINITY;
+    }
+    // ---- lazy max update: move the reference only when a score exceeds it by > kTau ----
+    float mb[SQ];
+    bool grow = false;
 #pragma unroll
     for (int t = 0; t < SQ; ++t) {
-      float mb = m[t];
+      mb[t] = sc[t][0];
 #pragma unroll
-      for (int u = 0; u < kUnroll; ++u) mb = fmaxf(mb, s[t][u]);
-      const float alpha = fast_exp2(m[t] - mb);
-      m[t] = mb;
-      float p[kUnroll], ps = 0.f;
+      for (int u = 1; u < kUnroll; ++u) mb[t] = fmaxf(mb[t], sc[t][u]);
+      grow = grow || mb[t] > m[t] + kTau;
+    }
+    if (__any(grow)) {
+#pragma unroll
+      for (int t = 0; t < SQ; ++t) {
+        const float mn = mb[t] > m[t] + kTau ? mb[t] : m[t];
+        const float alpha = fast_exp2(m[t] - mn);
+        m[t] = mn;
+        l[t] *= alpha;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[t][e] *= alpha;
+      }
+    }
+    // ---- P V ----
+    if constexpr (EB == 2) {
+      // Keys in pairs: v_perm gathers dim e of both keys into one dword, v_dot2 multiplies it
+      // with the packed pair of probabilities.
+#pragma unroll
+      for (int u = 0; u < kUnroll; u += 2) {
+        u32x4 vlo, vhi;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          vlo[i] = __builtin_amdgcn_perm(vr[u + 1][i], vr[u][i], 0x05040100u);
+          vhi[i] = __builtin_amdgcn_perm(vr[u + 1][i], vr[u][i], 0x07060302u);
+        }
+#pragma unroll
+        for (int t = 0; t < SQ; ++t) {
+          const uint32_t pp = Dot2<T>::pack(fast_exp2(sc[t][u] - m[t]), fast_exp2(sc[t][u + 1] - m[t]));
+          l[t] = Dot2<T>::run(pp, Dot2<T>::kOnes, l[t]);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            acc[t][2 * i] = Dot2<T>::run(pp, vlo[i], acc[t][2 * i]);
+            acc[t][2 * i + 1] = Dot2<T>::run(pp, vhi[i], acc[t][2 * i + 1]);
+          }
+        }
+      }
+    } else {
 #pragma unroll
       for (int u = 0; u < kUnroll; ++u) {
-        p[u] = fast_exp2(s[t][u] - mb);
-        ps += p[u];
-      }
-      l[t] = __builtin_fmaf(l[t], alpha, ps);
+        Slice<T> vs;
+        vs.from_raw(vr[u]);
 #pragma unroll
-      for (int e = 0; e < EPL; ++e) {
-        float o = acc[t][e] * alpha;
+        for (int t = 0; t < SQ; ++t) {
+          const float p = fast_exp2(sc[t][u] - m[t]);
+          l[t] += p;
 #pragma unroll
-        for (int u = 0; u < kUnroll; ++u) o = __builtin_fmaf(p[u], vs[u].v[e], o);
-        acc[t][e] = o;
+          for (int e = 0; e < EPL; ++e) acc[t][e] = __builtin_fmaf(p, vs.v[e], acc[t][e]);
+        }
       }
     }
   }
