@@ -107,8 +107,11 @@ size_t wdrz_attn_kvcache_workspace_size(int64_t B, int64_t sq, int64_t H, int64_
  *   whether k_new is given.
  * Duplicate cache_batch_idx entries with k_new given write the same cache rows from several
  *   batch rows; which write lands is unspecified (as with flash-attn).
- * workspace: device buffer of at least wdrz_attn_kvcache_workspace_size(...) bytes (may be
- *   NULL when that is 0). Concurrent calls must not share a workspace.
+ * workspace: device buffer of at least wdrz_attn_kvcache_workspace_size(...) bytes, 256-byte
+ *   aligned (may be NULL when that is 0). It holds per-row arrival counters and partials and
+ *   must be all-zero when a call starts: zero-fill the buffer once after allocating it; every
+ *   completed call leaves it all-zero again, whatever the shapes of earlier calls. Concurrent
+ *   calls must not share a workspace.
  */
 int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, const void* k_new,
                       const void* v_new, const int32_t* cache_seqlens,

@@ -141,3 +141,35 @@ def test_bad_slot_gives_nan_not_fault(cuda):
     assert torch.isnan(out[1].float()).all()
     snap_k[1, 5] = k[0, 0]
     assert torch.equal(kc, snap_k)
+
+
+def test_workspace_reuse_across_shapes(cuda):
+    """Split-path calls of different shapes share one workspace; each is correct and the
+    workspace is all-zero after every call (its counters start at zero for the next one)."""
+    from whisperdrz_amd import flash_attn_with_kvcache, kvcache_workspace_size
+
+    H, Lmax = 6, 700
+    shapes = [(1, 1), (3, 5), (2, 1), (1, 9), (4, 2), (1, 1)]
+    need = max(kvcache_workspace_size(B, sq, H, D, Lmax) for B, sq in shapes)
+    ws = torch.zeros(need, dtype=torch.uint8, device=cuda)
+    for i, (B, sq) in enumerate(shapes):
+        for self_attn in (True, False):
+            print(f"reuse case {i}: B={B} sq={sq} self={self_attn}", flush=True)
+            rng = np.random.default_rng(i)
+            kc, vc = make_cache(B + 1, Lmax, H, D, torch.bfloat16, cuda, "head_major", 40 + i)
+            kc0, vc0 = to_np(kc), to_np(vc)
+            q = randn((B, sq, H, D), 50 + i, torch.bfloat16).to(cuda)
+            bidx_np = rng.permutation(B + 1)[:B].astype(np.int32)
+            bidx = torch.from_numpy(bidx_np).to(cuda)
+            if self_attn:
+                k = randn((B, sq, H, D), 60 + i, torch.bfloat16).to(cuda)
+                cs = rng.integers(0, Lmax - sq + 1, size=B).astype(np.int32)
+                out = flash_attn_with_kvcache(q, kc, vc, k=k, v=k, cache_seqlens=torch.from_numpy(cs).to(cuda),
+                                              cache_batch_idx=bidx, softmax_scale=0.125, workspace=ws)
+                ref, _, _ = kvcache_ref(to_np(q), kc0, vc0, to_np(k), to_np(k), cs, bidx_np, 0.125)
+            else:
+                out = flash_attn_with_kvcache(q, kc, vc, cache_batch_idx=bidx, softmax_scale=0.125, workspace=ws)
+                ref, _, _ = kvcache_ref(to_np(q), kc0, vc0, None, None, None, bidx_np, 0.125)
+            torch.cuda.synchronize()
+            assert_close(out, ref, torch.bfloat16, f"reuse case {i}")
+            assert int(torch.count_nonzero(ws)) == 0, "workspace not left all-zero"

@@ -72,9 +72,11 @@ def _raise(rc: int, what: str) -> None:
 class WorkspaceCache:
     """Per-(device, stream) split-KV workspace, grown on demand and then reused.
 
-    Calls on one stream are ordered, so they can share a buffer; calls on different streams
-    (e.g. the reference's side ``prefill_stream``) get different buffers. Call
-    :meth:`reserve` before capturing a hipGraph so no allocation happens inside capture.
+    The workspace holds per-row arrival counters that must be zero before a call; every call
+    leaves them zero again, so a buffer is zero-filled once, when it is allocated. Calls on
+    one stream are ordered, so they can share a buffer; calls on different streams (e.g. the
+    reference's side ``prefill_stream``) get different buffers. Call :meth:`reserve` before
+    capturing a hipGraph so no allocation happens inside capture.
     """
 
     def __init__(self) -> None:
@@ -86,7 +88,7 @@ class WorkspaceCache:
         key = (device.index if device.index is not None else torch.cuda.current_device(), _stream_handle())
         buf = self._bufs.get(key)
         if buf is None or buf.numel() < nbytes:
-            buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+            buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
             self._bufs[key] = buf
         return buf
 
@@ -135,6 +137,10 @@ def flash_attn_with_kvcache(
     workspace: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Attention of ``q`` against a slot KV cache (reference ``model.py:20-95``).
+
+    ``out`` and ``workspace`` are keyword-only extensions: a preallocated output, and a
+    caller-owned split-KV workspace (zero-filled before its first use; see
+    :func:`kvcache_workspace_size`). Without ``workspace`` a per-stream cached one is used.
 
     Shapes: ``q`` ``[B, sq, H, D]``; ``k_cache``/``v_cache`` ``[n_slots, Lmax, H, D]`` (any
     strides with a contiguous last dim, e.g. head-major storage viewed as slot-major);

@@ -7,15 +7,17 @@
 //   * cross-attention over the full cache (model.py:64-67), non-causal;
 // and also serves as the fp32 dense SDPA kernel (model.py:288-296, top-left causal flag).
 //
-// Work decomposition. One workgroup (256 lanes) per (batch row b, query block, head h, split).
 // The decode work is a GEMV per (b, h): every key row is touched once, so the kernel is HBM
 // bound and uses no MFMA. A head row of K or V is 64 elements = one 16-byte load per lane
-// across LPK lanes (8 lanes in 16-bit types, 16 in fp32); the workgroup's 256/LPK lane groups
-// each own a strided subset of the split's keys, keep U keys in flight per batch, and run an
-// online softmax in the log2 domain. Group partials are merged with shuffles inside a
-// wavefront and through LDS across the four wavefronts. When several splits share a
-// (b, t, h) row they write (m, l, o) partials to the caller's workspace and a combine pass
-// merges them.
+// across LPK lanes (8 lanes in 16-bit types, 16 in fp32). Lane groups of LPK lanes each own
+// a strided subset of the keys, keep kUnroll keys in flight per batch and run an online
+// softmax in the log2 domain; in 16-bit types q.k and P.V run on v_dot2 (P.V over key pairs).
+//
+// Launch shape: one 4-wavefront workgroup per (batch row, query block of up to 8, head, key
+// split); its wavefront partials merge through LDS. Rows split their keys only when there are
+// too few rows to fill the chip; a row with several splits has each split publish an (m, l, o)
+// partial to the caller's workspace, and the split that arrives last (a per-row atomic
+// counter) merges them, writes the output and resets the counter, all in the same launch.
 //
 // Append: keys at positions >= cache_seqlens[b] are read straight from k_new / v_new, never
 // from the cache, so the in-place write (done by the split whose key range holds the row)
@@ -27,10 +29,11 @@ namespace wdrz {
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
 constexpr int kMaxSQ = 8;  // query rows per workgroup
-constexpr int kUnroll = 4; // keys per lane group per batch (even: P V runs on key pairs)
+constexpr int kWavesPerWg = 4;   // wavefronts per workgroup
+constexpr int kUnroll = 4;       // keys per lane group per batch (even: P V runs on key pairs)
+constexpr int kMinSplitKeys = 128;
+constexpr int kMaxMergeSplits = 32;  // upper bound on splits per row (host plan guarantees it)
 constexpr float kTau = 8.0f;  // lazy-rescale threshold (log2 units)
 
 // v_dot2 on packed 16-bit pairs with fp32 accumulation.
@@ -52,16 +55,24 @@ template <> struct Dot2<F16> {
   static __device__ __forceinline__ uint32_t pack(float lo, float hi) { return pack_f16x2(lo, hi); }
 };
 
+// A quiet NaN built from its bit pattern (this file is compiled with -fno-honor-nans, under
+// which a NaN literal would be undefined); it marks output rows with invalid metadata.
+__device__ __forceinline__ float quiet_nan() { return __uint_as_float(0x7fc00000u); }
+
 template <typename T, int SQ, bool HAS_NEW>
-__global__ __launch_bounds__(kThreads) void kv_attn_kernel(KvArgs a) {
+__global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
+  constexpr int kThreads = kWavesPerWg * 64;
+  constexpr int kWaves = kWavesPerWg;
   constexpr int EB = ElemBytes<T>::value;
   constexpr int EPL = 16 / EB;         // elements per lane per 16-byte load
   constexpr int LPK = kHeadDim / EPL;  // lanes per key row
   constexpr int G = kThreads / LPK;    // key groups per workgroup
+  constexpr int kPart = kHeadDim + 2;  // floats per partial: o[64], m, l
 
   __shared__ float sm_acc[kWaves][SQ][kHeadDim];
   __shared__ float sm_m[kWaves][SQ];
   __shared__ float sm_l[kWaves][SQ];
+  __shared__ int sm_last;
 
   const int tid = threadIdx.x;
   const int g = tid / LPK;
@@ -89,6 +100,9 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(KvArgs a) {
     key_lim = min(a.Lk, t0 + nq);
   else
     key_lim = a.Lk;
+  // Splits that hold keys of this row; the others have nothing to do.
+  const int n_split_b = bad ? 1 : max(1, (key_lim + a.split_len - 1) / a.split_len);
+  if (split >= n_split_b) return;
   const int k_begin = split * a.split_len;
   const int k_end = bad ? k_begin : min(key_lim, k_begin + a.split_len);
 
@@ -285,64 +299,98 @@ __global__ __launch_bounds__(kThreads) void kv_attn_kernel(KvArgs a) {
   }
   __syncthreads();
 
-  for (int idx = tid; idx < nq * kHeadDim; idx += kThreads) {
-    const int t = idx / kHeadDim, d = idx % kHeadDim;
-    float mm = kNegBig;
+  auto store_out = [&](int t, int d, float val) {
+    char* op = a.o + b * a.os[0] + (t0 + t) * a.os[1] + h * a.os[2];
+    if constexpr (EB == 4)
+      reinterpret_cast<float*>(op)[d] = val;
+    else if constexpr (__is_same(T, Bf16))
+      reinterpret_cast<__bf16*>(op)[d] = (__bf16)val;
+    else
+      reinterpret_cast<_Float16*>(op)[d] = (_Float16)val;
+  };
+  // This workgroup's (o, m, l) for query t, dim d, from the per-wavefront LDS partials.
+  auto wg_partial = [&](int t, int d, float& O, float& M, float& L) {
+    M = kNegBig;
 #pragma unroll
-    for (int w = 0; w < kWaves; ++w) mm = fmaxf(mm, sm_m[w][t]);
-    float L = 0.f, O = 0.f;
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][t]);
+    L = 0.f;
+    O = 0.f;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) {
-      const float f = fast_exp2(sm_m[w][t] - mm);
+      const float f = fast_exp2(sm_m[w][t] - M);
       L = __builtin_fmaf(sm_l[w][t], f, L);
       O = __builtin_fmaf(sm_acc[w][t][d], f, O);
     }
-    const int tt = t0 + t;
-    if (a.n_splits == 1) {
-      const float val = bad ? __builtin_nanf("") : O / L;
-      char* op = a.o + b * a.os[0] + tt * a.os[1] + h * a.os[2];
-      if constexpr (EB == 4)
-        reinterpret_cast<float*>(op)[d] = val;
-      else if constexpr (__is_same(T, Bf16))
-        reinterpret_cast<__bf16*>(op)[d] = (__bf16)val;
-      else
-        reinterpret_cast<_Float16*>(op)[d] = (_Float16)val;
-    } else {
-      const int64_t row = ((int64_t)b * a.sq + tt) * a.H + h;
-      float* p = a.ws + (row * a.n_splits + split) * (kHeadDim + 2);
-      p[d] = O;
-      if (d == 0) {
-        p[kHeadDim] = bad ? __builtin_nanf("") : mm;
-        p[kHeadDim + 1] = L;
-      }
+  };
+
+  if (n_split_b == 1) {
+    for (int idx = tid; idx < nq * kHeadDim; idx += kThreads) {
+      const int t = idx / kHeadDim, d = idx % kHeadDim;
+      float O, M, L;
+      wg_partial(t, d, O, M, L);
+      store_out(t, d, bad ? quiet_nan() : O / L);
+    }
+    return;
+  }
+
+  // ---- several splits: publish this split's partial; the last split to arrive merges ----
+  const int64_t unit = ((int64_t)b * a.n_qblocks + t0 / SQ) * a.H + h;
+  float* part = a.ws_part + (unit * a.n_splits) * (SQ * kPart);
+  for (int idx = tid; idx < nq * kHeadDim; idx += kThreads) {
+    const int t = idx / kHeadDim, d = idx % kHeadDim;
+    float O, M, L;
+    wg_partial(t, d, O, M, L);
+    float* pp = part + (split * SQ + t) * kPart;
+    __hip_atomic_store(pp + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (d == 0) {
+      __hip_atomic_store(pp + kHeadDim, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(pp + kHeadDim + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
-}
-
-// Merge the per-split partials of one (b, t, h) row: grid (sq, H, B), 64 lanes (one per d).
-template <typename T>
-__global__ __launch_bounds__(64) void kv_combine_kernel(KvArgs a) {
-  const int d = threadIdx.x;
-  const int t = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const int64_t row = ((int64_t)b * a.sq + t) * a.H + h;
-  const float* p = a.ws + row * a.n_splits * (kHeadDim + 2);
-  float mm = kNegBig;
-  for (int s = 0; s < a.n_splits; ++s) mm = fmaxf(mm, p[s * (kHeadDim + 2) + kHeadDim]);
-  float L = 0.f, O = 0.f;
-  for (int s = 0; s < a.n_splits; ++s) {
-    const float* ps = p + s * (kHeadDim + 2);
-    const float f = fast_exp2(ps[kHeadDim] - mm);
-    L = __builtin_fmaf(ps[kHeadDim + 1], f, L);
-    O = __builtin_fmaf(ps[d], f, O);
+  // Ordering without cache maintenance: the partial was written with agent-scope atomic
+  // stores, which complete at the device coherence point; waiting for them (vmcnt 0) before
+  // the counter update makes it visible to whichever split reads the count last. (A C++
+  // release fence here would write back the whole L2 of this XCD from every split.)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const int prev = __hip_atomic_fetch_add(a.ws_count + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sm_last = prev == n_split_b - 1;
   }
-  const float val = O / L;
-  char* op = a.o + b * a.os[0] + t * a.os[1] + h * a.os[2];
-  if constexpr (ElemBytes<T>::value == 4)
-    reinterpret_cast<float*>(op)[d] = val;
-  else if constexpr (__is_same(T, Bf16))
-    reinterpret_cast<__bf16*>(op)[d] = (__bf16)val;
-  else
-    reinterpret_cast<_Float16*>(op)[d] = (_Float16)val;
+  __syncthreads();
+  if (!sm_last) return;
+  // The merging workgroup reads the partials with agent-scope atomic loads (coherent, issued
+  // only after the counter told it every partial had landed): first every (m, l) pair in
+  // parallel into LDS, then one o value per (split, query, dim).
+  __shared__ float sm_pm[kMaxMergeSplits * SQ], sm_pl[kMaxMergeSplits * SQ];
+  for (int idx = tid; idx < n_split_b * nq; idx += kThreads) {
+    const int sp = idx / nq, t = idx % nq;
+    float* pp = part + (sp * SQ + t) * kPart;
+    sm_pm[sp * SQ + t] = __hip_atomic_load(pp + kHeadDim, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sm_pl[sp * SQ + t] = __hip_atomic_load(pp + kHeadDim + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    pp[kHeadDim] = 0.f;  // consumed: leave the workspace all-zero (see below)
+    pp[kHeadDim + 1] = 0.f;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < nq * kHeadDim; idx += kThreads) {
+    const int t = idx / kHeadDim, d = idx % kHeadDim;
+    float mm = kNegBig;
+    for (int sp = 0; sp < n_split_b; ++sp) mm = fmaxf(mm, sm_pm[sp * SQ + t]);
+    float L = 0.f, O = 0.f;
+    for (int sp = 0; sp < n_split_b; ++sp) {
+      const float f = fast_exp2(sm_pm[sp * SQ + t] - mm);
+      L = __builtin_fmaf(sm_pl[sp * SQ + t], f, L);
+      float* po = part + (sp * SQ + t) * kPart + d;
+      O = __builtin_fmaf(__hip_atomic_load(po, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), f, O);
+      *po = 0.f;
+    }
+    store_out(t, d, O / L);
+  }
+  // Leave the counter at zero too. Every call returns the whole workspace to all-zero, so the
+  // counters of any later call, whatever its shape and therefore its layout, start at zero.
+  if (tid == 0) __hip_atomic_store(a.ws_count + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 template <typename T>
@@ -350,12 +398,12 @@ hipError_t launch_typed(const KvArgs& a, hipStream_t stream) {
   dim3 grid(a.B * a.n_qblocks, a.H, a.n_splits);
   const bool has_new = a.kn != nullptr;
   const int sq_blk = a.n_qblocks > 1 ? kMaxSQ : a.sq;
-#define WDRZ_KV_CASE(SQV)                                                                   \
-  case SQV:                                                                                 \
-    if (has_new)                                                                            \
-      hipLaunchKernelGGL((kv_attn_kernel<T, SQV, true>), grid, dim3(kThreads), 0, stream, a); \
-    else                                                                                    \
-      hipLaunchKernelGGL((kv_attn_kernel<T, SQV, false>), grid, dim3(kThreads), 0, stream, a); \
+#define WDRZ_KV_CASE(SQV)                                                                       \
+  case SQV:                                                                                     \
+    if (has_new)                                                                                \
+      hipLaunchKernelGGL((kv_attn_kernel<T, SQV, true>), grid, dim3(kWavesPerWg * 64), 0, stream, a); \
+    else                                                                                         \
+      hipLaunchKernelGGL((kv_attn_kernel<T, SQV, false>), grid, dim3(kWavesPerWg * 64), 0, stream, a); \
     break;
   switch (sq_blk) {
     WDRZ_KV_CASE(1)
@@ -370,34 +418,37 @@ hipError_t launch_typed(const KvArgs& a, hipStream_t stream) {
       return hipErrorInvalidValue;
   }
 #undef WDRZ_KV_CASE
-  hipError_t err = hipGetLastError();
-  if (err != hipSuccess) return err;
-  if (a.n_splits > 1) {
-    hipLaunchKernelGGL((kv_combine_kernel<T>), dim3(a.sq, a.H, a.B), dim3(64), 0, stream, a);
-    err = hipGetLastError();
-  }
-  return err;
+  return hipGetLastError();
 }
 
 }  // namespace
 
 void kv_split_plan(int64_t units, int64_t Lk, int* n_splits, int* split_len) {
-  // Aim for >= 1024 workgroups (four per CU on 256 CUs) while keeping >= 64 keys per split.
-  const int64_t max_splits = (Lk + 63) / 64;
+  // One workgroup per row walks all its keys when there are enough rows to fill the chip
+  // (splitting costs a partial round trip per split and, measured, never pays off then).
+  // Fewer rows split their keys so that >= 1024 workgroups (four per CU) are in flight.
+  const int64_t max_splits = (Lk + kMinSplitKeys - 1) / kMinSplitKeys;
   int64_t want = (1024 + units - 1) / (units > 0 ? units : 1);
   if (want < 1) want = 1;
   if (want > max_splits) want = max_splits;
+  if (want > kMaxMergeSplits) want = kMaxMergeSplits;
   int64_t len = (Lk + want - 1) / want;
   len = (len + 63) / 64 * 64;
-  if (len < 64) len = 64;
   *split_len = (int)len;
   *n_splits = (int)((Lk + len - 1) / len);
   if (*n_splits < 1) *n_splits = 1;
 }
 
-size_t kv_workspace_bytes(int64_t B, int64_t sq, int64_t H, int n_splits) {
+size_t kv_workspace_bytes(int64_t units, int64_t sq_blk, int n_splits) {
   if (n_splits <= 1) return 0;
-  return (size_t)(B * sq * H) * (size_t)n_splits * (kHeadDim + 2) * sizeof(float);
+  const size_t counters = ((size_t)units * sizeof(int) + 255) / 256 * 256;
+  return counters + (size_t)units * n_splits * sq_blk * (kHeadDim + 2) * sizeof(float);
+}
+
+void kv_workspace_layout(void* ws, int64_t units, KvArgs* a) {
+  const size_t counters = ((size_t)units * sizeof(int) + 255) / 256 * 256;
+  a->ws_count = static_cast<int*>(ws);
+  a->ws_part = reinterpret_cast<float*>(static_cast<char*>(ws) + counters);
 }
 
 hipError_t launch_kv_attn(int dtype, const KvArgs& a, hipStream_t stream) {

@@ -141,9 +141,11 @@ int wdrz_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* 
 size_t wdrz_attn_kvcache_workspace_size(int64_t B, int64_t sq, int64_t H, int64_t D, int64_t Lmax) {
   (void)D;
   if (B <= 0 || sq <= 0 || H <= 0 || Lmax <= 0) return 0;
+  const int64_t n_qblocks = (sq + 7) / 8;
+  const int64_t units = B * n_qblocks * H;
   int n_splits, split_len;
-  wdrz::kv_split_plan(B * H * ((sq + 7) / 8), Lmax, &n_splits, &split_len);
-  return wdrz::kv_workspace_bytes(B, sq, H, n_splits);
+  wdrz::kv_split_plan(units, Lmax, &n_splits, &split_len);
+  return wdrz::kv_workspace_bytes(units, sq < 8 ? sq : 8, n_splits);
 }
 
 int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, const void* k_new, const void* v_new,
@@ -207,13 +209,15 @@ int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, co
       a.vns[j] = vn_strides[j] * eb;
     }
   a.c = softmax_scale * 1.4426950408889634f;
-  wdrz::kv_split_plan(B * H * a.n_qblocks, Lmax, &a.n_splits, &a.split_len);
-  const size_t need = wdrz::kv_workspace_bytes(B, sq, H, a.n_splits);
+  const int64_t units = B * a.n_qblocks * H;
+  wdrz::kv_split_plan(units, Lmax, &a.n_splits, &a.split_len);
+  const size_t need = wdrz::kv_workspace_bytes(units, sq < 8 ? sq : 8, a.n_splits);
   if (need > 0) {
     if (!workspace || workspace_bytes < need)
       return fail(WDRZ_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace ? workspace_bytes : 0);
-    if (!aligned16(workspace)) return fail(WDRZ_EINVAL, "workspace is not 16-byte aligned");
-    a.ws = static_cast<float*>(workspace);
+    if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+      return fail(WDRZ_EINVAL, "workspace is not 256-byte aligned");
+    wdrz::kv_workspace_layout(workspace, units, &a);
   }
   hipError_t err = wdrz::launch_kv_attn(dtype, a, reinterpret_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail(WDRZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));

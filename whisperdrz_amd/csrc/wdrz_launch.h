@@ -20,20 +20,23 @@ struct KvArgs {
   const int32_t* seqlens;  // pre-append lengths (required with k_new)
   const int32_t* bidx;     // batch row -> slot (nullptr: identity)
   char* o;
-  float* ws;  // split partials, nullptr when n_splits == 1
+  float* ws_part;  // split partials (split mode with n_splits > 1)
+  int* ws_count;   // per-row arrival counters, zero between calls
   int B, sq, H, Lk, n_slots, n_qblocks, n_splits, split_len;
   int causal;  // top-left causal mask (dense path only; the append path is always causal)
   int64_t qs[3], kcs[3], vcs[3], kns[3], vns[3], os[3];
   float c;  // softmax scale * log2(e)
 };
 
-// Split count and keys per split for B*H*n_qblocks work units over Lk keys. Depends only on
-// sizes, so the workspace size can be queried without data.
+// Split count and keys per split for `units` = B*n_qblocks*H rows over Lk keys.
+// Depends only on sizes, so the workspace size can be queried without data.
 void kv_split_plan(int64_t units, int64_t Lk, int* n_splits, int* split_len);
-size_t kv_workspace_bytes(int64_t B, int64_t sq, int64_t H, int n_splits);
+// Workspace when n_splits > 1: per-row int32 counters (zero between calls), then partials.
+size_t kv_workspace_bytes(int64_t units, int64_t sq_blk, int n_splits);
+void kv_workspace_layout(void* ws, int64_t units, KvArgs* a);
 
-// Launch the split-KV kernel (+ the combine pass when n_splits > 1). dtype: 0 f32, 1 f16,
-// 2 bf16. Returns hipSuccess or the launch error.
+// Launch the attention kernel: one workgroup per (row, key split); with n_splits > 1 the
+// partials merge in-launch through the workspace. dtype: 0 f32, 1 f16, 2 bf16.
 hipError_t launch_kv_attn(int dtype, const KvArgs& a, hipStream_t stream);
 
 // Dense MFMA attention (bf16 / fp16). Strides in ELEMENTS in [B, H, L, D] order.
