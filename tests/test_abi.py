@@ -1,0 +1,120 @@
+"""The C-ABI library: it loads (no GPU needed), exports every function include/wdrz_attn.h
+declares, and rejects bad arguments on the host with a code and a message before any launch."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "wdrz_attn.h")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from whisperdrz_amd import _lib
+
+    if not _lib.LIB_PATH.exists():
+        from whisperdrz_amd.build import build_library
+
+        build_library()
+    return _lib.load()
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?[\w\*\s]+?\b(wdrz_\w+)\s*\(", text, flags=re.M)))
+
+
+def test_header_declares_the_entry_points():
+    names = declared_functions()
+    for n in ("wdrz_attn_fwd", "wdrz_attn_kvcache", "wdrz_attn_kvcache_workspace_size", "wdrz_last_error",
+              "wdrz_abi_version"):
+        assert n in names
+
+
+def test_library_exports_every_declared_symbol(lib):
+    from whisperdrz_amd import _lib
+
+    for name in declared_functions():
+        assert hasattr(lib, name), f"{name} declared in wdrz_attn.h but not exported"
+    assert set(declared_functions()) == set(_lib.EXPORTED_SYMBOLS)
+
+
+def test_abi_version(lib):
+    from whisperdrz_amd import _lib
+
+    assert lib.wdrz_abi_version() == _lib.ABI_VERSION
+
+
+def test_workspace_size_plan(lib):
+    # many rows: one workgroup per row, no workspace; few rows: split keys, workspace needed
+    assert lib.wdrz_attn_kvcache_workspace_size(64, 1, 20, 64, 448) == 0
+    assert lib.wdrz_attn_kvcache_workspace_size(64, 1, 20, 64, 1500) == 0
+    small = lib.wdrz_attn_kvcache_workspace_size(1, 1, 20, 64, 1500)
+    assert small > 0 and small % 4 == 0
+    assert lib.wdrz_attn_kvcache_workspace_size(1, 5, 20, 64, 1500) > small
+    assert lib.wdrz_attn_kvcache_workspace_size(0, 1, 20, 64, 448) == 0
+
+
+def _strides(*s):
+    return (ctypes.c_int64 * 4)(*s)
+
+
+FAKE = 0x10000  # 16-byte-aligned non-null pointer value; validation fails before any use
+
+
+def call_fwd(lib, **over):
+    args = dict(dtype=2, q=FAKE, k=FAKE, v=FAKE, o=FAKE, B=1, H=2, Lq=8, Lk=8, D=64,
+                qs=_strides(1024, 512, 64, 1), ks=_strides(1024, 512, 64, 1), vs=_strides(1024, 512, 64, 1),
+                os_=_strides(1024, 512, 64, 1), scale=0.125, causal=0)
+    args.update(over)
+    return lib.wdrz_attn_fwd(args["dtype"], args["q"], args["k"], args["v"], args["o"], args["B"], args["H"],
+                             args["Lq"], args["Lk"], args["D"], args["qs"], args["ks"], args["vs"], args["os_"],
+                             args["scale"], args["causal"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(dtype=7), 1, "dtype"),
+    (dict(D=32), 2, "head_dim"),
+    (dict(q=None), 1, "q is NULL"),
+    (dict(k=FAKE + 2), 1, "not 16-byte aligned"),
+    (dict(Lk=0), 1, "bad sizes"),
+    (dict(scale=-1.0), 1, "scale"),
+    (dict(qs=_strides(1024, 512, 64, 2)), 1, "head_dim stride"),
+    (dict(vs=_strides(1024, 512, 60, 1)), 1, "not 16-byte aligned"),
+])
+def test_fwd_rejects_bad_arguments(lib, over, code, msg):
+    assert call_fwd(lib, **over) == code
+    assert msg in lib.wdrz_last_error().decode()
+
+
+def test_fwd_empty_batch_is_a_no_op(lib):
+    assert call_fwd(lib, B=0) == 0
+    assert lib.wdrz_last_error().decode() == ""
+
+
+def call_kv(lib, **over):
+    s = _strides(1024, 1024, 64, 1)
+    args = dict(dtype=2, q=FAKE, kc=FAKE, vc=FAKE, kn=None, vn=None, seqlens=None, bidx=None, o=FAKE, B=2, sq=1,
+                H=2, D=64, n_slots=4, Lmax=16, ws=None, ws_bytes=0, scale=0.125)
+    args.update(over)
+    return lib.wdrz_attn_kvcache(args["dtype"], args["q"], args["kc"], args["vc"], args["kn"], args["vn"],
+                                 args["seqlens"], args["bidx"], args["o"], args["B"], args["sq"], args["H"], args["D"],
+                                 args["n_slots"], args["Lmax"], s, s, s, s, s, s, args["scale"], 1, args["ws"],
+                                 args["ws_bytes"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(kn=FAKE), 1, "k and v must be given together"),
+    (dict(kn=FAKE, vn=FAKE), 1, "cache_seqlens is required"),
+    (dict(kn=FAKE, vn=FAKE, seqlens=FAKE, sq=40), 1, "exceeds cache length"),
+    (dict(D=128), 2, "head_dim"),
+    (dict(kc=None), 1, "k_cache is NULL"),
+    (dict(B=1, Lmax=1500), 4, "workspace"),
+    (dict(scale=float("nan")), 1, "softmax_scale"),
+])
+def test_kvcache_rejects_bad_arguments(lib, over, code, msg):
+    assert call_kv(lib, **over) == code
+    assert msg in lib.wdrz_last_error().decode()
