@@ -41,6 +41,20 @@ def log(msg: str) -> None:
     print(msg, file=sys.stderr, flush=True)
 
 
+_TRAFFIC_FILE = os.path.join(ROOT, "profiles", "pmc_traffic.json")
+
+
+def measured_traffic(kernel: str):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE passes
+    (profiles/pmc_traffic.json; calibrated against a copy of known size), or None."""
+    try:
+        with open(_TRAFFIC_FILE) as f:
+            k = json.load(f)["kernels"].get(kernel)
+    except (OSError, ValueError, KeyError):
+        return None
+    return None if k is None else int(k["traffic_bytes"])
+
+
 def timed_events(fn, iters: int, stream: torch.cuda.Stream) -> float:
     """Milliseconds per call of fn() over `iters` calls, timed with HIP events on `stream`."""
     start = torch.cuda.Event(enable_timing=True)
@@ -95,8 +109,9 @@ def bench_encoder(dev, steps: int, warmup: int) -> dict:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
-            "kernel": "dense_mfma_kernel<Bf16,false>",
+            "traffic": measured_traffic("dense_mfma_kernel<wdrz::Bf16, false, 1, 8>"),
+            "traffic_source": "profiles/pmc_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE passes)",
+            "kernel": "dense_mfma_kernel<Bf16,false,1,8>",
             "flop_per_launch": flop_layer,
             "ms_per_launch": ms_launch,
         },
@@ -134,7 +149,7 @@ def bench_decode(dev, steps: int, warmup: int) -> dict:
         t = torch.randn((3, Bs, sq, H, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
         return t[0], t[1], t[2]
 
-    def run_graph(name, body, bytes_per_layer, extra=None):
+    def run_graph(name, body, bytes_per_layer, extra=None, kernels=()):
         torch.cuda.synchronize()
         s = torch.cuda.Stream()
         s.wait_stream(torch.cuda.current_stream())
@@ -161,7 +176,8 @@ def bench_decode(dev, steps: int, warmup: int) -> dict:
                 "peak": PEAK_HBM_GBS,
                 "unit": "GB/s",
                 "frac": round(gbs / PEAK_HBM_GBS, 4),
-                "traffic": None,
+                "traffic": (sum(measured_traffic(k) or 0 for k in kernels) or None) if kernels else None,
+                "traffic_source": "profiles/pmc_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE passes)",
                 "bytes_per_layer": bytes_per_layer,
             },
             "graph": f"{N_LAYERS} layers in one hipGraph",
@@ -193,7 +209,8 @@ def bench_decode(dev, steps: int, warmup: int) -> dict:
 
     sumL3 = int(L3.sum())
     bytes3 = 2 * H * D * E * sumL3 + 2 * H * D * E * Bs + 2 * H * D * E * Bs + 8 * Bs
-    res["config3_self_decode"] = run_graph("config3 self sq=1", body3, bytes3, {"sum_L": sumL3})
+    res["config3_self_decode"] = run_graph("config3 self sq=1", body3, bytes3, {"sum_L": sumL3},
+                                           kernels=("kv_attn_kernel<wdrz::Bf16, 1, true>",))
 
     # ---- config 4: cross-attention decode, sq=1, 1500 keys per stream ----
     q4 = [q_new(6000 + i, 1)[0] for i in range(N_LAYERS)]
@@ -205,7 +222,8 @@ def bench_decode(dev, steps: int, warmup: int) -> dict:
                                     softmax_scale=0.125, causal=False, out=o4[i])
 
     bytes4 = 2 * Bs * Lcross * H * D * E + 2 * H * D * E * Bs + 4 * Bs
-    res["config4_cross_decode"] = run_graph("config4 cross sq=1", body4, bytes4)
+    res["config4_cross_decode"] = run_graph("config4 cross sq=1", body4, bytes4,
+                                            kernels=("kv_attn_kernel<wdrz::Bf16, 1, false>",))
 
     # ---- config 5: 5-token draft verify (self, causal within the draft) + cross ----
     sq = 5
@@ -230,6 +248,7 @@ def bench_decode(dev, steps: int, warmup: int) -> dict:
     res["config5_verify_self_plus_cross"] = run_graph(
         "config5 verify sq=5 (self+cross)", body5, bytes5_self + bytes5_cross,
         {"sum_L": sumL5, "bytes_self_per_layer": bytes5_self, "bytes_cross_per_layer": bytes5_cross},
+        kernels=("kv_attn_kernel<wdrz::Bf16, 5, true>", "kv_attn_kernel<wdrz::Bf16, 5, false>"),
     )
     del self_kv, cross_kv
     torch.cuda.empty_cache()
@@ -271,6 +290,48 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
     }
 
 
+def pmc_sample(dev) -> None:
+    """A short, fixed kernel sequence for hardware-counter passes (rocprofv3 --pmc):
+    a calibration copy of 1 GiB (known HBM bytes), then 3 launches of the encoder kernel and of
+    each decode kernel at the bench shapes (eager, distinct per-launch inputs)."""
+    from whisperdrz_amd import flash_attn_with_kvcache, scaled_dot_product_attention
+
+    n = 1 << 30
+    src = torch.empty(n // 2, dtype=torch.bfloat16, device=dev).normal_()
+    dst = torch.empty_like(src)
+    dst.copy_(src)  # calibration: reads 1 GiB, writes 1 GiB
+    torch.cuda.synchronize()
+    del src, dst
+    B, L = 16, 1500
+    for i in range(3):
+        g = torch.Generator(device=dev).manual_seed(100 + i)
+        qkv = torch.randn((3, B, L, H, D), generator=g, device=dev).to(torch.bfloat16)
+        scaled_dot_product_attention(*(x.permute(0, 2, 1, 3) for x in qkv), scale=0.125)
+        torch.cuda.synchronize()
+    del qkv
+    Bs = 64
+    slots = torch.arange(Bs, dtype=torch.int32, device=dev)
+    L3 = _lengths(3, Bs, 1, 448)
+    L5 = _lengths(5, Bs, 5, 448)
+    for i in range(3):
+        kv_s = _head_major_cache(Bs, 448, dev, 3000 + i)
+        kv_x = _head_major_cache(Bs, 1500, dev, 4000 + i)
+        g = torch.Generator(device=dev).manual_seed(200 + i)
+        q1, k1, v1, q5, k5, v5 = (torch.randn((Bs, s, H, D), generator=g, device=dev).to(torch.bfloat16)
+                                  for s in (1, 1, 1, 5, 5, 5))
+        cs3 = torch.from_numpy((L3 - 1).astype(np.int32)).to(dev)
+        cs5 = torch.from_numpy((L5 - 5).astype(np.int32)).to(dev)
+        flash_attn_with_kvcache(q1, kv_s[0], kv_s[1], k=k1, v=v1, cache_seqlens=cs3, cache_batch_idx=slots,
+                                softmax_scale=0.125)
+        flash_attn_with_kvcache(q1, kv_x[0], kv_x[1], cache_batch_idx=slots, softmax_scale=0.125)
+        flash_attn_with_kvcache(q5, kv_s[0], kv_s[1], k=k5, v=v5, cache_seqlens=cs5, cache_batch_idx=slots,
+                                softmax_scale=0.125)
+        flash_attn_with_kvcache(q5, kv_x[0], kv_x[1], cache_batch_idx=slots, softmax_scale=0.125)
+        torch.cuda.synchronize()
+        del kv_s, kv_x
+    log("[bench] pmc sample done")
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -278,6 +339,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--only", choices=["enc", "dec"], default=None)
+    ap.add_argument("--pmc-sample", action="store_true",
+                    help="run the short fixed kernel sequence used for rocprofv3 --pmc passes and exit")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
@@ -294,6 +357,9 @@ def main() -> int:
     _lib.load()  # fail loudly if the HIP library is missing
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.pmc_sample:
+        pmc_sample(dev)
+        return 0
 
     enc = bench_encoder(dev, args.steps, args.warmup) if args.only in (None, "enc") else None
     dec = bench_decode(dev, args.steps, args.warmup) if args.only in (None, "dec") else None
