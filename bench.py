@@ -109,9 +109,9 @@ def bench_encoder(dev, steps: int, warmup: int) -> dict:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": measured_traffic("dense_mfma_kernel<wdrz::Bf16, false, 1, 8>"),
+            "traffic": measured_traffic("dense_fwd_kernel<wdrz::Bf16>"),
             "traffic_source": "profiles/pmc_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE passes)",
-            "kernel": "dense_mfma_kernel<Bf16,false,1,8>",
+            "kernel": "dense_fwd_kernel<Bf16>",
             "flop_per_launch": flop_layer,
             "ms_per_launch": ms_launch,
         },

@@ -5,38 +5,38 @@
 // top-left causal). O = softmax(scale * Q K^T) V per (b, h), with an online softmax in the
 // log2 domain.
 //
-// Layout of the work. A workgroup of 8 wavefronts owns 256 query rows of one (b, h); each
-// wavefront owns 32 of them, which keeps it at ~120 VGPRs so four wavefronts share a SIMD and
-// hide each other's MFMA, LDS and exp latencies. Key/value tiles of 64 rows are staged through
-// LDS (three buffers: the global loads of tile t+1 are in flight while tile t is computed, one
-// barrier per tile). Each tile is consumed as two 32-key sub-steps.
+// Two kernels share the arithmetic below:
+//   * dense_fwd_kernel (non-causal; the encoder): 512-thread workgroups of eight 64-query
+//     wavefronts (two per SIMD), K/V tiles of 64 keys in four LDS buffers, Q and O moved
+//     through LDS as whole rows. Its own comment block gives the details.
+//   * dense_mfma_kernel (causal): eight 32-query wavefronts per workgroup (~120 VGPRs, four
+//     wavefronts per SIMD), three LDS buffers with V transposed at staging time, and the
+//     causal diagonal handled per wavefront (keys past a wavefront's last query are skipped).
+// Each 64-key tile is consumed as two 32-key sub-steps.
 //
-// Transposed products. The wavefront computes S^T = K Q^T with v_mfma_f32_32x32x16 (A = K from
+// Transposed products. A wavefront computes S^T = K Q^T with v_mfma_f32_32x32x16 (A = K from
 // LDS, B = Q kept in registers), so a lane owns whole query COLUMNS of S: the row max and row
 // sum are in-lane work plus one exchange between the two 32-lane halves, and the output rescale
 // is per lane. The output is produced transposed too, O^T = V^T P^T (A = V^T from LDS, B = P
 // straight from the S accumulators). For P to serve as the B operand without shuffles, the K
 // rows feeding S^T are loaded in a permuted order so that accumulator a of lane l holds key
 // 16*(a>>3) + 8*(l>>5) + (a&7) of its 32-key block: accumulators 8c..8c+7 are then the eight
-// consecutive keys the lane supplies for 16-key chunk c of the PV product, and the matching
-// V^T operand is one 16-byte LDS read. V is transposed into LDS at staging time.
+// consecutive keys the lane supplies for 16-key chunk c of the PV product.
 //
-// VALU diet (at head_dim 64 the softmax VALU work rivals the MFMA work):
-//   * Q is pre-scaled by scale*log2(e) once, so a score costs one subtract before exp2;
-//     fmax runs without NaN canonicalisation (the file is built with -fno-honor-nans; masked
-//     scores are -inf, never NaN).
+// VALU diet (at head_dim 64 the softmax VALU work rivals the MFMA work, and on gfx950 the two
+// largely serialise):
+//   * Q is pre-scaled by scale*log2(e) once; fmax runs without NaN canonicalisation (the file
+//     is built with -fno-honor-nans; masked scores are -inf, never NaN).
 //   * Lazy rescaling: the running max only moves when a score exceeds it by more than 2^kTau
 //     (P values up to 2^8 are exact enough in bf16 and harmless in fp32 sums); in steady state
 //     the output accumulator is never rescaled.
 //   * Row sums use v_dot2_f32_{bf16,f16} on the packed 16-bit P against (1, 1): one
 //     instruction per two scores, summing exactly the P that feeds the MFMA, into four
-//     independent partial sums (no serial dependency chain).
-// Within a sub-step the wavefront issues the S_s MFMAs, then the PV_{s-1} MFMAs, then the
-// softmax of S_s, so its VALU work can run while the matrix pipe drains PV_{s-1}.
+//     independent partial sums.
 //
-// Grid. One workgroup per (b, h, 256-query block), flattened and remapped so that the query
-// blocks of one (b, h) land on the same XCD (work-group ids are dealt round-robin over the
-// 8 XCDs): they then share K/V through that XCD's L2.
+// Grid. One workgroup per (b, h, query block), flattened and remapped so that the query blocks
+// of one (b, h) land on the same XCD (work-group ids are dealt round-robin over the 8 XCDs):
+// they then share K/V through that XCD's L2.
 #include "wdrz_common.h"
 #include "wdrz_launch.h"
 
@@ -102,6 +102,15 @@ __device__ __forceinline__ float half_swap_max(float x) {
 __device__ __forceinline__ int vt_index(int d, int key) {
   const int f = ((d >> 1) ^ (d >> 4)) & 7;
   return d * kBN + ((((key >> 3) ^ f) & 7) << 3) + (key & 7);
+}
+
+// Wave issue priority around MFMA sections: while this wavefront feeds the matrix core, the
+// SIMD's arbiter prefers it over wavefronts running softmax VALU work, so the matrix pipe is
+// not left idle between MFMAs (measured on gfx950 with two wavefronts per SIMD: +15% for the
+// encoder shape).
+template <int P>
+__device__ __forceinline__ void mfma_priority() {
+  __builtin_amdgcn_s_setprio(P);
 }
 
 // QB: 32-query blocks per wavefront; NW: wavefronts per workgroup.
@@ -235,6 +244,7 @@ __global__ __launch_bounds__(NW * 64) void dense_mfma_kernel(DenseArgs a) {
     const bool do_s = s < n_sub_w;
     const bool do_pv = s >= 1 && s - 1 < n_sub_w;
     f32x16 sacc[QB];
+    mfma_priority<1>();
     if (do_s) {
       // ---- S^T = K (cQ)^T ----
 #pragma unroll
@@ -261,6 +271,7 @@ __global__ __launch_bounds__(NW * 64) void dense_mfma_kernel(DenseArgs a) {
         }
       }
     }
+    mfma_priority<0>();
     if (do_s) {
       // ---- mask (tail keys, causal diagonal) ----
       const int k0 = s * kBS;
@@ -360,18 +371,312 @@ __global__ __launch_bounds__(NW * 64) void dense_mfma_kernel(DenseArgs a) {
   }
 }
 
-// Workgroup shape: query blocks per wavefront and wavefronts per workgroup.
-#ifndef WDRZ_DENSE_QB
-#define WDRZ_DENSE_QB 1
+// Transposing LDS read (gfx950 ds_read_b64_tr_b16). Within each 16-lane group, lane i gets
+// element (i % 4) of the 8-byte chunks read by lanes 4c + i/4 (c = 0..3) of its group: with
+// every lane pointing at 4 consecutive dims of one key row, this turns a row-major
+// [key][dim] tile into the dim-major operand an MFMA A-input needs.
+// `p` must point into __shared__ memory: its low 32 bits are then the LDS byte offset.
+__device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
+#if __HIP_DEVICE_COMPILE__
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uint32_t)(uintptr_t)p);
+  return __builtin_bit_cast(u32x2, v);
+#else
+  (void)p;
+  return u32x2{0, 0};
 #endif
-#ifndef WDRZ_DENSE_NW
-#define WDRZ_DENSE_NW 8
-#endif
-constexpr int kQB = WDRZ_DENSE_QB;
-constexpr int kNW = WDRZ_DENSE_NW;
+}
+
+// ============================================================================================
+// Non-causal kernel (the encoder shape): 512-thread workgroups, eight wavefronts of 64 queries
+// each (two per SIMD), one workgroup per (b, h, 512-query block).
+//
+// Per step s a wavefront issues PV(s-1) and S(s) (16 MFMAs at raised wave priority), reads the
+// next step's K and V^T operands from LDS, then runs the softmax of S(s). On gfx950 the softmax
+// VALU work and the MFMAs of the wavefronts sharing a SIMD largely serialise, so the step time
+// is their sum: the VALU side is cut to 32 exp2, 16 packs, 16 dot2 row sums and the max check
+// per step, and the subtraction of the running max is folded into the S accumulation, which
+// starts from -m_run (cinit) instead of zero.
+//
+// K/V tiles of 64 keys are staged through registers into four LDS buffers (tile t+2 loaded
+// while tile t is consumed), with one workgroup barrier per tile; the wavefronts otherwise run
+// free. Q and O move through LDS at the start and end, so that global memory sees whole
+// 128-byte head rows (the operand layouts would otherwise scatter 16- and 8-byte pieces over
+// 32 rows per instruction, which measured ~2.7 TB/s for these transfers).
+// ============================================================================================
+constexpr int kFWaves = 8;
+constexpr int kFThreads = kFWaves * 64;
+constexpr int kFBM = 64 * kFWaves;  // queries per workgroup
+constexpr int kFBuf = 4;            // LDS tile buffers
+// The Q and O staging areas ([512 rows][kPitchK]) alias the tile buffers.
+static_assert(kFBM * kPitchK <= 2 * kFBuf * kBN * kPitchK, "Q/O staging must fit the tile buffers");
+
+template <typename T>
+__global__ __launch_bounds__(kFThreads, 1) void dense_fwd_kernel(DenseArgs a) {
+  typedef typename Mfma<T>::op_t op_t;
+  typedef uint16_t e_t;
+  // K tiles then V tiles, each row-major [key][dim] with a 16-byte pad per row; at the start
+  // and end the same memory holds Q and O as [query][dim] rows.
+  __shared__ __attribute__((aligned(16))) e_t smem[2 * kFBuf * kBN * kPitchK];
+  e_t* const sK = smem;
+  e_t* const sV = smem + kFBuf * kBN * kPitchK;
+  constexpr int kTileElems = kBN * kPitchK;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int hl = lane >> 5;
+  const int l32 = lane & 31;
+
+  const int n_qblk = (a.Lq + kFBM - 1) / kFBM;
+  const int tile_id = remap_xcd(blockIdx.x, gridDim.x);
+  const int qblk = tile_id % n_qblk;
+  const int bh = tile_id / n_qblk;
+  const int b = bh / a.H, h = bh % a.H;
+
+  const e_t* Q = reinterpret_cast<const e_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
+  const e_t* K = reinterpret_cast<const e_t*>(a.k) + b * a.ks[0] + h * a.ks[1];
+  const e_t* V = reinterpret_cast<const e_t*>(a.v) + b * a.vs[0] + h * a.vs[1];
+  e_t* O = reinterpret_cast<e_t*>(a.o) + b * a.os[0] + h * a.os[1];
+  const int q_blk0 = qblk * kFBM;
+  const int q_wave = q_blk0 + wave * 64;
+  const float c = a.c;
+
+  // Row-contiguous transfers: thread tid moves 16-byte chunk (tid & 7) of rows tid/8 + 64*i.
+  const int crow = tid >> 3, cd0 = (tid & 7) * 8;
+
+  // Tile staging: one 16-byte piece of K and one of V per thread and tile.
+  const e_t* kg = K + (int64_t)crow * a.ks[2] + cd0;
+  const e_t* vg = V + (int64_t)crow * a.vs[2] + cd0;
+  const e_t* kg_last = K + (int64_t)(a.Lk - 1) * a.ks[2] + cd0;
+  const e_t* vg_last = V + (int64_t)(a.Lk - 1) * a.vs[2] + cd0;
+  const int64_t k_tile = (int64_t)kBN * a.ks[2], v_tile = (int64_t)kBN * a.vs[2];
+  u32x4 pk, pv;
+  auto gload = [&](int kt) __attribute__((always_inline)) {
+    const bool in = kt * kBN + crow < a.Lk;
+    pk = load16(in ? kg + kt * k_tile : kg_last);
+    pv = load16(in ? vg + kt * v_tile : vg_last);
+  };
+  const int st_off = crow * kPitchK + cd0;
+  auto lstore = [&](int buf) __attribute__((always_inline)) {
+    *reinterpret_cast<u32x4*>(&sK[buf * kTileElems + st_off]) = pk;
+    *reinterpret_cast<u32x4*>(&sV[buf * kTileElems + st_off]) = pv;
+  };
+
+  const int n_tiles = (a.Lk + kBN - 1) / kBN;
+  const int n_sub = (a.Lk + kBS - 1) / kBS;
+
+  // ---- Q: whole rows from global memory into LDS, then each wavefront's operand registers,
+  // pre-scaled by c (kept opaque so the scaled values stay resident) ----
+  op_t qreg[2][4];
+  {
+    u32x4 qc[kFBM / 64];
+#pragma unroll
+    for (int i = 0; i < kFBM / 64; ++i) qc[i] = load16(Q + min(q_blk0 + crow + 64 * i, a.Lq - 1) * a.qs[2] + cd0);
+    gload(0);
+#pragma unroll
+    for (int i = 0; i < kFBM / 64; ++i) *reinterpret_cast<u32x4*>(&smem[(crow + 64 * i) * kPitchK + cd0]) = qc[i];
+    __syncthreads();
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const u32x4 raw =
+            *reinterpret_cast<const u32x4*>(&smem[(wave * 64 + qb * 32 + l32) * kPitchK + ks * 16 + hl * 8]);
+        u32x4 sc;
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          sc[e] = Mfma<T>::pack(Mfma<T>::widen_lo(raw[e]) * c, Mfma<T>::widen_hi(raw[e]) * c);
+        asm volatile("" : "+v"(sc));
+        qreg[qb][ks] = __builtin_bit_cast(op_t, sc);
+      }
+    __syncthreads();
+  }
+
+  // Per-lane LDS offsets. K operand: permuted key row (see the header comment), dims
+  // ks*16 + hl*8. V^T operand through the transposing read: this lane points at key row
+  // 8*(g>>1) + (j>>2) (+4 for the second half) and dims 16*(g&1) + 4*(j&3) of a 32-dim block,
+  // where g is its 16-lane group and j its index in the group.
+  const int pm = l32;
+  const int pi_row = 16 * ((pm >> 3) >> 1) + 8 * ((pm >> 2) & 1) + 4 * ((pm >> 3) & 1) + (pm & 3);
+  const int k_off = pi_row * kPitchK + hl * 8;
+  const int g16 = lane >> 4, j16 = lane & 15;
+  const int v_off = (8 * (g16 >> 1) + (j16 >> 2)) * kPitchK + 16 * (g16 & 1) + 4 * (j16 & 3);
+
+  op_t kop[4], vop[2][2];  // operands of the next MFMA step: kop[ks], vop[ch][db]
+  auto read_k = [&](int s) __attribute__((always_inline)) {
+    const e_t* kb = &sK[((s >> 1) % kFBuf) * kTileElems + (s & 1) * 32 * kPitchK + k_off];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) kop[ks] = __builtin_bit_cast(op_t, *reinterpret_cast<const u32x4*>(kb + ks * 16));
+  };
+  auto read_v = [&](int s) __attribute__((always_inline)) {
+    const e_t* vb = &sV[((s >> 1) % kFBuf) * kTileElems + (s & 1) * 32 * kPitchK + v_off];
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        const e_t* p = vb + ch * 16 * kPitchK + db * 32;
+        const u32x2 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 4 * kPitchK);
+        vop[ch][db] = __builtin_bit_cast(op_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
+      }
+  };
+
+  f32x16 acc_o[2][2];  // [db][qb]: O^T rows d = db*32 + ..., column = query
+  f32x16 sacc[2];      // [qb] scores of the current step, relative to m_run
+  f32x16 cinit[2];     // [qb] -m_run: the starting value of every S accumulation
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      cinit[i][x] = 0.f;
+      acc_o[0][i][x] = 0.f;
+      acc_o[1][i][x] = 0.f;
+    }
+  float m_run[2] = {0.f, 0.f};
+  float l_part[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // 4 partial row sums
+  op_t pcur[2][2];  // [qb][16-key chunk] P of the last softmax
+
+  // Online softmax of step s on sacc.
+  auto softmax = [&](int s) __attribute__((always_inline)) {
+    const int k0 = s * kBS;
+    if (k0 + kBS > a.Lk) {
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int x = 0; x < 16; ++x)
+          if (k0 + 16 * (x >> 3) + 8 * hl + (x & 7) >= a.Lk) sacc[qb][x] = -INFINITY;
+    }
+    float mx[2];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+      float m = fmaxf(sacc[qb][0], sacc[qb][1]);
+#pragma unroll
+      for (int x = 2; x < 16; x += 2) m = fmaxf(fmaxf(m, sacc[qb][x]), sacc[qb][x + 1]);
+      mx[qb] = half_swap_max(m);  // relative to m_run
+    }
+    // First step: adopt the max. Later: move the max only when it grew by more than kTau.
+    if (__any(s == 0 || mx[0] > kTau || mx[1] > kTau)) {
+      asm volatile("" ::: "memory");  // keep this rare path a branch
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const float delta = s == 0 ? mx[qb] : fmaxf(mx[qb], 0.f);
+        m_run[qb] += delta;
+        if (s != 0) {
+          const float alpha = fast_exp2(-delta);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) l_part[qb][j] *= alpha;
+#pragma unroll
+          for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int x = 0; x < 16; ++x) acc_o[db][qb][x] *= alpha;
+        }
+#pragma unroll
+        for (int x = 0; x < 16; ++x) {
+          sacc[qb][x] -= delta;
+          cinit[qb][x] = -m_run[qb];
+        }
+      }
+    }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch) {
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = fast_exp2(sacc[qb][ch * 8 + 2 * e]);
+          const float p1 = fast_exp2(sacc[qb][ch * 8 + 2 * e + 1]);
+          w[e] = Mfma<T>::pack(p0, p1);
+          l_part[qb][e] = Mfma<T>::dot_ones(w[e], l_part[qb][e]);
+        }
+        pcur[qb][ch] = __builtin_bit_cast(op_t, w);
+      }
+  };
+
+  // ---- first tiles (tile 0's loads were issued with Q) ----
+  lstore(0);
+  if (n_tiles > 1) {
+    gload(1);
+    lstore(1);
+  }
+  __syncthreads();
+  read_k(0);
+
+  for (int s = 0; s <= n_sub; ++s) {
+    const int t = s >> 1;
+    if (!(s & 1) && t + 2 < n_tiles) gload(t + 2);
+    // ---- MFMAs: PV of step s-1, then S of step s ----
+    mfma_priority<1>();
+    if (s >= 1) {
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+        for (int db = 0; db < 2; ++db)
+#pragma unroll
+          for (int qb = 0; qb < 2; ++qb) acc_o[db][qb] = Mfma<T>::run(vop[ch][db], pcur[qb][ch], acc_o[db][qb]);
+    }
+    if (s < n_sub) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) sacc[qb] = Mfma<T>::run(kop[ks], qreg[qb][ks], ks == 0 ? cinit[qb] : sacc[qb]);
+    }
+    mfma_priority<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    // operands of the next step: V of this one, K of the next
+    if (s < n_sub) read_v(s);
+    if (s + 1 < n_sub) read_k(s + 1);
+    // ---- VALU ----
+    if (s < n_sub) softmax(s);
+    // Tile t+2 replaces tile t-2, whose last reads (V of step 2t-3) came before the previous
+    // tile's barrier; its first reads (K of step 2t+4, read in step 2t+3) come after this one.
+    if (s & 1) {
+      if (t + 2 < n_tiles) lstore((t + 2) % kFBuf);
+      __syncthreads();
+    }
+  }
+  if (!(n_sub & 1)) __syncthreads();  // the loop's last step (s = n_sub, even) had no barrier
+
+  // ---- normalise, stage O^T through LDS as [query][dim] rows, store whole rows ----
+#pragma unroll
+  for (int qb = 0; qb < 2; ++qb) {
+    const float l_run = (l_part[qb][0] + l_part[qb][1]) + (l_part[qb][2] + l_part[qb][3]);
+    const float inv = 1.f / (l_run + __shfl_xor(l_run, 32));
+    e_t* orow = &smem[(wave * 64 + qb * 32 + l32) * kPitchK];
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        u32x2 w;
+        w[0] = Mfma<T>::pack(acc_o[db][qb][i * 4 + 0] * inv, acc_o[db][qb][i * 4 + 1] * inv);
+        w[1] = Mfma<T>::pack(acc_o[db][qb][i * 4 + 2] * inv, acc_o[db][qb][i * 4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(orow + db * 32 + i * 8 + hl * 4) = w;
+      }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kFBM / 64; ++i) {
+    const int qi = q_blk0 + crow + 64 * i;
+    if (qi < a.Lq)
+      store16(O + qi * a.os[2] + cd0, *reinterpret_cast<const u32x4*>(&smem[(crow + 64 * i) * kPitchK + cd0]));
+  }
+}
+
+// Causal / generic kernel shape: 32-query wavefronts, 8 per workgroup.
+constexpr int kQB = 1;
+constexpr int kNW = 8;
 
 template <typename T>
 hipError_t launch_typed(const DenseArgs& a, hipStream_t stream) {
+  if (!a.causal) {
+    const int n_qblk = (a.Lq + kFBM - 1) / kFBM;
+    const int64_t n = (int64_t)a.B * a.H * n_qblk;
+    if (n <= 0) return hipSuccess;
+    if (n > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((dense_fwd_kernel<T>), dim3((unsigned)n), dim3(kFThreads), 0, stream, a);
+    return hipGetLastError();
+  }
   constexpr int kBM = 32 * kQB * kNW;
   const int n_qblk = (a.Lq + kBM - 1) / kBM;
   const int64_t n = (int64_t)a.B * a.H * n_qblk;
