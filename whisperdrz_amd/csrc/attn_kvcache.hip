@@ -160,8 +160,8 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
         kp = kc_row + (int64_t)kk * a.kcs[1];
         vp = vc_row + (int64_t)kk * a.vcs[1];
       }
-      kr[u] = load16(kp);
-      vr[u] = load16(vp);
+      kr[u] = load16_stream(kp);
+      vr[u] = load16_stream(vp);
     }
     // ---- scores (log2 units), masked to -inf outside each query's key range ----
     float sc[SQ][kUnroll];
