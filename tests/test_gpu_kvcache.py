@@ -125,6 +125,41 @@ def test_verify_equals_sequential_steps(cuda):
         assert_close(out, to_np(seqout), dtype, "verify vs sequential")
 
 
+@pytest.mark.parametrize("sq", [1, 2, 5, 8, 9])
+@pytest.mark.parametrize("self_attn", [True, False])
+def test_split_workspace_stays_in_bounds(cuda, sq, self_attn):
+    """Split-path calls touch exactly the workspace bytes the size query reports: a guard
+    region right behind it keeps its bytes, and the workspace itself is left all-zero."""
+    from whisperdrz_amd import flash_attn_with_kvcache, kvcache_workspace_size
+
+    B, H, Lmax = 2, 4, 600
+    need = kvcache_workspace_size(B, sq, H, D, Lmax)
+    assert need > 0, "this shape is meant to take the split path"
+    guard = 4096
+    buf = torch.zeros(need + guard, dtype=torch.uint8, device=cuda)
+    buf[need:] = 0xAB
+    rng = np.random.default_rng(sq)
+    kc, vc = make_cache(B, Lmax, H, D, torch.bfloat16, cuda, "head_major", 70 + sq)
+    kc0, vc0 = to_np(kc), to_np(vc)
+    q = randn((B, sq, H, D), 71 + sq, torch.bfloat16).to(cuda)
+    bidx_np = np.array([1, 0], dtype=np.int32)
+    bidx = torch.from_numpy(bidx_np).to(cuda)
+    print(f"workspace guard: sq={sq} self={self_attn} need={need}", flush=True)
+    if self_attn:
+        k = randn((B, sq, H, D), 72 + sq, torch.bfloat16).to(cuda)
+        cs = rng.integers(0, Lmax - sq + 1, size=B).astype(np.int32)
+        out = flash_attn_with_kvcache(q, kc, vc, k=k, v=k, cache_seqlens=torch.from_numpy(cs).to(cuda),
+                                      cache_batch_idx=bidx, softmax_scale=0.125, workspace=buf[:need])
+        ref, _, _ = kvcache_ref(to_np(q), kc0, vc0, to_np(k), to_np(k), cs, bidx_np, 0.125)
+    else:
+        out = flash_attn_with_kvcache(q, kc, vc, cache_batch_idx=bidx, softmax_scale=0.125, workspace=buf[:need])
+        ref, _, _ = kvcache_ref(to_np(q), kc0, vc0, None, None, None, bidx_np, 0.125)
+    torch.cuda.synchronize()
+    assert_close(out, ref, torch.bfloat16, f"guarded workspace sq={sq}")
+    assert int(torch.count_nonzero(buf[:need])) == 0, "workspace not left all-zero"
+    assert bool((buf[need:] == 0xAB).all()), "bytes past the reported workspace size were written"
+
+
 def test_bad_slot_gives_nan_not_fault(cuda):
     """An out-of-range slot id (which the host cannot see) yields NaN rows and no memory access."""
     from whisperdrz_amd import flash_attn_with_kvcache

@@ -59,6 +59,137 @@ template <> struct Dot2<F16> {
 // which a NaN literal would be undefined); it marks output rows with invalid metadata.
 __device__ __forceinline__ float quiet_nan() { return __uint_as_float(0x7fc00000u); }
 
+// In-place append (fused cache write) of query block [t0, t0 + nq) of batch row b, head h: the
+// new rows whose cache position falls in this split's key range are copied from k_new / v_new.
+template <typename T>
+__device__ __forceinline__ void kv_append(const KvArgs& a, int b, int t0, int nq, int h, int split, int slot,
+                                          int cs) {
+  constexpr int LPK = kHeadDim * ElemBytes<T>::value / 16;  // 16-byte pieces per head row
+  const int lo = split * a.split_len, hi = lo + a.split_len;
+  for (int idx = threadIdx.x; idx < nq * 2 * LPK; idx += blockDim.x) {
+    const int t = idx / (2 * LPK);
+    const int which = (idx / LPK) & 1;
+    const int rr = idx % LPK;
+    const int pos = cs + t0 + t;
+    if (pos >= lo && pos < hi) {
+      if (which == 0)
+        store16(a.kc + slot * a.kcs[0] + (int64_t)pos * a.kcs[1] + h * a.kcs[2] + rr * 16,
+                load16(a.kn + b * a.kns[0] + (int64_t)(t0 + t) * a.kns[1] + h * a.kns[2] + rr * 16));
+      else
+        store16(a.vc + slot * a.vcs[0] + (int64_t)pos * a.vcs[1] + h * a.vcs[2] + rr * 16,
+                load16(a.vn + b * a.vns[0] + (int64_t)(t0 + t) * a.vns[1] + h * a.vns[2] + rr * 16));
+    }
+  }
+}
+
+// Combines the per-wavefront partials (o[64], m, l per query, in LDS) of one workgroup and
+// writes the output rows, or, when the row's keys are split over several workgroups,
+// publishes this split's partial and lets the last split to arrive merge them all.
+template <typename T, int SQ, int kWaves>
+__device__ __forceinline__ void kv_finish(const KvArgs& a, int b, int t0, int nq, int sq_stride, int h, int split,
+                                          int n_split_b, bool bad, float (&sm_acc)[kWaves][SQ][kHeadDim],
+                                          float (&sm_m)[kWaves][SQ], float (&sm_l)[kWaves][SQ]) {
+  constexpr int kThreads = kWaves * 64;
+  constexpr int EB = ElemBytes<T>::value;
+  constexpr int kPart = kHeadDim + 2;  // floats per partial: o[64], m, l
+  __shared__ int sm_last;
+  const int tid = threadIdx.x;
+  auto store_out = [&](int t, int d, float val) {
+    char* op = a.o + b * a.os[0] + (t0 + t) * a.os[1] + h * a.os[2];
+    if constexpr (EB == 4)
+      reinterpret_cast<float*>(op)[d] = val;
+    else if constexpr (__is_same(T, Bf16))
+      reinterpret_cast<__bf16*>(op)[d] = (__bf16)val;
+    else
+      reinterpret_cast<_Float16*>(op)[d] = (_Float16)val;
+  };
+  // This workgroup's (o, m, l) for query t, dim d, from the per-wavefront LDS partials.
+  auto wg_partial = [&](int t, int d, float& O, float& M, float& L) {
+    M = kNegBig;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][t]);
+    L = 0.f;
+    O = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float f = fast_exp2(sm_m[w][t] - M);
+      L = __builtin_fmaf(sm_l[w][t], f, L);
+      O = __builtin_fmaf(sm_acc[w][t][d], f, O);
+    }
+  };
+
+  if (n_split_b == 1) {
+    for (int idx = tid; idx < nq * kHeadDim; idx += kThreads) {
+      const int t = idx / kHeadDim, d = idx % kHeadDim;
+      float O, M, L;
+      wg_partial(t, d, O, M, L);
+      store_out(t, d, bad ? quiet_nan() : O / L);
+    }
+    return;
+  }
+
+  // ---- several splits: publish this split's partial; the last split to arrive merges ----
+  // Partials are laid out with the workspace's row stride sq_stride (= the launch's query block,
+  // which the host sized the workspace for; it can be smaller than SQ).
+  const int64_t unit = ((int64_t)b * a.n_qblocks + t0 / sq_stride) * a.H + h;
+  float* part = a.ws_part + (unit * a.n_splits) * (sq_stride * kPart);
+  for (int idx = tid; idx < nq * kHeadDim; idx += kThreads) {
+    const int t = idx / kHeadDim, d = idx % kHeadDim;
+    float O, M, L;
+    wg_partial(t, d, O, M, L);
+    float* pp = part + (split * sq_stride + t) * kPart;
+    __hip_atomic_store(pp + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (d == 0) {
+      __hip_atomic_store(pp + kHeadDim, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(pp + kHeadDim + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  // Ordering without cache maintenance: the partial was written with agent-scope atomic
+  // stores, which complete at the device coherence point; waiting for them (vmcnt 0) before
+  // the counter update makes it visible to whichever split reads the count last. (A C++
+  // release fence here would write back the whole L2 of this XCD from every split.)
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0);
+  asm volatile("" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const int prev = __hip_atomic_fetch_add(a.ws_count + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sm_last = prev == n_split_b - 1;
+  }
+  __syncthreads();
+  if (!sm_last) return;
+  // The merging workgroup reads the partials with agent-scope atomic loads (coherent, issued
+  // only after the counter told it every partial had landed): first every (m, l) pair in
+  // parallel into LDS, then one o value per (split, query, dim).
+  __shared__ float sm_pm[kMaxMergeSplits * SQ], sm_pl[kMaxMergeSplits * SQ];
+  for (int idx = tid; idx < n_split_b * nq; idx += kThreads) {
+    const int sp = idx / nq, t = idx % nq;
+    float* pp = part + (sp * sq_stride + t) * kPart;
+    sm_pm[sp * SQ + t] = __hip_atomic_load(pp + kHeadDim, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    sm_pl[sp * SQ + t] = __hip_atomic_load(pp + kHeadDim + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    pp[kHeadDim] = 0.f;  // consumed: leave the workspace all-zero (see below)
+    pp[kHeadDim + 1] = 0.f;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < nq * kHeadDim; idx += kThreads) {
+    const int t = idx / kHeadDim, d = idx % kHeadDim;
+    float mm = kNegBig;
+    for (int sp = 0; sp < n_split_b; ++sp) mm = fmaxf(mm, sm_pm[sp * SQ + t]);
+    float L = 0.f, O = 0.f;
+    for (int sp = 0; sp < n_split_b; ++sp) {
+      const float f = fast_exp2(sm_pm[sp * SQ + t] - mm);
+      L = __builtin_fmaf(sm_pl[sp * SQ + t], f, L);
+      float* po = part + (sp * sq_stride + t) * kPart + d;
+      O = __builtin_fmaf(__hip_atomic_load(po, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), f, O);
+      *po = 0.f;
+    }
+    store_out(t, d, O / L);
+  }
+  // Leave the counter at zero too. Every call returns the whole workspace to all-zero, so the
+  // counters of any later call, whatever its shape and therefore its layout, start at zero.
+  if (tid == 0) __hip_atomic_store(a.ws_count + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 template <typename T, int SQ, bool HAS_NEW>
 __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
   constexpr int kThreads = kWavesPerWg * 64;
@@ -67,12 +198,10 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
   constexpr int EPL = 16 / EB;         // elements per lane per 16-byte load
   constexpr int LPK = kHeadDim / EPL;  // lanes per key row
   constexpr int G = kThreads / LPK;    // key groups per workgroup
-  constexpr int kPart = kHeadDim + 2;  // floats per partial: o[64], m, l
 
   __shared__ float sm_acc[kWaves][SQ][kHeadDim];
   __shared__ float sm_m[kWaves][SQ];
   __shared__ float sm_l[kWaves][SQ];
-  __shared__ int sm_last;
 
   const int tid = threadIdx.x;
   const int g = tid / LPK;
@@ -251,25 +380,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
   }
 
   // In-place append of this block's new rows that fall in this split's key range.
-  if (HAS_NEW && !bad) {
-    const int lo = split * a.split_len, hi = lo + a.split_len;
-    for (int idx = tid; idx < nq * 2 * LPK; idx += kThreads) {
-      const int t = idx / (2 * LPK);
-      const int which = (idx / LPK) & 1;
-      const int rr = idx % LPK;
-      const int pos = cs + t0 + t;
-      if (pos >= lo && pos < hi) {
-        if (which == 0)
-          store16(a.kc + slot * a.kcs[0] + (int64_t)pos * a.kcs[1] + h * a.kcs[2] + rr * 16,
-                  load16(a.kn + b * a.kns[0] + (int64_t)(t0 + t) * a.kns[1] + h * a.kns[2] +
-                         rr * 16));
-        else
-          store16(a.vc + slot * a.vcs[0] + (int64_t)pos * a.vcs[1] + h * a.vcs[2] + rr * 16,
-                  load16(a.vn + b * a.vns[0] + (int64_t)(t0 + t) * a.vns[1] + h * a.vns[2] +
-                         rr * 16));
-      }
-    }
-  }
+  if (HAS_NEW && !bad) kv_append<T>(a, b, t0, nq, h, split, slot, cs);
 
   // Merge lane groups inside the wavefront (groups differ in lane bits >= log2(LPK)).
 #pragma unroll
@@ -299,98 +410,228 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
   }
   __syncthreads();
 
-  auto store_out = [&](int t, int d, float val) {
-    char* op = a.o + b * a.os[0] + (t0 + t) * a.os[1] + h * a.os[2];
-    if constexpr (EB == 4)
-      reinterpret_cast<float*>(op)[d] = val;
-    else if constexpr (__is_same(T, Bf16))
-      reinterpret_cast<__bf16*>(op)[d] = (__bf16)val;
-    else
-      reinterpret_cast<_Float16*>(op)[d] = (_Float16)val;
+  kv_finish<T, SQ, kWaves>(a, b, t0, nq, SQ, h, split, n_split_b, bad, sm_acc, sm_m, sm_l);
+}
+
+// ============================================================================================
+// Multi-query rows on the matrix core (16-bit types, 2 <= sq <= 8: draft verify, prefill
+// chunks). With several queries per row the VALU form above spends most of its time on the
+// per-query dot products, reductions and exps of every key; here a wavefront takes 32 keys
+// per step and computes
+//   S^T (32 keys x 16 query slots) = K . Q^T       with 4 v_mfma_f32_16x16x32,
+//   O^T (64 dims x 16 query slots) += V^T . P^T    with 4 more,
+// so the VALU only runs the softmax of 8 scores per lane. K rows feed the A operand straight
+// from global memory (lane l: key l%16 of a 16-key block, dims 8*(l/16)..+7 of a 32-dim half);
+// V rows go through a per-wavefront LDS tile and come back transposed by ds_read_b64_tr_b16.
+// The P^T operand is the S^T accumulator itself: lane l holds query l%16 and keys
+// 4*(l/16)..+3 of each 16-key block, i.e. keys {4g..4g+3, 16+4g..16+4g+3} for g = l/16, and the
+// V^T operand is read in that same key order. Query slots >= sq are computed and discarded.
+// The four wavefronts of a workgroup take interleaved 32-key chunks of the row (or split);
+// their partials merge through LDS as in the VALU kernel.
+// ============================================================================================
+constexpr int kMqChunk = 32;                   // keys per wavefront step
+constexpr int kMqPitch = kHeadDim + 8;         // V tile row pitch (elements)
+
+template <typename T> struct Mfma16;
+template <> struct Mfma16<Bf16> {
+  typedef bf16x8 op_t;
+  static __device__ __forceinline__ f32x4 run(op_t a, op_t b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma16<F16> {
+  typedef f16x8 op_t;
+  static __device__ __forceinline__ f32x4 run(op_t a, op_t b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// Transposing LDS read (ds_read_b64_tr_b16): within each 16-lane group, lane i receives element
+// i%4 of the 8-byte chunks read by lanes 4c + i/4 (c = 0..3). `p` must point into __shared__
+// memory (its low 32 bits are the LDS byte address).
+__device__ __forceinline__ u32x2 kv_read_tr16(const uint16_t* p) {
+#if __HIP_DEVICE_COMPILE__
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(uint32_t)(uintptr_t)p));
+#else
+  (void)p;
+  return u32x2{0, 0};
+#endif
+}
+
+// max of x over lanes l, l^16, l^32, l^48 (the four 16-lane groups), in every lane
+__device__ __forceinline__ float group4_max(float x) {
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+}
+
+template <typename T, bool HAS_NEW>
+__global__ __launch_bounds__(kWavesPerWg * 64) void kv_mq_kernel(KvArgs a) {
+  typedef typename Mfma16<T>::op_t op_t;
+  constexpr int kWaves = kWavesPerWg;
+  constexpr int SQ = kMaxSQ;
+  __shared__ float sm_acc[kWaves][SQ][kHeadDim];
+  __shared__ float sm_m[kWaves][SQ];
+  __shared__ float sm_l[kWaves][SQ];
+  __shared__ __attribute__((aligned(16))) uint16_t sm_v[kWaves][kMqChunk * kMqPitch];
+
+  const int tid = threadIdx.x;
+  const int wave = tid / 64;
+  const int lane = tid % 64;
+  const int qi = lane & 15;  // query slot of this lane
+  const int gq = lane >> 4;  // 16-lane group
+
+  const int b = blockIdx.x;
+  const int h = blockIdx.y;
+  const int split = blockIdx.z;
+  const int nq = a.sq;
+
+  const int slot = a.bidx ? a.bidx[b] : b;
+  const int cs = HAS_NEW ? a.seqlens[b] : 0;
+  const bool bad = slot < 0 || slot >= a.n_slots || cs < 0 || (HAS_NEW && cs + a.sq > a.Lk);
+  int key_lim;
+  if (HAS_NEW)
+    key_lim = cs + nq;
+  else if (a.causal)
+    key_lim = min(a.Lk, nq);
+  else
+    key_lim = a.Lk;
+  const int n_split_b = bad ? 1 : max(1, (key_lim + a.split_len - 1) / a.split_len);
+  if (split >= n_split_b) return;
+  const int k_begin = split * a.split_len;
+  const int k_end = bad ? k_begin : min(key_lim, k_begin + a.split_len);
+  // last key this lane's query may see (slots >= nq see none)
+  int lim = k_end - 1;
+  if (HAS_NEW) lim = min(lim, cs + qi);
+  else if (a.causal) lim = min(lim, qi);
+  if (qi >= nq) lim = -1;
+
+  // Q^T operand halves: query qi (clamped), dims 32*dh + 8*gq .. +7
+  op_t qop[2];
+  {
+    const char* qrow = a.q + b * a.qs[0] + min(qi, nq - 1) * a.qs[1] + h * a.qs[2];
+#pragma unroll
+    for (int dh = 0; dh < 2; ++dh) qop[dh] = __builtin_bit_cast(op_t, load16(qrow + (32 * dh + 8 * gq) * 2));
+  }
+
+  const int safe_slot = bad ? 0 : slot;
+  const char* kc_row = a.kc + safe_slot * a.kcs[0] + h * a.kcs[2];
+  const char* vc_row = a.vc + safe_slot * a.vcs[0] + h * a.vcs[2];
+  const char* kn_row = HAS_NEW ? a.kn + b * a.kns[0] + h * a.kns[2] : nullptr;
+  const char* vn_row = HAS_NEW ? a.vn + b * a.vns[0] + h * a.vns[2] : nullptr;
+  auto k_ptr = [&](int key) __attribute__((always_inline)) {
+    return (HAS_NEW && key >= cs) ? kn_row + (int64_t)(key - cs) * a.kns[1] : kc_row + (int64_t)key * a.kcs[1];
   };
-  // This workgroup's (o, m, l) for query t, dim d, from the per-wavefront LDS partials.
-  auto wg_partial = [&](int t, int d, float& O, float& M, float& L) {
-    M = kNegBig;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, sm_m[w][t]);
-    L = 0.f;
-    O = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float f = fast_exp2(sm_m[w][t] - M);
-      L = __builtin_fmaf(sm_l[w][t], f, L);
-      O = __builtin_fmaf(sm_acc[w][t][d], f, O);
-    }
+  auto v_ptr = [&](int key) __attribute__((always_inline)) {
+    return (HAS_NEW && key >= cs) ? vn_row + (int64_t)(key - cs) * a.vns[1] : vc_row + (int64_t)key * a.vcs[1];
   };
 
-  if (n_split_b == 1) {
-    for (int idx = tid; idx < nq * kHeadDim; idx += kThreads) {
-      const int t = idx / kHeadDim, d = idx % kHeadDim;
-      float O, M, L;
-      wg_partial(t, d, O, M, L);
-      store_out(t, d, bad ? quiet_nan() : O / L);
+  // Loads of one 32-key chunk: K operands (kop[kb][dh]: key kb*16 + l%16, 16 bytes at dims
+  // 32*dh + 8*(l/16)) and this lane's four 16-byte pieces of the V tile (rows (l + 64*i)/8).
+  op_t kop[2][2];
+  u32x4 vld[4];
+  auto load_chunk = [&](int key0) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const char* kp = k_ptr(min(key0 + kb * 16 + qi, k_end - 1));
+#pragma unroll
+      for (int dh = 0; dh < 2; ++dh) kop[kb][dh] = __builtin_bit_cast(op_t, load16_stream(kp + (32 * dh + 8 * gq) * 2));
     }
-    return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int piece = lane + 64 * i;
+      vld[i] = load16_stream(v_ptr(min(key0 + (piece >> 3), k_end - 1)) + (piece & 7) * 16);
+    }
+  };
+  uint16_t* vt = sm_v[wave];
+  // transposing-read base for this lane: key row 4*gq + (j>>2) (+16 for the second read), dims
+  // 4*(j&3) of each 16-dim block, j = lane index in its 16-lane group
+  const uint16_t* vt_lane = vt + (4 * gq + (qi >> 2)) * kMqPitch + 4 * (qi & 3);
+
+  float m = kNegBig, l = 0.f;
+  f32x4 o[4];  // O^T blocks: dims 16*db + 4*gq + i, query qi
+#pragma unroll
+  for (int db = 0; db < 4; ++db) o[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int stride = kWaves * kMqChunk;
+  int key0 = k_begin + wave * kMqChunk;
+  if (key0 < k_end) load_chunk(key0);
+  for (; key0 < k_end; key0 += stride) {
+    // V tile of this chunk into LDS ([key][dim], padded rows)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int piece = lane + 64 * i;
+      *reinterpret_cast<u32x4*>(&vt[(piece >> 3) * kMqPitch + (piece & 7) * 8]) = vld[i];
+    }
+    // ---- S^T = K Q^T for the two 16-key blocks ----
+    f32x4 sblk[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      sblk[kb] = Mfma16<T>::run(kop[kb][0], qop[0], f32x4{0.f, 0.f, 0.f, 0.f});
+      sblk[kb] = Mfma16<T>::run(kop[kb][1], qop[1], sblk[kb]);
+    }
+    // next chunk's loads (registers are free once the MFMAs above are issued)
+    if (key0 + stride < k_end) load_chunk(key0 + stride);
+    // ---- V^T operands (same key order as P^T) ----
+    op_t vop[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const u32x2 lo = kv_read_tr16(vt_lane + 16 * db);
+      const u32x2 hi = kv_read_tr16(vt_lane + 16 * kMqPitch + 16 * db);
+      vop[db] = __builtin_bit_cast(op_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
+    }
+    // ---- softmax of the lane's 8 scores (log2 units), masked past each query's limit ----
+    float sc[8];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int key = key0 + kb * 16 + 4 * gq + i;
+        sc[kb * 4 + i] = key <= lim ? sblk[kb][i] * a.c : -INFINITY;
+      }
+    float mb = fmaxf(fmaxf(fmaxf(sc[0], sc[1]), fmaxf(sc[2], sc[3])), fmaxf(fmaxf(sc[4], sc[5]), fmaxf(sc[6], sc[7])));
+    mb = group4_max(mb);
+    if (__any(mb > m + kTau)) {
+      asm volatile("" ::: "memory");  // keep this rare path a branch
+      const float mn = mb > m + kTau ? mb : m;
+      const float alpha = fast_exp2(m - mn);
+      m = mn;
+      l *= alpha;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) o[db] *= alpha;
+    }
+    uint32_t pw[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      pw[j] = Dot2<T>::pack(fast_exp2(sc[2 * j] - m), fast_exp2(sc[2 * j + 1] - m));
+      l = Dot2<T>::run(pw[j], Dot2<T>::kOnes, l);
+    }
+    const op_t pop = __builtin_bit_cast(op_t, u32x4{pw[0], pw[1], pw[2], pw[3]});
+    // ---- O^T += V^T P^T ----
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[db] = Mfma16<T>::run(vop[db], pop, o[db]);
   }
 
-  // ---- several splits: publish this split's partial; the last split to arrive merges ----
-  const int64_t unit = ((int64_t)b * a.n_qblocks + t0 / SQ) * a.H + h;
-  float* part = a.ws_part + (unit * a.n_splits) * (SQ * kPart);
-  for (int idx = tid; idx < nq * kHeadDim; idx += kThreads) {
-    const int t = idx / kHeadDim, d = idx % kHeadDim;
-    float O, M, L;
-    wg_partial(t, d, O, M, L);
-    float* pp = part + (split * SQ + t) * kPart;
-    __hip_atomic_store(pp + d, O, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (d == 0) {
-      __hip_atomic_store(pp + kHeadDim, M, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(pp + kHeadDim + 1, L, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (HAS_NEW && !bad) kv_append<T>(a, b, 0, nq, h, split, slot, cs);
+
+  // row sums: the four lane groups hold different keys of the same query
+  l += __shfl_xor(l, 16);
+  l += __shfl_xor(l, 32);
+  if (qi < nq) {
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) sm_acc[wave][qi][16 * db + 4 * gq + i] = o[db][i];
+    if (gq == 0) {
+      sm_m[wave][qi] = m;
+      sm_l[wave][qi] = l;
     }
   }
-  // Ordering without cache maintenance: the partial was written with agent-scope atomic
-  // stores, which complete at the device coherence point; waiting for them (vmcnt 0) before
-  // the counter update makes it visible to whichever split reads the count last. (A C++
-  // release fence here would write back the whole L2 of this XCD from every split.)
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_waitcnt(0);
-  asm volatile("" ::: "memory");
   __syncthreads();
-  if (tid == 0) {
-    const int prev = __hip_atomic_fetch_add(a.ws_count + unit, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sm_last = prev == n_split_b - 1;
-  }
-  __syncthreads();
-  if (!sm_last) return;
-  // The merging workgroup reads the partials with agent-scope atomic loads (coherent, issued
-  // only after the counter told it every partial had landed): first every (m, l) pair in
-  // parallel into LDS, then one o value per (split, query, dim).
-  __shared__ float sm_pm[kMaxMergeSplits * SQ], sm_pl[kMaxMergeSplits * SQ];
-  for (int idx = tid; idx < n_split_b * nq; idx += kThreads) {
-    const int sp = idx / nq, t = idx % nq;
-    float* pp = part + (sp * SQ + t) * kPart;
-    sm_pm[sp * SQ + t] = __hip_atomic_load(pp + kHeadDim, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    sm_pl[sp * SQ + t] = __hip_atomic_load(pp + kHeadDim + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    pp[kHeadDim] = 0.f;  // consumed: leave the workspace all-zero (see below)
-    pp[kHeadDim + 1] = 0.f;
-  }
-  __syncthreads();
-  for (int idx = tid; idx < nq * kHeadDim; idx += kThreads) {
-    const int t = idx / kHeadDim, d = idx % kHeadDim;
-    float mm = kNegBig;
-    for (int sp = 0; sp < n_split_b; ++sp) mm = fmaxf(mm, sm_pm[sp * SQ + t]);
-    float L = 0.f, O = 0.f;
-    for (int sp = 0; sp < n_split_b; ++sp) {
-      const float f = fast_exp2(sm_pm[sp * SQ + t] - mm);
-      L = __builtin_fmaf(sm_pl[sp * SQ + t], f, L);
-      float* po = part + (sp * SQ + t) * kPart + d;
-      O = __builtin_fmaf(__hip_atomic_load(po, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT), f, O);
-      *po = 0.f;
-    }
-    store_out(t, d, O / L);
-  }
-  // Leave the counter at zero too. Every call returns the whole workspace to all-zero, so the
-  // counters of any later call, whatever its shape and therefore its layout, start at zero.
-  if (tid == 0) __hip_atomic_store(a.ws_count + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  kv_finish<T, SQ, kWaves>(a, b, 0, nq, nq, h, split, n_split_b, bad, sm_acc, sm_m, sm_l);
 }
 
 template <typename T>
@@ -398,6 +639,15 @@ hipError_t launch_typed(const KvArgs& a, hipStream_t stream) {
   dim3 grid(a.B * a.n_qblocks, a.H, a.n_splits);
   const bool has_new = a.kn != nullptr;
   const int sq_blk = a.n_qblocks > 1 ? kMaxSQ : a.sq;
+  if constexpr (ElemBytes<T>::value == 2) {
+    if (a.n_qblocks == 1 && sq_blk >= 2) {
+      if (has_new)
+        hipLaunchKernelGGL((kv_mq_kernel<T, true>), grid, dim3(kWavesPerWg * 64), 0, stream, a);
+      else
+        hipLaunchKernelGGL((kv_mq_kernel<T, false>), grid, dim3(kWavesPerWg * 64), 0, stream, a);
+      return hipGetLastError();
+    }
+  }
 #define WDRZ_KV_CASE(SQV)                                                                       \
   case SQV:                                                                                     \
     if (has_new)                                                                                \
