@@ -248,7 +248,7 @@ def bench_decode(dev, steps: int, warmup: int) -> dict:
     res["config5_verify_self_plus_cross"] = run_graph(
         "config5 verify sq=5 (self+cross)", body5, bytes5_self + bytes5_cross,
         {"sum_L": sumL5, "bytes_self_per_layer": bytes5_self, "bytes_cross_per_layer": bytes5_cross},
-        kernels=("kv_attn_kernel<wdrz::Bf16, 5, true>", "kv_attn_kernel<wdrz::Bf16, 5, false>"),
+        kernels=("kv_mq_kernel<wdrz::Bf16, true>", "kv_mq_kernel<wdrz::Bf16, false>"),
     )
     del self_kv, cross_kv
     torch.cuda.empty_cache()
