@@ -62,7 +62,7 @@ def test_self_attention(cuda, dtype, sq, layout):
     _case(cuda, dtype, B=6, sq=sq, H=4, n_slots=9, Lmax=448, layout=layout, seed=100 + sq)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("Lmax", [1, 63, 100, 1500])
 @pytest.mark.parametrize("sq", [1, 5])
 def test_cross_attention(cuda, dtype, Lmax, sq):
@@ -160,21 +160,27 @@ def test_split_workspace_stays_in_bounds(cuda, sq, self_attn):
     assert bool((buf[need:] == 0xAB).all()), "bytes past the reported workspace size were written"
 
 
-def test_bad_slot_gives_nan_not_fault(cuda):
+@pytest.mark.parametrize("sq", [1, 4])
+@pytest.mark.parametrize("self_attn", [True, False])
+def test_bad_slot_gives_nan_not_fault(cuda, sq, self_attn):
     """An out-of-range slot id (which the host cannot see) yields NaN rows and no memory access."""
     from whisperdrz_amd import flash_attn_with_kvcache
 
     kc, vc = make_cache(3, 64, 2, D, torch.bfloat16, cuda, "slot_major", 1)
     snap_k = kc.clone()
-    q = randn((2, 1, 2, D), 2, torch.bfloat16).to(cuda)
-    k = randn((2, 1, 2, D), 3, torch.bfloat16).to(cuda)
+    q = randn((2, sq, 2, D), 2, torch.bfloat16).to(cuda)
+    k = randn((2, sq, 2, D), 3, torch.bfloat16).to(cuda)
     bidx = torch.tensor([1, 3], dtype=torch.int32, device=cuda)
     seq = torch.tensor([5, 5], dtype=torch.int32, device=cuda)
-    out = flash_attn_with_kvcache(q, kc, vc, k=k, v=k, cache_seqlens=seq, cache_batch_idx=bidx)
+    if self_attn:
+        out = flash_attn_with_kvcache(q, kc, vc, k=k, v=k, cache_seqlens=seq, cache_batch_idx=bidx)
+    else:
+        out = flash_attn_with_kvcache(q, kc, vc, cache_batch_idx=bidx)
     torch.cuda.synchronize()
     assert torch.isfinite(out[0].float()).all()
     assert torch.isnan(out[1].float()).all()
-    snap_k[1, 5] = k[0, 0]
+    if self_attn:
+        snap_k[1, 5 : 5 + sq] = k[0]
     assert torch.equal(kc, snap_k)
 
 
