@@ -540,9 +540,12 @@ __global__ __launch_bounds__(kFThreads, 1) void dense_fwd_kernel(DenseArgs a) {
     float mx[2];
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb) {
-      float m = fmaxf(sacc[qb][0], sacc[qb][1]);
-#pragma unroll
-      for (int x = 2; x < 16; x += 2) m = fmaxf(fmaxf(m, sacc[qb][x]), sacc[qb][x + 1]);
+      // a tree of 3-input maxima (depth 3, not a chain of 8)
+      const f32x16& v = sacc[qb];
+      const float t0 = fmaxf(fmaxf(v[0], v[1]), v[2]), t1 = fmaxf(fmaxf(v[3], v[4]), v[5]);
+      const float t2 = fmaxf(fmaxf(v[6], v[7]), v[8]), t3 = fmaxf(fmaxf(v[9], v[10]), v[11]);
+      const float t4 = fmaxf(fmaxf(v[12], v[13]), v[14]);
+      const float m = fmaxf(fmaxf(fmaxf(t0, t1), t2), fmaxf(fmaxf(t3, t4), v[15]));
       mx[qb] = half_swap_max(m);  // relative to m_run
     }
     // First step: adopt the max. Later: move the max only when it grew by more than kTau.
