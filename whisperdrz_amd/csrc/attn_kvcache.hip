@@ -59,27 +59,40 @@ template <> struct Dot2<F16> {
 // which a NaN literal would be undefined); it marks output rows with invalid metadata.
 __device__ __forceinline__ float quiet_nan() { return __uint_as_float(0x7fc00000u); }
 
-// In-place append (fused cache write) of query block [t0, t0 + nq) of batch row b, head h: the
-// new rows whose cache position falls in this split's key range are copied from k_new / v_new.
+// In-place append (fused cache write) of query block [t0, t0 + nq) of batch row b, head h:
+// thread i moves 16-byte piece i of the block's new K and V rows. The load is issued at kernel
+// start, the store (by the split whose key range holds the row's position) after the key loop,
+// so the load latency stays off the critical path.
+struct AppendPiece {
+  u32x4 v;
+  bool on;
+  int t, which, rr;  // query row in the block, K (0) or V (1), 16-byte piece in the head row
+};
 template <typename T>
-__device__ __forceinline__ void kv_append(const KvArgs& a, int b, int t0, int nq, int h, int split, int slot,
-                                          int cs) {
+__device__ __forceinline__ AppendPiece kv_append_load(const KvArgs& a, int b, int t0, int nq, int h) {
   constexpr int LPK = kHeadDim * ElemBytes<T>::value / 16;  // 16-byte pieces per head row
+  AppendPiece p;
+  const int idx = threadIdx.x;
+  p.on = idx < nq * 2 * LPK;
+  p.t = idx / (2 * LPK);
+  p.which = (idx / LPK) & 1;
+  p.rr = idx % LPK;
+  p.v = u32x4{0, 0, 0, 0};
+  if (p.on)
+    p.v = load16((p.which ? a.vn + b * a.vns[0] + (int64_t)(t0 + p.t) * a.vns[1] + h * a.vns[2]
+                          : a.kn + b * a.kns[0] + (int64_t)(t0 + p.t) * a.kns[1] + h * a.kns[2]) +
+                 p.rr * 16);
+  return p;
+}
+__device__ __forceinline__ void kv_append_store(const KvArgs& a, const AppendPiece& p, int t0, int h, int split,
+                                                int slot, int cs) {
   const int lo = split * a.split_len, hi = lo + a.split_len;
-  for (int idx = threadIdx.x; idx < nq * 2 * LPK; idx += blockDim.x) {
-    const int t = idx / (2 * LPK);
-    const int which = (idx / LPK) & 1;
-    const int rr = idx % LPK;
-    const int pos = cs + t0 + t;
-    if (pos >= lo && pos < hi) {
-      if (which == 0)
-        store16(a.kc + slot * a.kcs[0] + (int64_t)pos * a.kcs[1] + h * a.kcs[2] + rr * 16,
-                load16(a.kn + b * a.kns[0] + (int64_t)(t0 + t) * a.kns[1] + h * a.kns[2] + rr * 16));
-      else
-        store16(a.vc + slot * a.vcs[0] + (int64_t)pos * a.vcs[1] + h * a.vcs[2] + rr * 16,
-                load16(a.vn + b * a.vns[0] + (int64_t)(t0 + t) * a.vns[1] + h * a.vns[2] + rr * 16));
-    }
-  }
+  const int pos = cs + t0 + p.t;
+  if (p.on && pos >= lo && pos < hi)
+    store16((p.which ? a.vc + slot * a.vcs[0] + (int64_t)pos * a.vcs[1] + h * a.vcs[2]
+                     : a.kc + slot * a.kcs[0] + (int64_t)pos * a.kcs[1] + h * a.kcs[2]) +
+                p.rr * 16,
+            p.v);
 }
 
 // Combines the per-wavefront partials (o[64], m, l per query, in LDS) of one workgroup and
@@ -217,6 +230,16 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
 
   const int slot = a.bidx ? a.bidx[b] : b;
   const int cs = HAS_NEW ? a.seqlens[b] : 0;
+  // Loads that need no metadata are issued while it arrives: the queries and the rows to
+  // append (stored after the key loop, when they have long arrived).
+  u32x4 qraw[SQ];
+#pragma unroll
+  for (int t = 0; t < SQ; ++t) {
+    const int tt = t0 + min(t, nq - 1);
+    qraw[t] = load16(a.q + b * a.qs[0] + tt * a.qs[1] + h * a.qs[2] + r * 16);
+  }
+  static_assert(kMaxSQ * 2 * LPK <= kThreads, "one append piece per thread");
+  const AppendPiece app = HAS_NEW ? kv_append_load<T>(a, b, t0, nq, h) : AppendPiece{};
   // Metadata the host cannot validate without reading device memory. A bad row produces NaN
   // output instead of touching memory outside the cache.
   const bool bad = slot < 0 || slot >= a.n_slots || cs < 0 || (HAS_NEW && cs + a.sq > a.Lk);
@@ -237,12 +260,9 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
 
   // Queries. 16-bit types keep the raw packed pairs for v_dot2 (the scale is applied to the
   // reduced score); fp32 keeps floats pre-scaled into the log2 domain.
-  u32x4 qraw[SQ];
   float qf[SQ][EPL];
 #pragma unroll
   for (int t = 0; t < SQ; ++t) {
-    const int tt = t0 + min(t, nq - 1);
-    qraw[t] = load16(a.q + b * a.qs[0] + tt * a.qs[1] + h * a.qs[2] + r * 16);
     if constexpr (EB == 4) {
       Slice<T> sl;
       sl.from_raw(qraw[t]);
@@ -379,8 +399,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
     }
   }
 
-  // In-place append of this block's new rows that fall in this split's key range.
-  if (HAS_NEW && !bad) kv_append<T>(a, b, t0, nq, h, split, slot, cs);
+  if (HAS_NEW && !bad) kv_append_store(a, app, t0, h, split, slot, cs);
 
   // Merge lane groups inside the wavefront (groups differ in lane bits >= log2(LPK)).
 #pragma unroll
@@ -493,6 +512,8 @@ __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
 
   const int slot = a.bidx ? a.bidx[b] : b;
   const int cs = HAS_NEW ? a.seqlens[b] : 0;
+  static_assert(kMaxSQ * 2 * (kHeadDim * 2 / 16) <= kWaves * 64, "one append piece per thread");
+  const AppendPiece app = HAS_NEW ? kv_append_load<T>(a, b, 0, nq, h) : AppendPiece{};
   const bool bad = slot < 0 || slot >= a.n_slots || cs < 0 || (HAS_NEW && cs + a.sq > a.Lk);
   int key_lim;
   if (HAS_NEW)
@@ -617,7 +638,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
     for (int db = 0; db < 4; ++db) o[db] = Mfma16<T>::run(vop[db], pop, o[db]);
   }
 
-  if (HAS_NEW && !bad) kv_append<T>(a, b, 0, nq, h, split, slot, cs);
+  if (HAS_NEW && !bad) kv_append_store(a, app, 0, h, split, slot, cs);
 
   // row sums: the four lane groups hold different keys of the same query
   l += __shfl_xor(l, 16);
