@@ -527,64 +527,62 @@ __global__ __launch_bounds__(kFThreads, 1) void dense_fwd_kernel(DenseArgs a) {
   float l_part[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // 4 partial row sums
   op_t pcur[2][2];  // [qb][16-key chunk] P of the last softmax
 
-  // Online softmax of step s on sacc.
-  auto softmax = [&](int s) __attribute__((always_inline)) {
+  // Online softmax of step s for query block qb (on sacc[qb]).
+  auto softmax = [&](int qb, int s) __attribute__((always_inline)) {
     const int k0 = s * kBS;
     if (k0 + kBS > a.Lk) {
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-        for (int x = 0; x < 16; ++x)
-          if (k0 + 16 * (x >> 3) + 8 * hl + (x & 7) >= a.Lk) sacc[qb][x] = -INFINITY;
+      for (int x = 0; x < 16; ++x)
+        if (k0 + 16 * (x >> 3) + 8 * hl + (x & 7) >= a.Lk) sacc[qb][x] = -INFINITY;
     }
-    float mx[2];
-#pragma unroll
-    for (int qb = 0; qb < 2; ++qb) {
-      // a tree of 3-input maxima (depth 3, not a chain of 8)
-      const f32x16& v = sacc[qb];
-      const float t0 = fmaxf(fmaxf(v[0], v[1]), v[2]), t1 = fmaxf(fmaxf(v[3], v[4]), v[5]);
-      const float t2 = fmaxf(fmaxf(v[6], v[7]), v[8]), t3 = fmaxf(fmaxf(v[9], v[10]), v[11]);
-      const float t4 = fmaxf(fmaxf(v[12], v[13]), v[14]);
-      const float m = fmaxf(fmaxf(fmaxf(t0, t1), t2), fmaxf(fmaxf(t3, t4), v[15]));
-      mx[qb] = half_swap_max(m);  // relative to m_run
-    }
+    // a tree of 3-input maxima (depth 3, not a chain of 8), then across the lane halves
+    const f32x16& v = sacc[qb];
+    const float t0 = fmaxf(fmaxf(v[0], v[1]), v[2]), t1 = fmaxf(fmaxf(v[3], v[4]), v[5]);
+    const float t2 = fmaxf(fmaxf(v[6], v[7]), v[8]), t3 = fmaxf(fmaxf(v[9], v[10]), v[11]);
+    const float t4 = fmaxf(fmaxf(v[12], v[13]), v[14]);
+    const float mx = half_swap_max(fmaxf(fmaxf(fmaxf(t0, t1), t2), fmaxf(fmaxf(t3, t4), v[15])));  // relative to m_run
     // First step: adopt the max. Later: move the max only when it grew by more than kTau.
-    if (__any(s == 0 || mx[0] > kTau || mx[1] > kTau)) {
+    if (__any(s == 0 || mx > kTau)) {
       asm volatile("" ::: "memory");  // keep this rare path a branch
+      const float delta = s == 0 ? mx : fmaxf(mx, 0.f);
+      m_run[qb] += delta;
+      if (s != 0) {
+        const float alpha = fast_exp2(-delta);
 #pragma unroll
-      for (int qb = 0; qb < 2; ++qb) {
-        const float delta = s == 0 ? mx[qb] : fmaxf(mx[qb], 0.f);
-        m_run[qb] += delta;
-        if (s != 0) {
-          const float alpha = fast_exp2(-delta);
+        for (int j = 0; j < 4; ++j) l_part[qb][j] *= alpha;
 #pragma unroll
-          for (int j = 0; j < 4; ++j) l_part[qb][j] *= alpha;
+        for (int db = 0; db < 2; ++db)
 #pragma unroll
-          for (int db = 0; db < 2; ++db)
+          for (int x = 0; x < 16; ++x) acc_o[db][qb][x] *= alpha;
+      }
 #pragma unroll
-            for (int x = 0; x < 16; ++x) acc_o[db][qb][x] *= alpha;
-        }
-#pragma unroll
-        for (int x = 0; x < 16; ++x) {
-          sacc[qb][x] -= delta;
-          cinit[qb][x] = -m_run[qb];
-        }
+      for (int x = 0; x < 16; ++x) {
+        sacc[qb][x] -= delta;
+        cinit[qb][x] = -m_run[qb];
       }
     }
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
+    for (int ch = 0; ch < 2; ++ch) {
+      u32x4 w;
 #pragma unroll
-      for (int ch = 0; ch < 2; ++ch) {
-        u32x4 w;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float p0 = fast_exp2(sacc[qb][ch * 8 + 2 * e]);
-          const float p1 = fast_exp2(sacc[qb][ch * 8 + 2 * e + 1]);
-          w[e] = Mfma<T>::pack(p0, p1);
-          l_part[qb][e] = l_part[qb][e] + p0 + p1;
-        }
-        pcur[qb][ch] = __builtin_bit_cast(op_t, w);
+      for (int e = 0; e < 4; ++e) {
+        const float p0 = fast_exp2(sacc[qb][ch * 8 + 2 * e]);
+        const float p1 = fast_exp2(sacc[qb][ch * 8 + 2 * e + 1]);
+        w[e] = Mfma<T>::pack(p0, p1);
+        l_part[qb][e] = l_part[qb][e] + p0 + p1;
       }
+      pcur[qb][ch] = __builtin_bit_cast(op_t, w);
+    }
+  };
+  auto mfma_s = [&](int qb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) sacc[qb] = Mfma<T>::run(kop[ks], qreg[qb][ks], ks == 0 ? cinit[qb] : sacc[qb]);
+  };
+  auto mfma_pv = [&](int qb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+      for (int db = 0; db < 2; ++db) acc_o[db][qb] = Mfma<T>::run(vop[ch][db], pcur[qb][ch], acc_o[db][qb]);
   };
 
   // ---- first tiles (tile 0's loads were issued with Q) ----
@@ -596,32 +594,31 @@ __global__ __launch_bounds__(kFThreads, 1) void dense_fwd_kernel(DenseArgs a) {
   __syncthreads();
   read_k(0);
 
+  // Step s, software-pipelined over the two query blocks so that each softmax has MFMAs of the
+  // same wavefront to run under: [S(s) of block 0, PV(s-1) of block 1] [softmax(s) of block 0]
+  // [S(s) of block 1, PV(s) of block 0] [softmax(s) of block 1]. Block 1's PV therefore lags
+  // one step and runs on the V operands of step s-1, which are replaced only after it.
   for (int s = 0; s <= n_sub; ++s) {
     const int t = s >> 1;
     if (!(s & 1) && t + 2 < n_tiles) gload(t + 2);
-    // ---- MFMAs: PV of step s-1, then S of step s ----
+    const bool has_s = s < n_sub;
     mfma_priority<1>();
-    if (s >= 1) {
-#pragma unroll
-      for (int ch = 0; ch < 2; ++ch)
-#pragma unroll
-        for (int db = 0; db < 2; ++db)
-#pragma unroll
-          for (int qb = 0; qb < 2; ++qb) acc_o[db][qb] = Mfma<T>::run(vop[ch][db], pcur[qb][ch], acc_o[db][qb]);
-    }
-    if (s < n_sub) {
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks)
-#pragma unroll
-        for (int qb = 0; qb < 2; ++qb) sacc[qb] = Mfma<T>::run(kop[ks], qreg[qb][ks], ks == 0 ? cinit[qb] : sacc[qb]);
+    if (has_s) mfma_s(0);
+    if (s >= 1) mfma_pv(1);
+    mfma_priority<0>();
+    __builtin_amdgcn_sched_barrier(0);
+    if (has_s) read_v(s);
+    if (has_s) softmax(0, s);
+    __builtin_amdgcn_sched_barrier(0);
+    mfma_priority<1>();
+    if (has_s) {
+      mfma_s(1);
+      mfma_pv(0);
     }
     mfma_priority<0>();
     __builtin_amdgcn_sched_barrier(0);
-    // operands of the next step: V of this one, K of the next
-    if (s < n_sub) read_v(s);
     if (s + 1 < n_sub) read_k(s + 1);
-    // ---- VALU ----
-    if (s < n_sub) softmax(s);
+    if (has_s) softmax(1, s);
     // Tile t+2 replaces tile t-2, whose last reads (V of step 2t-3) came before the previous
     // tile's barrier; its first reads (K of step 2t+4, read in step 2t+3) come after this one.
     if (s & 1) {
