@@ -122,6 +122,41 @@ int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, co
                       const int64_t* o_strides, float softmax_scale, int causal, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/*
+ * Workspace (bytes) that wdrz_dtw_prep needs: one (max, 1/sum) pair per score row and one
+ * (mean, 1/std) pair per score column, 8 * B*H*(T + A) bytes plus alignment.
+ * No counterpart in the reference: torch allocates the intermediates of _dtw_prep_batch itself.
+ */
+size_t wdrz_dtw_prep_workspace_size(int64_t B, int64_t H, int64_t T, int64_t A);
+
+/*
+ * DTW alignment prep of the cross-attention scores.
+ *
+ * Replaces: _dtw_prep_batch(full_weights, actual_lens, audio_caps, medfilt_width)
+ *           (src/whisperdrz/dtw_align.py:700-753) up to its device->host copy, with the median
+ *           filter it calls (median_filter, dtw_align.py:156-167: the Triton kernel at
+ *           dtw_align.py:87-155 on GPU, the sort-based filter at dtw_align.py:65-78 elsewhere).
+ *
+ * weights:     fp32 [B, H, T, A] raw Q K^T of the H alignment heads (CrossAttnCapture.
+ *              compute_attention, dtw_align.py:553-586), strides w_strides[4] in elements,
+ *              last one 1 (rows that start 16-byte aligned are read with 16-byte loads).
+ * actual_lens: int32 [B] valid text rows per batch row (the column statistics use rows
+ *              t < actual_lens[b] and divide by actual_lens[b]; every row is normalised).
+ * audio_caps:  int32 [B] valid audio columns per batch row (columns >= cap get softmax 0).
+ * out:         fp32 [B, T, C], strides out_strides[3] (last one 1). C must be
+ *              min(max(audio_caps), A) — the reference's slice [:, :, :max_audio_cap] — as the
+ *              library does not read the device-side caps on the host.
+ * medfilt_width: 1 (no filter) or odd <= 15; reflect padding; skipped when A <= width / 2.
+ * workspace:   device buffer of wdrz_dtw_prep_workspace_size(B, H, T, A) bytes, 256-byte aligned;
+ *              no state is kept in it between calls.
+ * T <= 512 (Whisper's text context is 448). A batch row with actual_lens[b] == 0 or
+ * audio_caps[b] == 0 gives NaN everywhere, as the reference's 0/0 does. Inputs must be finite.
+ */
+int wdrz_dtw_prep(const float* weights, const int64_t* w_strides, const int32_t* actual_lens,
+                  const int32_t* audio_caps, float* out, const int64_t* out_strides, int64_t B,
+                  int64_t H, int64_t T, int64_t A, int64_t C, int medfilt_width, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -118,3 +118,44 @@ def call_kv(lib, **over):
 def test_kvcache_rejects_bad_arguments(lib, over, code, msg):
     assert call_kv(lib, **over) == code
     assert msg in lib.wdrz_last_error().decode()
+
+
+def call_dtw(lib, **over):
+    args = dict(w=FAKE, ws_=_strides(4 * 16 * 64, 16 * 64, 64, 1), lens=FAKE, caps=FAKE, out=FAKE,
+                os_=(ctypes.c_int64 * 3)(16 * 60, 60, 1), B=1, H=4, T=16, A=64, C=60, width=7, work=None,
+                work_bytes=0)
+    args.update(over)
+    return lib.wdrz_dtw_prep(args["w"], args["ws_"], args["lens"], args["caps"], args["out"], args["os_"], args["B"],
+                             args["H"], args["T"], args["A"], args["C"], args["width"], args["work"],
+                             args["work_bytes"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(width=4), 1, "must be 1 or odd"),
+    (dict(width=0), 1, "must be 1 or odd"),
+    (dict(width=17), 2, "exceeds the supported 15"),
+    (dict(T=513), 2, "exceed the supported 512"),
+    (dict(C=65), 1, "exceeds A"),
+    (dict(H=0), 1, "bad sizes"),
+    (dict(w=None), 1, "weights is NULL"),
+    (dict(ws_=_strides(4 * 16 * 64, 16 * 64, 64, 2)), 1, "last stride"),
+    (dict(lens=None), 1, "actual_lens"),
+    (dict(), 4, "workspace"),
+    (dict(work=FAKE + 16, work_bytes=1 << 20), 1, "256-byte aligned"),
+])
+def test_dtw_prep_rejects_bad_arguments(lib, over, code, msg):
+    assert call_dtw(lib, **over) == code
+    assert msg in lib.wdrz_last_error().decode()
+
+
+def test_dtw_prep_empty_is_a_no_op(lib):
+    assert call_dtw(lib, B=0) == 0
+    assert call_dtw(lib, C=0) == 0
+    assert call_dtw(lib, T=0) == 0
+
+
+def test_dtw_workspace_size(lib):
+    B, H, T, A = 16, 10, 448, 1500
+    n = lib.wdrz_dtw_prep_workspace_size(B, H, T, A)
+    assert 8 * B * H * (T + A) <= n <= 8 * B * H * (T + A) + 256
+    assert lib.wdrz_dtw_prep_workspace_size(0, H, T, A) == 0

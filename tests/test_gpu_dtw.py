@@ -1,0 +1,118 @@
+"""GPU parity of the DTW alignment prep (wdrz_dtw_prep via whisperdrz_amd.dtw) against the
+float64 oracle restating _dtw_prep_batch (src/whisperdrz/dtw_align.py:700-753).
+
+Tolerance: fp32 contract, max |diff| <= 1e-5 * max |ref| over the finite entries; NaN exactly
+where the reference has NaN (a batch row with cap 0 or length 0). The full bench shape is
+checked against the reference's own op sequence run with torch fp32 ops on the GPU.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle.dtw_oracle import dtw_prep_ref, dtw_prep_torch
+
+pytestmark = pytest.mark.gpu
+
+TOL_REL = 1e-5
+
+
+def _scores(shape, seed, scale=2.5):
+    g = torch.Generator().manual_seed(seed)
+    return scale * torch.randn(*shape, generator=g, dtype=torch.float32)
+
+
+def _check(got: torch.Tensor, ref: np.ndarray, what: str):
+    got = got.detach().cpu().numpy().astype(np.float64)
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    nan_ref = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan_ref), f"{what}: NaN pattern differs"
+    fin = ~nan_ref
+    if fin.any():
+        err = float(np.max(np.abs(got[fin] - ref[fin])))
+        bound = TOL_REL * float(np.max(np.abs(ref[fin])))
+        assert err <= bound, f"{what}: max|diff|={err:.3e} > {bound:.3e}"
+
+
+def _run(cuda, w, lens, caps, width, what):
+    from whisperdrz_amd import dtw_prep
+
+    print(what, flush=True)
+    out = dtw_prep(w.to(cuda), lens, caps, width)
+    torch.cuda.synchronize()
+    _check(out, dtw_prep_ref(w.numpy(), lens, caps, width), what)
+    return out
+
+
+@pytest.mark.parametrize("width", [1, 3, 5, 7, 9, 15])
+def test_widths(cuda, width):
+    B, H, T, A = 3, 4, 37, 203
+    w = _scores((B, H, T, A), 10 + width)
+    _run(cuda, w, [37, 20, 5], [203, 150, 61], width, f"dtw width={width}")
+
+
+@pytest.mark.parametrize("B,H,T,A,lens,caps", [
+    (1, 1, 1, 5, [1], [5]),                    # single row, narrow
+    (2, 10, 64, 1500, [64, 33], [1500, 1499]),  # whole window, cap just short of A
+    (2, 3, 130, 257, [200, 130], [257, 3]),     # length beyond T (divides by the length), cap 3
+    (3, 2, 17, 130, [17, 9, 12], [130, 127, 66]),
+    (2, 2, 448, 96, [448, 300], [96, 50]),      # the full text context
+])
+def test_shapes(cuda, B, H, T, A, lens, caps):
+    w = _scores((B, H, T, A), B * 1000 + T + A)
+    _run(cuda, w, lens, caps, 7, f"dtw B={B} H={H} T={T} A={A} lens={lens} caps={caps}")
+
+
+def test_degenerate_rows_are_nan(cuda):
+    w = _scores((3, 2, 9, 40), 5)
+    out = _run(cuda, w, [9, 0, 5], [40, 30, 0], 7, "dtw degenerate cap/len")
+    assert torch.isnan(out[1]).all() and torch.isnan(out[2]).all()
+
+
+def test_short_audio_axis_skips_filter(cuda):
+    # T_audio <= width // 2: the reference returns the input of the filter unchanged
+    w = _scores((2, 3, 6, 3), 6)
+    _run(cuda, w, [6, 4], [3, 2], 7, "dtw A=3 width=7")
+
+
+def test_strided_scores(cuda):
+    # a view whose rows are longer than T_audio (strides stay multiples of 4 elements)
+    base = _scores((2, 3, 21, 72), 7)
+    w = base[:, :, :, :65]
+    from whisperdrz_amd import dtw_prep
+
+    print("dtw strided view", flush=True)
+    out = dtw_prep(base.to(cuda)[:, :, :, :65], [21, 10], [65, 40], 7)
+    torch.cuda.synchronize()
+    _check(out, dtw_prep_ref(w.numpy(), [21, 10], [65, 40], 7), "dtw strided view")
+
+
+def test_batch_returns_host_array_and_is_deterministic(cuda):
+    from whisperdrz_amd import dtw_prep, dtw_prep_batch
+
+    w = _scores((4, 10, 100, 1500), 8).to(cuda)
+    lens, caps = [100, 80, 60, 99], [1500, 1200, 700, 1499]
+    print("dtw batch host copy", flush=True)
+    a = dtw_prep(w, lens, caps).cpu().numpy()
+    b = dtw_prep_batch(w, lens, caps)
+    assert isinstance(b, np.ndarray) and b.shape == (4, 100, 1500) and b.dtype == np.float32
+    np.testing.assert_array_equal(a, b)
+
+
+def test_bench_shape_matches_torch_ops(cuda):
+    # The bench workload (16 chunks x 10 alignment heads x 448 text rows x 1500 audio columns)
+    # against the reference's op sequence in torch fp32 on the same GPU.
+    from whisperdrz_amd import dtw_prep
+
+    B, H, T, A = 16, 10, 448, 1500
+    g = torch.Generator(device=cuda).manual_seed(11)
+    w = 2.5 * torch.randn((B, H, T, A), generator=g, device=cuda)
+    rng = np.random.default_rng(11)
+    lens = [int(x) for x in rng.integers(T // 2, T + 1, B)]
+    caps = [int(x) for x in rng.integers(A // 2, A + 1, B)]
+    caps[0] = A
+    print("dtw bench shape vs torch ops", flush=True)
+    out = dtw_prep(w, lens, caps)
+    ref = dtw_prep_torch(w, lens, caps)  # torch ops on the GPU tensor (fp32)
+    torch.cuda.synchronize()
+    err = (out - ref).abs().max().item()
+    assert err <= 1e-4 * ref.abs().max().item(), err

@@ -2,7 +2,8 @@
 
 Drop-in entry points for the reference's two attention seams (src/whisperdrz/model.py:88-95 and
 model.py:288-296), backed by hand-written HIP kernels in libwdrz_attn.so, plus the slot KV cache
-(model.py:98-192) and the decode-step plumbing around them.
+(model.py:98-192), the decode-step plumbing around them, and the DTW alignment prep
+(dtw_align.py:700-753).
 """
 from . import _lib
 from .attention import (
@@ -12,11 +13,15 @@ from .attention import (
     qkv_attention,
     scaled_dot_product_attention,
 )
+from .dtw import dtw_prep, dtw_prep_batch, dtw_prep_workspace_size
 
 HAS_WDRZ = _lib.available()
 
 __all__ = [
     "HAS_WDRZ",
+    "dtw_prep",
+    "dtw_prep_batch",
+    "dtw_prep_workspace_size",
     "WorkspaceCache",
     "flash_attn_with_kvcache",
     "kvcache_workspace_size",

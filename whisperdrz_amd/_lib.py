@@ -21,6 +21,8 @@ EXPORTED_SYMBOLS = (
     "wdrz_attn_fwd",
     "wdrz_attn_kvcache_workspace_size",
     "wdrz_attn_kvcache",
+    "wdrz_dtw_prep_workspace_size",
+    "wdrz_dtw_prep",
 )
 ABI_VERSION = 1
 
@@ -55,6 +57,14 @@ def _declare(lib: ctypes.CDLL) -> None:
         _i64, _i64, _i64, _i64, _i64, _i64,  # B, sq, H, D, n_slots, Lmax
         _i64p, _i64p, _i64p, _i64p, _i64p, _i64p,  # strides
         ctypes.c_float, ctypes.c_int,  # softmax_scale, causal
+        _p, ctypes.c_size_t, _p,  # workspace, bytes, stream
+    ]
+    lib.wdrz_dtw_prep_workspace_size.restype = ctypes.c_size_t
+    lib.wdrz_dtw_prep_workspace_size.argtypes = [_i64, _i64, _i64, _i64]
+    lib.wdrz_dtw_prep.restype = ctypes.c_int
+    lib.wdrz_dtw_prep.argtypes = [
+        _p, _i64p, _i32p, _i32p, _p, _i64p,  # weights, strides, lens, caps, out, out strides
+        _i64, _i64, _i64, _i64, _i64, ctypes.c_int,  # B, H, T, A, C, medfilt_width
         _p, ctypes.c_size_t, _p,  # workspace, bytes, stream
     ]
 

@@ -18,7 +18,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libwdrz_attn.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["attn_kvcache.hip", "attn_dense.hip", "wdrz_capi.cpp"]
+SOURCES = ["attn_kvcache.hip", "attn_dense.hip", "dtw_prep.hip", "wdrz_capi.cpp"]
 ARCH = "gfx950"
 
 
@@ -47,7 +47,11 @@ def build_library(debug: bool = False, verbose: bool = False) -> Path:
     device_flags = ["-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops"]
     # Per-file device flags. The kernels assume no NaN inputs (masking uses -inf): without
     # this, every fmaxf on a computed score pays an extra canonicalising max.
-    per_file = {"attn_dense.hip": ["-fno-honor-nans"], "attn_kvcache.hip": ["-fno-honor-nans"]}
+    per_file = {
+        "attn_dense.hip": ["-fno-honor-nans"],
+        "attn_kvcache.hip": ["-fno-honor-nans"],
+        "dtw_prep.hip": ["-fno-honor-nans"],  # NaN outputs are written explicitly, never computed
+    }
     objs = []
     for src in SOURCES:
         obj = out_dir / (src + ".o")

@@ -224,4 +224,61 @@ int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, co
   return WDRZ_OK;
 }
 
+size_t wdrz_dtw_prep_workspace_size(int64_t B, int64_t H, int64_t T, int64_t A) {
+  if (B <= 0 || H <= 0 || T <= 0 || A <= 0) return 0;
+  return wdrz::dtw_workspace_bytes(B, H, T, A);
+}
+
+int wdrz_dtw_prep(const float* weights, const int64_t* w_strides, const int32_t* actual_lens,
+                  const int32_t* audio_caps, float* out, const int64_t* out_strides, int64_t B, int64_t H,
+                  int64_t T, int64_t A, int64_t C, int medfilt_width, void* workspace, size_t workspace_bytes,
+                  void* stream) {
+  g_last_error.clear();
+  if (B < 0 || H <= 0 || T < 0 || A <= 0 || C < 0)
+    return fail(WDRZ_EINVAL, "bad sizes B=%lld H=%lld T=%lld A=%lld C=%lld", (long long)B, (long long)H,
+                (long long)T, (long long)A, (long long)C);
+  if (C > A) return fail(WDRZ_EINVAL, "C=%lld exceeds A=%lld", (long long)C, (long long)A);
+  if (T > wdrz::kDtwMaxRows)
+    return fail(WDRZ_EUNSUPPORTED, "T=%lld text rows exceed the supported %d", (long long)T, wdrz::kDtwMaxRows);
+  if (B > 65535 || H > 65535 || A > (1 << 24) || B * H * T > (int64_t(1) << 31))
+    return fail(WDRZ_EUNSUPPORTED, "sizes too large");
+  if (medfilt_width < 1 || (medfilt_width > 1 && medfilt_width % 2 == 0))
+    return fail(WDRZ_EINVAL, "medfilt_width=%d must be 1 or odd", medfilt_width);
+  if (medfilt_width / 2 > wdrz::kDtwMaxPad)
+    return fail(WDRZ_EUNSUPPORTED, "medfilt_width=%d exceeds the supported %d", medfilt_width,
+                2 * wdrz::kDtwMaxPad + 1);
+  if (!weights) return fail(WDRZ_EINVAL, "weights is NULL");
+  if (!out) return fail(WDRZ_EINVAL, "out is NULL");
+  if (!actual_lens || !audio_caps) return fail(WDRZ_EINVAL, "actual_lens / audio_caps is NULL");
+  if (!w_strides || !out_strides) return fail(WDRZ_EINVAL, "strides pointer is NULL");
+  if (w_strides[3] != 1) return fail(WDRZ_EINVAL, "weights: last stride must be 1");
+  if (out_strides[2] != 1) return fail(WDRZ_EINVAL, "out: last stride must be 1");
+  if (B == 0 || T == 0 || C == 0) return WDRZ_OK;
+  const size_t need = wdrz::dtw_workspace_bytes(B, H, T, A);
+  if (!workspace || workspace_bytes < need)
+    return fail(WDRZ_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace ? workspace_bytes : 0);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+    return fail(WDRZ_EINVAL, "workspace is not 256-byte aligned");
+
+  wdrz::DtwArgs a{};
+  a.w = weights;
+  a.lens = actual_lens;
+  a.caps = audio_caps;
+  a.out = out;
+  a.B = (int)B;
+  a.H = (int)H;
+  a.T = (int)T;
+  a.A = (int)A;
+  a.C = (int)C;
+  const int pad = medfilt_width / 2;
+  a.pad = (medfilt_width > 1 && A > pad) ? pad : 0;  // dtw_align.py:68-69: too short -> unfiltered
+  for (int i = 0; i < 3; ++i) a.ws[i] = w_strides[i];
+  a.os[0] = out_strides[0];
+  a.os[1] = out_strides[1];
+  wdrz::dtw_workspace_layout(workspace, &a);
+  hipError_t err = wdrz::launch_dtw_prep(a, reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(WDRZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  return WDRZ_OK;
+}
+
 }  // extern "C"

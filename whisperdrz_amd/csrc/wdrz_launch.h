@@ -51,4 +51,22 @@ struct DenseArgs {
 };
 hipError_t launch_dense_mfma(int dtype, const DenseArgs& a, hipStream_t stream);
 
+// DTW alignment prep over fp32 scores W [B, H, T, A] (strides in ELEMENTS, last one 1).
+constexpr int kDtwMaxRows = 512;  // T limit (Whisper's text context is 448)
+constexpr int kDtwMaxPad = 7;     // median width <= 15
+struct DtwArgs {
+  const float* w;
+  const int32_t* lens;  // [B] valid text rows
+  const int32_t* caps;  // [B] valid audio columns
+  float* out;           // [B, T, C]
+  float2* rs;           // workspace: per-row (max*log2e, 1/sum)
+  float2* cs;           // workspace: per-column (mean, 1/std)
+  int B, H, T, A, C, pad;
+  int64_t ws[3];  // W strides b, h, t
+  int64_t os[2];  // out strides b, t
+};
+size_t dtw_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A);
+void dtw_workspace_layout(void* ws, DtwArgs* a);
+hipError_t launch_dtw_prep(const DtwArgs& a, hipStream_t stream);
+
 }  // namespace wdrz

@@ -1,0 +1,112 @@
+"""DTW alignment prep on the GPU, backed by the gfx950 kernels in libwdrz_attn.so.
+
+Mirrors the reference's batched prep ``_dtw_prep_batch(full_weights, actual_lens, audio_caps,
+medfilt_width=7)`` (``src/whisperdrz/dtw_align.py:700-753``): capped row softmax, column
+mean/std normalisation over each chunk's valid text rows, width-``medfilt_width`` median filter
+along the audio axis (reflect padding), mean over the alignment heads, slice to the largest cap,
+one device->host copy into a reused pinned buffer.
+
+There is no CPU fallback: CPU tensors and a missing library raise.
+"""
+from __future__ import annotations
+
+from typing import Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+from .attention import WorkspaceCache, _check_cuda, _raise, _stream_handle
+
+__all__ = ["dtw_prep", "dtw_prep_batch", "dtw_prep_workspace_size"]
+
+# The prep's workspace holds no state between calls; it is kept apart from the split-KV
+# workspace, whose counters must stay zero.
+_DTW_WORKSPACES = WorkspaceCache()
+_PINNED: dict[tuple, torch.Tensor] = {}
+
+
+def dtw_prep_workspace_size(B: int, H: int, T: int, A: int) -> int:
+    """Bytes of device workspace :func:`dtw_prep` needs for a [B, H, T, A] score tensor."""
+    return int(_lib.load().wdrz_dtw_prep_workspace_size(B, H, T, A))
+
+
+def _kernel_ready(w: torch.Tensor) -> torch.Tensor:
+    """The kernels need unit stride along the audio axis (compute_attention's output has it)."""
+    return w if w.stride(-1) == 1 else w.contiguous()
+
+
+def dtw_prep(
+    full_weights: torch.Tensor,
+    actual_lens: Sequence[int],
+    audio_caps: Sequence[int],
+    medfilt_width: int = 7,
+) -> torch.Tensor:
+    """The prep of ``_dtw_prep_batch`` without the host copy: returns the device tensor
+    ``[B, T_text_pad, max_audio_cap]`` (fp32).
+
+    full_weights: fp32 ``[B, H, T_text_pad, T_audio]`` on the GPU (raw Q K^T of the alignment
+    heads). ``actual_lens[b]`` rows enter the column statistics; columns ``>= audio_caps[b]``
+    are masked out of the softmax (dtw_align.py:720-738).
+    """
+    w = full_weights
+    if not isinstance(w, torch.Tensor):
+        raise TypeError("full_weights must be a torch.Tensor")
+    if w.dim() != 4:
+        raise ValueError(f"full_weights must be [B, H, T_text, T_audio], got shape {tuple(w.shape)}")
+    if w.dtype != torch.float32:
+        raise TypeError(f"full_weights: dtype {w.dtype} is not supported (float32, as compute_attention gives)")
+    device = w.device
+    _check_cuda("full_weights", w, device)
+    B, H, T, A = (int(x) for x in w.shape)
+    lens = [int(x) for x in actual_lens]
+    caps = [int(x) for x in audio_caps]
+    if len(lens) != B or len(caps) != B:
+        raise ValueError(f"actual_lens / audio_caps must have {B} entries")
+    if B == 0:
+        raise ValueError("empty batch (the reference's max() over no caps raises too)")
+    # matrix[:, :, :max_audio_cap] (dtw_align.py:746), with Python's slice semantics.
+    C = len(range(A)[: max(caps)])
+    out = torch.empty((B, T, C), dtype=torch.float32, device=device)
+    if T == 0 or C == 0:
+        return out
+    w = _kernel_ready(w)
+    lens_t = torch.tensor(lens, dtype=torch.int32, device=device)
+    caps_t = torch.tensor(caps, dtype=torch.int32, device=device)
+    lib = _lib.load()
+    nbytes = dtw_prep_workspace_size(B, H, T, A)
+    ws = _DTW_WORKSPACES.get(device, nbytes)
+    ws_ptr = ws.data_ptr() if ws is not None else None
+    rc = lib.wdrz_dtw_prep(
+        w.data_ptr(), _lib.strides4(w.stride()), lens_t.data_ptr(), caps_t.data_ptr(),
+        out.data_ptr(), (_lib.ctypes.c_int64 * 3)(*out.stride()),
+        B, H, T, A, C, int(medfilt_width), ws_ptr, ws.numel() if ws is not None else 0,
+        _stream_handle(),
+    )
+    if rc != _lib.WDRZ_OK:
+        _raise(rc, "dtw_prep")
+    return out
+
+
+def dtw_prep_batch(
+    full_weights: torch.Tensor,
+    actual_lens: Sequence[int],
+    audio_caps: Sequence[int],
+    medfilt_width: int = 7,
+) -> np.ndarray:
+    """Drop-in for ``_dtw_prep_batch`` (dtw_align.py:700-753): the prep on the GPU, then ONE
+    device->host copy into a pinned buffer reused per shape. As in the reference, the returned
+    array shares that buffer, so it is overwritten by the next call of the same shape."""
+    matrix = dtw_prep(full_weights, actual_lens, audio_caps, medfilt_width)
+    key = (tuple(matrix.shape), matrix.dtype)
+    host = _PINNED.get(key)
+    if host is None:
+        host = torch.empty(matrix.shape, dtype=matrix.dtype, pin_memory=True)
+        _PINNED[key] = host
+    host.copy_(matrix, non_blocking=True)
+    torch.cuda.synchronize(matrix.device)
+    return host.numpy()
+
+
+# The reference's private name, for a one-line swap at dtw_align.py:1197.
+_dtw_prep_batch = dtw_prep_batch
