@@ -8,9 +8,11 @@ algorithmic work (4*B*H*L^2*D per layer) and as a fraction of the bf16 dense MFM
 The same line carries, under ``decode``, the decoder paths (configs 3, 4, 5) in GB/s of
 algorithmic HBM bytes (only valid K/V rows are counted), each with 32 distinct per-layer caches
 captured into one hipGraph and replayed, and under ``cpu_baseline`` the reference's CPU torch
-path (torch SDPA, fp32) timed on this host's cores on a bounded sample.
+path (torch SDPA, fp32) timed on this host's cores on a bounded sample. Under ``dtw_prep`` it
+carries the DTW alignment prep (_dtw_prep_batch) in GB/s of algorithmic HBM bytes, with its own
+roofline and CPU baseline.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only enc|dec]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only enc|dec|dtw]
 """
 from __future__ import annotations
 
@@ -260,6 +262,110 @@ def bench_decode(dev, steps: int, warmup: int) -> dict:
 # --------------------------------------------------------------------------------------------
 
 
+# --------------------------------------------------------------------------------------------
+# DTW alignment prep (_dtw_prep_batch, dtw_align.py:700-753)
+# --------------------------------------------------------------------------------------------
+
+DTW_B, DTW_H, DTW_T, DTW_A = 16, 10, 448, 1500  # chunks x large-v3 alignment heads x text x audio
+
+
+def _dtw_inputs(dev, seed):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    w = 2.5 * torch.randn((DTW_B, DTW_H, DTW_T, DTW_A), generator=g, device=dev)
+    rng = np.random.default_rng(seed)
+    lens = [int(x) for x in rng.integers(DTW_T // 2, DTW_T + 1, DTW_B)]
+    return w, lens, [DTW_A] * DTW_B
+
+
+def dtw_bytes(lens, caps) -> int:
+    """Algorithmic HBM bytes of one prep: every valid score read once (4 B per column < cap of
+    every row of every head) and the [B, T, max cap] result written once."""
+    read = sum(4 * DTW_H * DTW_T * c for c in caps)
+    return read + 4 * DTW_B * DTW_T * max(caps)
+
+
+def bench_dtw(dev, steps: int, warmup: int) -> dict:
+    from whisperdrz_amd import dtw_prep
+    from oracle.dtw_oracle import dtw_prep_torch
+
+    n_in = 4
+    log(f"[bench] dtw prep: {n_in} distinct score tensors [{DTW_B}, {DTW_H}, {DTW_T}, {DTW_A}] fp32")
+    inputs = [_dtw_inputs(dev, 5000 + i) for i in range(n_in)]
+    outs = [None] * n_in
+
+    def step():
+        for i, (w, lens, caps) in enumerate(inputs):
+            outs[i] = dtw_prep(w, lens, caps, 7)
+
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        step()
+    ms = timed_events(step, steps, stream) / n_in
+    nbytes = dtw_bytes(inputs[0][1], inputs[0][2])
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"[bench] dtw prep: {ms * 1e3:.1f} us per prep, {gbs:.0f} GB/s algorithmic ({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM)")
+    # The reference's op sequence (torch ops; sort-based median in place of its Triton kernel)
+    # on the same GPU, for comparison.
+    w, lens, caps = inputs[0]
+    dtw_prep_torch(w, lens, caps)
+    ms_torch = timed_events(lambda: dtw_prep_torch(w, lens, caps), 3, stream)
+    log(f"[bench] dtw prep: torch op sequence on the GPU {ms_torch * 1e3:.0f} us ({ms_torch / ms:.1f}x)")
+    del inputs, outs
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"_dtw_prep_batch: B={DTW_B} chunks x H={DTW_H} alignment heads x T_text={DTW_T} x "
+        f"T_audio={DTW_A} fp32 scores, caps={DTW_A}, lens ~ U[{DTW_T // 2},{DTW_T}], median width 7; "
+        f"{n_in} distinct inputs in rotation",
+        "us_per_prep": round(ms * 1e3, 2),
+        "GB_per_s": round(gbs, 1),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4),
+            "traffic": (sum(measured_traffic(k) or 0 for k in DTW_KERNELS) or None),
+            "traffic_source": "profiles/pmc_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE passes)",
+            "bytes_per_prep": nbytes,
+            "kernels": list(DTW_KERNELS),
+        },
+        "torch_ops_gpu_us": round(ms_torch * 1e3, 1),
+    }
+
+
+DTW_KERNELS = ("dtw_row_stats_kernel<true>", "dtw_col_stats_kernel", "dtw_filter_kernel<3>")
+
+
+def dtw_cpu_baseline(budget_s: float = 12.0) -> dict:
+    """The reference's op sequence in torch fp32 on the host cores, on one chunk."""
+    from oracle.dtw_oracle import dtw_prep_torch
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(1)
+    w = 2.5 * torch.randn((1, DTW_H, DTW_T, DTW_A), generator=g)
+    lens, caps = [DTW_T - 17], [DTW_A]
+    nbytes = 4 * DTW_H * DTW_T * DTW_A + 4 * DTW_T * DTW_A
+    dtw_prep_torch(w, lens, caps)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 100):
+        t0 = time.perf_counter()
+        dtw_prep_torch(w, lens, caps)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    log(f"[bench] dtw cpu baseline: {med * 1e3:.1f} ms per chunk on {cores} threads -> {nbytes / med / 1e9:.2f} GB/s")
+    return {
+        "value": round(nbytes / med / 1e9, 3),
+        "unit": "GB/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"torch CPU fp32 op sequence of _dtw_prep_batch (dtw_align.py:720-746, sort-based median "
+        f"of dtw_align.py:65-78) on one chunk H={DTW_H} T={DTW_T} A={DTW_A}, median of {len(times)} runs "
+        f"({med * 1e3:.1f} ms each)",
+    }
+
+
 def cpu_baseline(budget_s: float = 12.0) -> dict:
     from oracle.attention_oracle import sdpa_torch
 
@@ -292,8 +398,8 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
 
 def pmc_sample(dev) -> None:
     """A short, fixed kernel sequence for hardware-counter passes (rocprofv3 --pmc):
-    a calibration copy of 1 GiB (known HBM bytes), then 3 launches of the encoder kernel and of
-    each decode kernel at the bench shapes (eager, distinct per-launch inputs)."""
+    a calibration copy of 1 GiB (known HBM bytes), then 3 launches of the encoder kernel, of
+    each decode kernel and of the DTW prep at the bench shapes (eager, distinct inputs)."""
     from whisperdrz_amd import flash_attn_with_kvcache, scaled_dot_product_attention
 
     n = 1 << 30
@@ -329,6 +435,13 @@ def pmc_sample(dev) -> None:
         flash_attn_with_kvcache(q5, kv_x[0], kv_x[1], cache_batch_idx=slots, softmax_scale=0.125)
         torch.cuda.synchronize()
         del kv_s, kv_x
+    from whisperdrz_amd import dtw_prep
+
+    for i in range(3):
+        w, lens, caps = _dtw_inputs(dev, 5000 + i)
+        dtw_prep(w, lens, caps, 7)
+        torch.cuda.synchronize()
+        del w
     log("[bench] pmc sample done")
 
 
@@ -338,7 +451,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["enc", "dec"], default=None)
+    ap.add_argument("--only", choices=["enc", "dec", "dtw"], default=None)
     ap.add_argument("--pmc-sample", action="store_true",
                     help="run the short fixed kernel sequence used for rocprofv3 --pmc passes and exit")
     args = ap.parse_args()
@@ -363,7 +476,10 @@ def main() -> int:
 
     enc = bench_encoder(dev, args.steps, args.warmup) if args.only in (None, "enc") else None
     dec = bench_decode(dev, args.steps, args.warmup) if args.only in (None, "dec") else None
+    dtw = bench_dtw(dev, args.steps, args.warmup) if args.only in (None, "dtw") else None
     cpu = None if args.no_cpu else cpu_baseline()
+    if dtw is not None and not args.no_cpu:
+        dtw["cpu_baseline"] = dtw_cpu_baseline()
 
     line = {
         "metric": METRIC,
@@ -391,6 +507,7 @@ def main() -> int:
         "roofline": enc["roofline"] if enc else None,
         "cpu_baseline": cpu,
         "decode": dec,
+        "dtw_prep": dtw,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -43,11 +43,12 @@ def _run(cuda, w, lens, caps, width, what):
     return out
 
 
+@pytest.mark.parametrize("A", [203, 200])  # rows unaligned (column-strip kernels) / aligned (whole rows)
 @pytest.mark.parametrize("width", [1, 3, 5, 7, 9, 15])
-def test_widths(cuda, width):
-    B, H, T, A = 3, 4, 37, 203
-    w = _scores((B, H, T, A), 10 + width)
-    _run(cuda, w, [37, 20, 5], [203, 150, 61], width, f"dtw width={width}")
+def test_widths(cuda, width, A):
+    B, H, T = 3, 4, 37
+    w = _scores((B, H, T, A), 10 + width + A)
+    _run(cuda, w, [37, 20, 5], [A, 150, 61], width, f"dtw width={width} A={A}")
 
 
 @pytest.mark.parametrize("B,H,T,A,lens,caps", [
@@ -56,6 +57,13 @@ def test_widths(cuda, width):
     (2, 3, 130, 257, [200, 130], [257, 3]),     # length beyond T (divides by the length), cap 3
     (3, 2, 17, 130, [17, 9, 12], [130, 127, 66]),
     (2, 2, 448, 96, [448, 300], [96, 50]),      # the full text context
+    # fused row/column pass (rows 16-byte aligned, A <= 2048): 1, 2 and 3 row chunks of 64,
+    # every register width, a length beyond T
+    (2, 3, 70, 1000, [70, 65], [1000, 999]),
+    (2, 2, 130, 512, [130, 129], [511, 512]),
+    (2, 2, 100, 1500, [150, 100], [1500, 1497]),
+    (1, 2, 64, 2048, [64], [2047]),
+    (1, 2, 20, 2100, [20], [2100]),             # A > 2048: separate row and column passes
 ])
 def test_shapes(cuda, B, H, T, A, lens, caps):
     w = _scores((B, H, T, A), B * 1000 + T + A)

@@ -41,24 +41,39 @@ constexpr int kTileCols = kColBlock + 2 * kHalo;  // 80
 constexpr int kTilePitch = 84;  // floats; staggers rows across LDS banks
 constexpr int kMaxRowsPerLane = kDtwMaxRows / 8;  // col stats: rows held per lane (8 waves)
 
+// Wave-wide reductions without LDS round trips: DPP inside each 16-lane row (lane ^ 1, ^ 2, then
+// the half-row and row mirrors), then the gfx950 row swaps across the four rows.
+__device__ __forceinline__ float swap_max(float x) {
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+}
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v = fmaxf(v, __shfl_xor(v, o));
-  return v;
+  v = fmaxf(v, dpp_xor1(v));
+  v = fmaxf(v, dpp_xor2(v));
+  v = fmaxf(v, dpp_half_mirror(v));
+  v = fmaxf(v, dpp_row_mirror(v));
+  return swap_max(v);
 }
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-  return v;
+  v = group_sum<16>(v);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
 }
 
 // Softmax value of score x in a row with statistics (max*log2e, 1/sum). The column-statistics
 // and filter kernels must compute bit-identical p for one score: a column whose valid rows are
 // all equal has variance 0 and std 1e-6, so any difference would be amplified a million-fold.
 // Contraction is off so the rounded product, not the exact one, meets the later subtraction.
-__device__ __forceinline__ float softmax_value(float x, float2 st) {
+__device__ __forceinline__ float softmax_scale_e(float e, float rl) {
 #pragma clang fp contract(off)
-  return exp2f(__builtin_fmaf(x, kLog2e, -st.x)) * st.y;
+  return e * rl;
+}
+__device__ __forceinline__ float softmax_value(float x, float2 st) {
+  return softmax_scale_e(exp2f(__builtin_fmaf(x, kLog2e, -st.x)), st.y);
 }
 
 __device__ __forceinline__ int clamp_cap(int cap, int A) { return cap < 0 ? 0 : (cap > A ? A : cap); }
@@ -190,13 +205,196 @@ __global__ __launch_bounds__(512) void dtw_col_stats_kernel(DtwArgs a) {
     float2 r;
     r.x = mean;
     r.y = 1.f / sqrtf(v);
-    a.cs[bh * a.A + c] = r;
+    a.cs[bh * a.cpitch + c] = r;
   }
 }
 
 // ---------------------------------------------------------------------------------------------
-// Median selection. Any exact selection returns an element of the window, so the result equals
-// the reference's sort / bubble-network median for finite inputs.
+// Fused row + column statistics (rows 16-byte aligned, A <= 256*NK): one workgroup per
+// (64-row chunk, h, b), 4 waves x 16 rows. A wave holds a whole row in registers (NK 16-byte
+// loads per lane, the next row's loads in flight), reduces its max and sum across the wave,
+// stores the row statistics, and folds the row's softmax values into per-column Welford
+// accumulators (mean, M2) when the row is valid. The 4 waves' accumulators are merged (Chan)
+// through LDS and the chunk's partial (mean, M2) per column is stored for dtw_col_merge_kernel.
+// ---------------------------------------------------------------------------------------------
+constexpr int kRcWaves = 4;
+constexpr int kRcRowsPerWave = 16;
+constexpr int kRcRows = kRcWaves * kRcRowsPerWave;
+
+__device__ __forceinline__ void chan_merge(float na, float& ma, float& qa, float nb, float mb, float qb) {
+  if (nb == 0.f) return;
+  const float n = na + nb;
+  const float d = mb - ma;
+  ma += d * (nb / n);
+  qa += qb + d * d * (na * nb / n);
+}
+
+template <int NK>
+__global__ __launch_bounds__(256) void dtw_rowcol_kernel(DtwArgs a) {
+  const int chunk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int cap = clamp_cap(a.caps[b], a.A);
+  const int len = a.lens[b];
+  if (cap <= 0 || len <= 0) return;  // the filter writes NaN for this batch row
+  const int rows_valid = len < a.T ? len : a.T;
+  const int64_t bh = (int64_t)b * a.H + h;
+  const float* base = a.w + b * a.ws[0] + h * a.ws[1];
+  const int t_first = chunk * kRcRows + wave * kRcRowsPerWave;
+  const int t_end = min(t_first + kRcRowsPerWave, a.T);
+
+  float cm[NK][4], cq[NK][4];
+#pragma unroll
+  for (int j = 0; j < NK; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) cm[j][i] = cq[j][i] = 0.f;
+
+  auto load_row = [&](int t, float (&x)[NK][4]) {
+    const float* src = base + (int64_t)t * a.ws[2];
+#pragma unroll
+    for (int j = 0; j < NK; ++j) {
+      const int col = 4 * (lane + 64 * j);
+      if (col + 4 <= cap) {
+        const f32x4 v = *reinterpret_cast<const f32x4*>(src + col);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[j][i] = v[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[j][i] = col + i < cap ? src[col + i] : -INFINITY;
+      }
+    }
+  };
+
+  float x[NK][4], xn[NK][4];
+  if (t_first < t_end) load_row(t_first, x);
+  int k = 0;  // valid rows folded in by this wave
+  for (int t = t_first; t < t_end; ++t) {
+    if (t + 1 < t_end) load_row(t + 1, xn);
+    // max(x) * log2e == max(x * log2e): the scaling is monotone, rounding included.
+    float mx = -INFINITY;
+#pragma unroll
+    for (int j = 0; j < NK; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) mx = fmaxf(mx, x[j][i]);
+    float2 st;
+    st.x = wave_max(mx) * kLog2e;
+    // e = exp2(x*log2e - m) as softmax_value forms it; kept for the column update (-inf -> 0).
+    float sum = 0.f;
+#pragma unroll
+    for (int j = 0; j < NK; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        x[j][i] = exp2f(__builtin_fmaf(x[j][i], kLog2e, -st.x));
+        sum += x[j][i];
+      }
+    st.y = 1.f / wave_sum(sum);
+    if (lane == 0) a.rs[bh * a.T + t] = st;
+    if (t < rows_valid) {
+      ++k;
+      const float inv = 1.f / (float)k;
+#pragma unroll
+      for (int j = 0; j < NK; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = softmax_scale_e(x[j][i], st.y);
+          const float d = p - cm[j][i];
+          cm[j][i] += d * inv;
+          cq[j][i] += d * (p - cm[j][i]);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < NK; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[j][i] = xn[j][i];
+  }
+
+  // Merge the waves' accumulators: 2+3 into 0+1, then 1 into 0.
+  __shared__ f32x4 red[2][NK * 64][2];  // [wave slot][lane j][mean4 | M2 4]
+  auto wave_rows = [&](int w) {
+    const int lo = chunk * kRcRows + w * kRcRowsPerWave;
+    const int hi = min(lo + kRcRowsPerWave, rows_valid);
+    return (float)(hi > lo ? hi - lo : 0);
+  };
+  float n_self = (float)k;
+#pragma unroll
+  for (int step = 0; step < 2; ++step) {
+    const int half = step == 0 ? 2 : 1;
+    if (wave >= half && wave < 2 * half) {
+#pragma unroll
+      for (int j = 0; j < NK; ++j) {
+        red[wave - half][j * 64 + lane][0] = f32x4{cm[j][0], cm[j][1], cm[j][2], cm[j][3]};
+        red[wave - half][j * 64 + lane][1] = f32x4{cq[j][0], cq[j][1], cq[j][2], cq[j][3]};
+      }
+    }
+    __syncthreads();
+    if (wave < half) {
+      float n_other = wave_rows(wave + half);
+      if (step == 1) n_other += wave_rows(3);  // wave 1 already holds waves 1 and 3
+#pragma unroll
+      for (int j = 0; j < NK; ++j) {
+        const f32x4 om = red[wave][j * 64 + lane][0];
+        const f32x4 oq = red[wave][j * 64 + lane][1];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) chan_merge(n_self, cm[j][i], cq[j][i], n_other, om[i], oq[i]);
+      }
+      n_self += n_other;
+    }
+    __syncthreads();
+  }
+  if (wave == 0 && n_self > 0.f) {
+    const int n_chunks = (a.T + kRcRows - 1) / kRcRows;
+    float2* part = a.part + (bh * n_chunks + chunk) * a.cpitch;
+#pragma unroll
+    for (int j = 0; j < NK; ++j) {
+      const int col = 4 * (lane + 64 * j);
+      if (col < cap) {
+        // (mean, M2) pairs of 4 columns: 32 bytes.
+        f32x4* dst = reinterpret_cast<f32x4*>(part + col);
+        dst[0] = f32x4{cm[j][0], cq[j][0], cm[j][1], cq[j][1]};
+        dst[1] = f32x4{cm[j][2], cq[j][2], cm[j][3], cq[j][3]};
+      }
+    }
+  }
+}
+
+// Final column statistics from the chunk partials: cs = (mean, 1/sqrt(max(var, 1e-12))) with
+// mean and var dividing by lens[b] (which may exceed T: the reference divides by the length,
+// dtw_align.py:731-736). One thread per column; grid (ceil(need / 256), H, B).
+__global__ __launch_bounds__(256) void dtw_col_merge_kernel(DtwArgs a, int need) {
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int c = blockIdx.x * 256 + threadIdx.x;
+  const int cap = clamp_cap(a.caps[b], a.A);
+  const int len = a.lens[b];
+  if (cap <= 0 || len <= 0 || c >= cap || c >= need) return;
+  const int rows_valid = len < a.T ? len : a.T;
+  const int n_chunks = (a.T + kRcRows - 1) / kRcRows;
+  const int64_t bh = (int64_t)b * a.H + h;
+  const float2* part = a.part + bh * n_chunks * a.cpitch + c;
+  float n = 0.f, mean = 0.f, m2 = 0.f;
+  for (int i = 0; i * kRcRows < rows_valid; ++i) {
+    const int rows_i = min(rows_valid - i * kRcRows, kRcRows);
+    const float2 pi = part[(int64_t)i * a.cpitch];
+    chan_merge(n, mean, m2, (float)rows_i, pi.x, pi.y);
+    n += (float)rows_i;
+  }
+  float var;
+  if (len == rows_valid) {
+    var = m2 / (float)len;
+  } else {  // rows beyond T count in the divisor only
+    const float mean_len = mean * (n / (float)len);
+    const float d = mean - mean_len;
+    var = (m2 + n * d * d) / (float)len;
+    mean = mean_len;
+  }
+  var = var < 1e-12f ? 1e-12f : var;
+  float2 r;
+  r.x = mean;
+  r.y = 1.f / sqrtf(var);
+  a.cs[bh * a.cpitch + c] = r;
+}
+
+// ---------------------------------------------------------------------------------------------
+// Median selection. Every routine returns an element of the window, so the result equals the
+// reference's sort / bubble-network median for finite inputs.
 // ---------------------------------------------------------------------------------------------
 __device__ __forceinline__ void cx(float& lo, float& hi) {
   const float a = fminf(lo, hi);
@@ -204,13 +402,29 @@ __device__ __forceinline__ void cx(float& lo, float& hi) {
   lo = a;
 }
 
-// Median of 7 with a 13-exchange selection network (verified on all 128 0-1 inputs).
-__device__ __forceinline__ float median7(float p0, float p1, float p2, float p3, float p4, float p5,
-                                         float p6) {
-  cx(p0, p5); cx(p0, p3); cx(p1, p6); cx(p2, p4); cx(p0, p1); cx(p3, p5);
-  cx(p2, p6); cx(p2, p3); cx(p3, p6); cx(p4, p5); cx(p1, p4);
-  // The last two exchanges (1,3) and (3,4), of which only the middle output is used.
-  return fminf(fmaxf(p1, p3), p4);
+// Medians of the 4 width-7 windows over x[0..9] (window i = x[i..i+6]), 30 min/max operations
+// instead of 4 separate networks. Windows (0,1) share x[1..6] and windows (2,3) share x[3..8];
+// both share x[3..6]. With t = sorted x[3..6] and a <= b the pair's two extra shared values, the
+// 3rd and 4th smallest of the 6 shared values are
+//   s2 = min(t2, max(t1, a), max(t0, b)),  s3 = min(t3, max(t2, a), max(t1, b))
+// (k-th smallest of a merge of two sorted lists), and the median of the shared 6 plus one more
+// value v is med3(s2, v, s3). Checked against a sort on all 1024 0-1 inputs and on random inputs
+// with ties.
+__device__ __forceinline__ void median7_x4(const float (&x)[10], float (&out)[4]) {
+  float t0 = x[3], t1 = x[4], t2 = x[5], t3 = x[6];
+  cx(t0, t1); cx(t2, t3); cx(t0, t2); cx(t1, t3); cx(t1, t2);
+  auto mid = [&](float a, float b, float& s2, float& s3) {
+    cx(a, b);
+    s2 = fminf(fminf(t2, fmaxf(t1, a)), fmaxf(t0, b));
+    s3 = fminf(fminf(t3, fmaxf(t2, a)), fmaxf(t1, b));
+  };
+  float s2, s3;
+  mid(x[1], x[2], s2, s3);
+  out[0] = __builtin_amdgcn_fmed3f(s2, x[0], s3);
+  out[1] = __builtin_amdgcn_fmed3f(s2, x[7], s3);
+  mid(x[7], x[8], s2, s3);
+  out[2] = __builtin_amdgcn_fmed3f(s2, x[2], s3);
+  out[3] = __builtin_amdgcn_fmed3f(s2, x[9], s3);
 }
 
 // Median of W (odd) by partial exchange sort: after W/2 + 1 passes that each carry the largest
@@ -224,30 +438,41 @@ __device__ __forceinline__ float median_generic(float (&v)[W]) {
   return v[W / 2];
 }
 
+// Medians of the 4 windows of width 2*PAD+1 over x[0 .. 3+2*PAD].
 template <int PAD>
-__device__ __forceinline__ float window_median(const float* win) {  // win[0 .. 2*PAD]
+__device__ __forceinline__ void window_medians(const float (&x)[4 + 2 * PAD], float (&out)[4]) {
   if constexpr (PAD == 0) {
-    return win[0];
-  } else if constexpr (PAD == 1) {
-    return __builtin_amdgcn_fmed3f(win[0], win[1], win[2]);
-  } else if constexpr (PAD == 3) {
-    return median7(win[0], win[1], win[2], win[3], win[4], win[5], win[6]);
-  } else {
-    float v[2 * PAD + 1];
 #pragma unroll
-    for (int i = 0; i < 2 * PAD + 1; ++i) v[i] = win[i];
-    return median_generic<2 * PAD + 1>(v);
+    for (int i = 0; i < 4; ++i) out[i] = x[i];
+  } else if constexpr (PAD == 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = __builtin_amdgcn_fmed3f(x[i], x[i + 1], x[i + 2]);
+  } else if constexpr (PAD == 3) {
+    median7_x4(x, out);
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float v[2 * PAD + 1];
+#pragma unroll
+      for (int j = 0; j < 2 * PAD + 1; ++j) v[j] = x[i + j];
+      out[i] = median_generic<2 * PAD + 1>(v);
+    }
   }
 }
 
 // ---------------------------------------------------------------------------------------------
 // Normalise + median filter + head mean. Grid: (ceil(C / 64), ceil(T / 16), B), 256 threads.
-// Load mapping: thread = (column j in [0, 80), row group g in [0, 3)); rows g, g+3, ... < 16.
-// Filter mapping: thread = (row tid/16, output columns 4*(tid%16) .. +3).
+// The LDS tile holds 16 rows x columns [c0 - 8, c0 + 72) of z; only the float4 columns that
+// reach within PAD of the strip are filled. Load mapping: thread = (float4 column lq, row group
+// lg), rows lg, lg + RG. Filter mapping: thread = (row tid/16, output columns 4*(tid%16) .. +3).
 // ---------------------------------------------------------------------------------------------
 template <int PAD>
 __global__ __launch_bounds__(256) void dtw_filter_kernel(DtwArgs a) {
-  constexpr int kLoadRows = (kFiltRows + 2) / 3;  // 6
+  constexpr int kQ0 = (kHalo - PAD) / 4;                   // first float4 column filled
+  constexpr int kQ1 = (kHalo + kColBlock + PAD + 3) / 4;   // one past the last
+  constexpr int NQ = kQ1 - kQ0;
+  constexpr int RG = 256 / NQ;
+  constexpr int RPT = (kFiltRows + RG - 1) / RG;
   const int b = blockIdx.z;
   const int t0 = blockIdx.y * kFiltRows;
   const int c0 = blockIdx.x * kColBlock;
@@ -255,7 +480,7 @@ __global__ __launch_bounds__(256) void dtw_filter_kernel(DtwArgs a) {
   const int cap = clamp_cap(a.caps[b], a.A);
   const int len = a.lens[b];
 
-  const int fr = tid >> 4;       // filter row
+  const int fr = tid >> 4;        // filter row
   const int fq = 4 * (tid & 15);  // first of 4 output columns
   const int ot = t0 + fr;
 
@@ -267,69 +492,133 @@ __global__ __launch_bounds__(256) void dtw_filter_kernel(DtwArgs a) {
     return;
   }
 
-  __shared__ float tile[kFiltRows * kTilePitch];
+  __shared__ f32x4 tile4[kFiltRows * kTilePitch / 4];
   __shared__ float2 rstat[kFiltRows];
+  __shared__ f32x4 cstat[NQ][2];  // column (mean, 1/std) of the tile's float4 columns
+  float* tile = reinterpret_cast<float*>(tile4);
 
-  // Load-side column of this thread (tid < 240).
-  const int lj = tid % kTileCols;
-  const int lg = tid / kTileCols;  // 0..2 (3 for the 16 idle threads)
-  int g = c0 - kHalo + lj;         // unreflected column
-  // Only columns within +-PAD of an output column < C are read.
-  const bool lneed = lg < 3 && lj >= kHalo - PAD && lj < kHalo + kColBlock + PAD && g < a.C + PAD;
-  if (g < 0) g = -g;
-  if (g >= a.A) g = 2 * (a.A - 1) - g;
-  const bool lvalid = lneed && g < cap;  // g >= cap: p = 0, mean 0, z = 0
+  const int lq = tid % NQ, lg = tid / NQ;
+  const bool lactive = lg < RG;
+  const int gc = c0 - kHalo + 4 * (kQ0 + lq);  // first (unreflected) column of this thread's 4
+  // Fast: 4 in-range valid columns, loaded with one 16-byte load from aligned rows.
+  const bool fast = a.vec && gc >= 0 && gc + 4 <= cap;
+  int gs[4];
+  bool vs[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    int g = gc + i;
+    // Only columns within +-PAD of an output column < C are read.
+    const bool need = g >= c0 - PAD && g < c0 + kColBlock + PAD && g < a.C + PAD;
+    if (g < 0) g = -g;
+    if (g >= a.A) g = 2 * (a.A - 1) - g;
+    gs[i] = g;
+    vs[i] = lactive && need && g < cap;  // g >= cap: p = 0, mean 0, z = 0
+  }
+  const bool any_valid = vs[0] || vs[1] || vs[2] || vs[3];
 
   float acc[4] = {0.f, 0.f, 0.f, 0.f};
-  float xv[kLoadRows];
-  float2 cst = make_float2(0.f, 0.f);
-
-  auto issue = [&](int h) {
-    const float* src = a.w + b * a.ws[0] + h * a.ws[1] + g;
-#pragma unroll
-    for (int i = 0; i < kLoadRows; ++i) {
-      const int r = lg + 3 * i;
-      const int t = t0 + r;
-      xv[i] = (lvalid && r < kFiltRows && t < a.T) ? src[(int64_t)t * a.ws[2]] : 0.f;
-    }
-    if (lvalid) cst = a.cs[((int64_t)b * a.H + h) * a.A + g];
+  // Everything one head needs from global memory: this thread's scores, and (for row group 0)
+  // its columns' statistics, (for tid < 16) one row's statistics. Two heads are in flight.
+  struct Prefetch {
+    float x[RPT][4];
+    f32x4 c[2];
+    float2 r;
   };
+  Prefetch pf[2];
 
-  issue(0);
-  for (int h = 0; h < a.H; ++h) {
-    // Row statistics of this head for the 16 rows.
+  auto issue = [&](int h, Prefetch& q) {
+    const int64_t bh = (int64_t)b * a.H + h;
+    const float* src = a.w + b * a.ws[0] + h * a.ws[1];
+#pragma unroll
+    for (int r = 0; r < RPT; ++r) {
+      const int t = t0 + lg + RG * r;
+      const bool row_ok = lactive && lg + RG * r < kFiltRows && t < a.T;
+      const float* rowp = src + (int64_t)t * a.ws[2];
+      if (fast) {
+        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (row_ok) v = *reinterpret_cast<const f32x4*>(rowp + gc);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q.x[r][i] = v[i];
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q.x[r][i] = (row_ok && vs[i]) ? rowp[gs[i]] : 0.f;
+      }
+    }
+    if (lg == 0) {  // one thread per float4 column fetches the statistics for all row groups
+      const float2* cs = a.cs + bh * a.cpitch;
+      if (fast) {
+        q.c[0] = *reinterpret_cast<const f32x4*>(cs + gc);
+        q.c[1] = *reinterpret_cast<const f32x4*>(cs + gc + 2);
+      } else {
+        float2 c[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) c[i] = vs[i] ? cs[gs[i]] : make_float2(0.f, 0.f);
+        q.c[0] = f32x4{c[0].x, c[0].y, c[1].x, c[1].y};
+        q.c[1] = f32x4{c[2].x, c[2].y, c[3].x, c[3].y};
+      }
+    }
     if (tid < kFiltRows) {
       const int t = t0 + tid;
-      rstat[tid] = t < a.T ? a.rs[((int64_t)b * a.H + h) * a.T + t] : make_float2(0.f, 0.f);
+      q.r = t < a.T ? a.rs[bh * a.T + t] : make_float2(0.f, 0.f);
+    }
+  };
+
+  auto head = [&](int h, Prefetch& q) {
+    if (tid < kFiltRows) rstat[tid] = q.r;
+    if (lg == 0) {
+      cstat[lq][0] = q.c[0];
+      cstat[lq][1] = q.c[1];
     }
     __syncthreads();
-    // Normalised tile: z = (exp2(x*log2e - m) / l - mean) / std.
-    if (lg < 3) {
+    // Normalised tile: z = (softmax - mean) / std; 0 in masked columns.
+    if (lactive) {
+      const f32x4 c01 = cstat[lq][0], c23 = cstat[lq][1];
+      const float cmean[4] = {c01[0], c01[2], c23[0], c23[2]};
+      const float crstd[4] = {c01[1], c01[3], c23[1], c23[3]};
 #pragma unroll
-      for (int i = 0; i < kLoadRows; ++i) {
-        const int r = lg + 3 * i;
-        if (r < kFiltRows) {
-          float z = 0.f;
-          if (lvalid) {
-            const float2 st = rstat[r];
-            z = (softmax_value(xv[i], st) - cst.x) * cst.y;
+      for (int r = 0; r < RPT; ++r) {
+        const int rr = lg + RG * r;
+        if (rr < kFiltRows) {
+          f32x4 z = f32x4{0.f, 0.f, 0.f, 0.f};
+          if (any_valid) {
+            const float2 st = rstat[rr];
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (vs[i]) z[i] = (softmax_value(q.x[r][i], st) - cmean[i]) * crstd[i];
           }
-          tile[r * kTilePitch + lj] = z;
+          tile4[(rr * kTilePitch) / 4 + kQ0 + lq] = z;
         }
       }
     }
     __syncthreads();
-    if (h + 1 < a.H) issue(h + 1);  // next head's scores in flight during the filter
-    // 4 medians from the LDS row segment [fq + kHalo - PAD, fq + 3 + kHalo + PAD].
+    if (h + 2 < a.H) issue(h + 2, q);  // refill this slot; it lands two heads from now
     {
+      // Window values: tile columns [fq + kHalo - PAD, fq + kHalo + 3 + PAD], read as float4s.
+      constexpr int kJ0 = (kHalo - PAD) / 4, kJ1 = (kHalo + 3 + PAD) / 4;
+      constexpr int kOff = kHalo - PAD - 4 * kJ0;
+      float seg[4 * (kJ1 - kJ0 + 1)];
+#pragma unroll
+      for (int j = kJ0; j <= kJ1; ++j) {
+        const f32x4 v = tile4[(fr * kTilePitch + fq) / 4 + j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) seg[4 * (j - kJ0) + i] = v[i];
+      }
       float win[4 + 2 * PAD];
-      const float* rowp = tile + fr * kTilePitch + fq + kHalo - PAD;
 #pragma unroll
-      for (int i = 0; i < 4 + 2 * PAD; ++i) win[i] = rowp[i];
+      for (int i = 0; i < 4 + 2 * PAD; ++i) win[i] = seg[kOff + i];
+      float med[4];
+      window_medians<PAD>(win, med);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] += window_median<PAD>(win + i);
+      for (int i = 0; i < 4; ++i) acc[i] += med[i];
     }
-    __syncthreads();  // the tile and rstat are rewritten for the next head
+    __syncthreads();  // the tile and the statistics are rewritten for the next head
+  };
+
+  issue(0, pf[0]);
+  if (a.H > 1) issue(1, pf[1]);
+  for (int h = 0; h < a.H; h += 2) {
+    head(h, pf[0]);
+    if (h + 1 < a.H) head(h + 1, pf[1]);
   }
   if (ot < a.T) {
     float* dst = a.out + b * a.os[0] + (int64_t)ot * a.os[1] + c0 + fq;
@@ -339,33 +628,224 @@ __global__ __launch_bounds__(256) void dtw_filter_kernel(DtwArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Normalise + median filter + head mean over whole rows (rows 16-byte aligned, A <= 2048):
+// one workgroup per (4 rows, b), 256 threads. Per head, the 4 rows are read as contiguous
+// 16-byte vectors (the next head's loads are issued before this head is filtered), normalised
+// into an LDS tile with PAD reflected columns on each side, and each thread accumulates the
+// medians of its groups of 4 output columns. Reading whole rows keeps every HBM line fetched
+// exactly once; a column strip of the rows would fetch its edge lines twice.
+// ---------------------------------------------------------------------------------------------
+constexpr int kBandRows = 4;
+constexpr int kBandMaxA4 = 512;                  // float4 columns per row (A <= 2048)
+constexpr int kBandLoads = kBandMaxA4 / 256;      // float4 columns per thread per row
+constexpr int kBandPitch = 4 * kBandMaxA4 + 16;  // floats: 8 halo columns each side
+
+template <int PAD>
+__global__ __launch_bounds__(256) void dtw_band_kernel(DtwArgs a) {
+  const int b = blockIdx.y;
+  const int t0 = blockIdx.x * kBandRows;
+  const int tid = threadIdx.x;
+  const int cap = clamp_cap(a.caps[b], a.A);
+  const int len = a.lens[b];
+  const int A4 = (a.A + 3) >> 2;
+  const int C4 = (a.C + 3) >> 2;
+  const int n_rows = min(kBandRows, a.T - t0);
+
+  if (cap <= 0 || len <= 0) {  // 0/0 in the reference: the whole batch row is NaN
+    for (int r = 0; r < n_rows; ++r)
+      for (int c = tid; c < a.C; c += 256) a.out[b * a.os[0] + (int64_t)(t0 + r) * a.os[1] + c] = __builtin_nanf("");
+    return;
+  }
+
+  __shared__ f32x4 tile4[kBandRows * kBandPitch / 4];
+  float* tile = reinterpret_cast<float*>(tile4);
+
+  struct Prefetch {
+    f32x4 x[kBandRows][kBandLoads];
+    f32x4 c[kBandLoads][2];  // (mean, 1/std) of the 4 columns of each float4 column
+    float2 r[kBandRows];
+  };
+  Prefetch pf;
+
+  auto issue = [&](int h, Prefetch& q) {
+    const int64_t bh = (int64_t)b * a.H + h;
+    const float* src = a.w + b * a.ws[0] + h * a.ws[1];
+    const float2* cs = a.cs + bh * a.cpitch;
+#pragma unroll
+    for (int r = 0; r < kBandRows; ++r) q.r[r] = r < n_rows ? a.rs[bh * a.T + t0 + r] : make_float2(0.f, 0.f);
+#pragma unroll
+    for (int k = 0; k < kBandLoads; ++k) {
+      const int col = 4 * (tid + 256 * k);
+      q.c[k][0] = q.c[k][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (col < cap) {
+        q.c[k][0] = *reinterpret_cast<const f32x4*>(cs + col);
+        q.c[k][1] = *reinterpret_cast<const f32x4*>(cs + col + 2);
+      }
+#pragma unroll
+      for (int r = 0; r < kBandRows; ++r) {
+        const float* rowp = src + (int64_t)(t0 + r) * a.ws[2];
+        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+        if (r < n_rows) {
+          if (col + 4 <= cap) {
+            v = *reinterpret_cast<const f32x4*>(rowp + col);
+          } else if (col < cap) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = col + i < cap ? rowp[col + i] : 0.f;
+          }
+        }
+        q.x[r][k] = v;
+      }
+    }
+  };
+
+  float acc[kBandRows][kBandLoads][4];
+#pragma unroll
+  for (int r = 0; r < kBandRows; ++r)
+#pragma unroll
+    for (int k = 0; k < kBandLoads; ++k)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[r][k][i] = 0.f;
+
+  auto head = [&](int h, Prefetch& q) {
+    // Normalised rows: z = (softmax - mean) / std; 0 in masked columns (c >= cap).
+#pragma unroll
+    for (int k = 0; k < kBandLoads; ++k) {
+      const int q4 = tid + 256 * k;
+      if (q4 < A4) {
+        const int col = 4 * q4;
+        const float cmean[4] = {q.c[k][0][0], q.c[k][0][2], q.c[k][1][0], q.c[k][1][2]};
+        const float crstd[4] = {q.c[k][0][1], q.c[k][0][3], q.c[k][1][1], q.c[k][1][3]};
+#pragma unroll
+        for (int r = 0; r < kBandRows; ++r) {
+          f32x4 z = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (col + i < cap) z[i] = (softmax_value(q.x[r][k][i], q.r[r]) - cmean[i]) * crstd[i];
+          tile4[(r * kBandPitch + kHalo) / 4 + q4] = z;
+        }
+      }
+    }
+    __syncthreads();
+    if (h + 1 < a.H) issue(h + 1, q);  // the next head's loads are in flight during the filter
+    if constexpr (PAD > 0) {
+      // Reflect padding: column -i is column i, column A-1+i is column A-1-i.
+      if (tid < kBandRows * 2 * PAD) {
+        const int r = tid / (2 * PAD), i = tid % (2 * PAD);
+        float* row = tile + r * kBandPitch + kHalo;
+        if (i < PAD) row[-1 - i] = row[1 + i];
+        else row[a.A + (i - PAD)] = row[a.A - 2 - (i - PAD)];
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int k = 0; k < kBandLoads; ++k) {
+      const int g = tid + 256 * k;  // output columns 4g .. 4g+3
+      if (g < C4) {
+#pragma unroll
+        for (int r = 0; r < kBandRows; ++r) {
+          constexpr int kJ0 = (kHalo - PAD) / 4, kJ1 = (kHalo + 3 + PAD) / 4;
+          constexpr int kOff = kHalo - PAD - 4 * kJ0;
+          float seg[4 * (kJ1 - kJ0 + 1)];
+#pragma unroll
+          for (int j = kJ0; j <= kJ1; ++j) {
+            const f32x4 v = tile4[(r * kBandPitch) / 4 + g + j];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) seg[4 * (j - kJ0) + i] = v[i];
+          }
+          float win[4 + 2 * PAD];
+#pragma unroll
+          for (int i = 0; i < 4 + 2 * PAD; ++i) win[i] = seg[kOff + i];
+          float med[4];
+          window_medians<PAD>(win, med);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) acc[r][k][i] += med[i];
+        }
+      }
+    }
+    __syncthreads();  // the tile is rewritten for the next head
+  };
+
+  issue(0, pf);
+  for (int h = 0; h < a.H; ++h) head(h, pf);
+#pragma unroll
+  for (int k = 0; k < kBandLoads; ++k) {
+    const int g = tid + 256 * k;
+    if (g < C4) {
+#pragma unroll
+      for (int r = 0; r < kBandRows; ++r) {
+        if (r < n_rows) {
+          float* dst = a.out + b * a.os[0] + (int64_t)(t0 + r) * a.os[1] + 4 * g;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (4 * g + i < a.C) dst[i] = acc[r][k][i] / (float)a.H;
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+// Workspace: row statistics [B*H*T], column statistics [B*H, cpitch], chunk partials
+// [B*H, n_chunks, cpitch] (float2 each; cpitch = A rounded up to 4), each 256-byte aligned.
+namespace {
+size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 }  // namespace
 
 size_t dtw_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A) {
-  const size_t rows = (size_t)(B * H * T) * sizeof(float2);
-  const size_t cols = (size_t)(B * H * A) * sizeof(float2);
-  return ((rows + 255) & ~(size_t)255) + cols;
+  const int64_t cpitch = (A + 3) & ~int64_t(3);
+  const int64_t n_chunks = (T + kRcRows - 1) / kRcRows;
+  return align256((size_t)(B * H * T) * sizeof(float2)) + align256((size_t)(B * H * cpitch) * sizeof(float2)) +
+         (size_t)(B * H * n_chunks * cpitch) * sizeof(float2);
 }
 
 void dtw_workspace_layout(void* ws, DtwArgs* a) {
   char* p = static_cast<char*>(ws);
+  a->cpitch = (a->A + 3) & ~3;
+  const int64_t bh = (int64_t)a->B * a->H;
   a->rs = reinterpret_cast<float2*>(p);
-  const size_t rows = (size_t)((int64_t)a->B * a->H * a->T) * sizeof(float2);
-  a->cs = reinterpret_cast<float2*>(p + ((rows + 255) & ~(size_t)255));
+  p += align256((size_t)(bh * a->T) * sizeof(float2));
+  a->cs = reinterpret_cast<float2*>(p);
+  p += align256((size_t)(bh * a->cpitch) * sizeof(float2));
+  a->part = reinterpret_cast<float2*>(p);
 }
 
-hipError_t launch_dtw_prep(const DtwArgs& a, hipStream_t stream) {
+hipError_t launch_dtw_prep(DtwArgs a, hipStream_t stream) {
   const int64_t n_rows = (int64_t)a.B * a.H * a.T;
   if (n_rows == 0 || a.C == 0) return hipSuccess;
-  const bool vec = (reinterpret_cast<uintptr_t>(a.w) & 15) == 0 && a.ws[0] % 4 == 0 && a.ws[1] % 4 == 0 &&
-                   a.ws[2] % 4 == 0;
-  const dim3 rgrid((unsigned)((n_rows + 3) / 4));
-  if (vec) hipLaunchKernelGGL(dtw_row_stats_kernel<true>, rgrid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL(dtw_row_stats_kernel<false>, rgrid, dim3(256), 0, stream, a);
+  a.vec = (reinterpret_cast<uintptr_t>(a.w) & 15) == 0 && a.ws[0] % 4 == 0 && a.ws[1] % 4 == 0 &&
+          a.ws[2] % 4 == 0;
   // Columns the filter reads: [0, min(A, C + pad)).
   const int need = a.C + a.pad < a.A ? a.C + a.pad : a.A;
-  hipLaunchKernelGGL(dtw_col_stats_kernel, dim3((need + kColBlock - 1) / kColBlock, a.H, a.B), dim3(512), 0,
-                     stream, a);
+  if (a.vec && a.A <= 2048) {
+    const dim3 grid((a.T + kRcRows - 1) / kRcRows, a.H, a.B);
+    if (a.A <= 512) hipLaunchKernelGGL(dtw_rowcol_kernel<2>, grid, dim3(256), 0, stream, a);
+    else if (a.A <= 1024) hipLaunchKernelGGL(dtw_rowcol_kernel<4>, grid, dim3(256), 0, stream, a);
+    else if (a.A <= 1536) hipLaunchKernelGGL(dtw_rowcol_kernel<6>, grid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL(dtw_rowcol_kernel<8>, grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(dtw_col_merge_kernel, dim3((need + 255) / 256, a.H, a.B), dim3(256), 0, stream, a, need);
+  } else {
+    const dim3 rgrid((unsigned)((n_rows + 3) / 4));
+    if (a.vec) hipLaunchKernelGGL(dtw_row_stats_kernel<true>, rgrid, dim3(256), 0, stream, a);
+    else hipLaunchKernelGGL(dtw_row_stats_kernel<false>, rgrid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL(dtw_col_stats_kernel, dim3((need + kColBlock - 1) / kColBlock, a.H, a.B), dim3(512), 0,
+                       stream, a);
+  }
+  if (a.vec && a.A <= 4 * kBandMaxA4) {
+    const dim3 grid((a.T + kBandRows - 1) / kBandRows, a.B);
+    switch (a.pad) {
+#define WDRZ_BAND(P) \
+  case P:            \
+    hipLaunchKernelGGL(dtw_band_kernel<P>, grid, dim3(256), 0, stream, a); \
+    break;
+      WDRZ_BAND(0) WDRZ_BAND(1) WDRZ_BAND(2) WDRZ_BAND(3) WDRZ_BAND(4) WDRZ_BAND(5) WDRZ_BAND(6) WDRZ_BAND(7)
+#undef WDRZ_BAND
+      default:
+        return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
+  }
   const dim3 grid((a.C + kColBlock - 1) / kColBlock, (a.T + kFiltRows - 1) / kFiltRows, a.B);
   switch (a.pad) {
 #define WDRZ_FILT(P) \

@@ -60,13 +60,16 @@ struct DtwArgs {
   const int32_t* caps;  // [B] valid audio columns
   float* out;           // [B, T, C]
   float2* rs;           // workspace: per-row (max*log2e, 1/sum)
-  float2* cs;           // workspace: per-column (mean, 1/std)
+  float2* cs;           // workspace: per-column (mean, 1/std), row pitch cpitch
+  float2* part;         // workspace: per-64-row-chunk column partials (mean, M2), pitch cpitch
   int B, H, T, A, C, pad;
+  int cpitch;  // A rounded up to a multiple of 4
+  int vec;     // rows of W start 16-byte aligned (set by the launcher)
   int64_t ws[3];  // W strides b, h, t
   int64_t os[2];  // out strides b, t
 };
 size_t dtw_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A);
 void dtw_workspace_layout(void* ws, DtwArgs* a);
-hipError_t launch_dtw_prep(const DtwArgs& a, hipStream_t stream);
+hipError_t launch_dtw_prep(DtwArgs a, hipStream_t stream);
 
 }  // namespace wdrz

@@ -71,8 +71,9 @@ def dtw_prep(
     if T == 0 or C == 0:
         return out
     w = _kernel_ready(w)
-    lens_t = torch.tensor(lens, dtype=torch.int32, device=device)
-    caps_t = torch.tensor(caps, dtype=torch.int32, device=device)
+    # One small host->device copy from pinned memory, ordered on the current stream.
+    meta = torch.tensor([lens, caps], dtype=torch.int32).pin_memory().to(device, non_blocking=True)
+    lens_t, caps_t = meta[0], meta[1]
     lib = _lib.load()
     nbytes = dtw_prep_workspace_size(B, H, T, A)
     ws = _DTW_WORKSPACES.get(device, nbytes)
