@@ -157,7 +157,7 @@ def test_dtw_prep_empty_is_a_no_op(lib):
 def test_dtw_workspace_size(lib):
     B, H, T, A = 16, 10, 448, 1500
     n = lib.wdrz_dtw_prep_workspace_size(B, H, T, A)
-    # row stats + column stats + per-64-row-chunk column partials, each 256-byte aligned
-    n_chunks = (T + 63) // 64
-    assert n == 8 * B * H * (T + A + n_chunks * A)
+    # row stats + column stats + column partials of the row chunks (as many chunks as keep
+    # B*H*chunks <= 768: 4 chunks of 112 rows here), each 256-byte aligned
+    assert n == 8 * B * H * (T + A + 4 * A)
     assert lib.wdrz_dtw_prep_workspace_size(0, H, T, A) == 0

@@ -72,8 +72,20 @@ __device__ __forceinline__ float softmax_scale_e(float e, float rl) {
 #pragma clang fp contract(off)
   return e * rl;
 }
+// The hardware exp2 (no denormal-range fix-up: a value below 2^-126 is negligible next to the
+// column mean it is compared with).
+__device__ __forceinline__ float softmax_exp(float x, float m) { return fast_exp2(__builtin_fmaf(x, kLog2e, -m)); }
 __device__ __forceinline__ float softmax_value(float x, float2 st) {
-  return softmax_scale_e(exp2f(__builtin_fmaf(x, kLog2e, -st.x)), st.y);
+  return softmax_scale_e(softmax_exp(x, st.x), st.y);
+}
+
+// f(0), f(1), ..., f(N-1) as straight-line code.
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (N > 0) {
+    static_for<N - 1>(f);
+    f(N - 1);
+  }
 }
 
 __device__ __forceinline__ int clamp_cap(int cap, int A) { return cap < 0 ? 0 : (cap > A ? A : cap); }
@@ -218,8 +230,10 @@ __global__ __launch_bounds__(512) void dtw_col_stats_kernel(DtwArgs a) {
 // through LDS and the chunk's partial (mean, M2) per column is stored for dtw_col_merge_kernel.
 // ---------------------------------------------------------------------------------------------
 constexpr int kRcWaves = 4;
-constexpr int kRcRowsPerWave = 16;
-constexpr int kRcRows = kRcWaves * kRcRowsPerWave;
+// Workgroups of the fused pass that fit on the GPU at once (256 CUs x 3 four-wave workgroups at
+// up to 168 VGPRs). The rows of each (b, h) are cut into as many chunks as keep B*H*chunks
+// within one such round, so no workgroup runs in a second, mostly idle round.
+constexpr int kRcSlots = 768;
 
 __device__ __forceinline__ void chan_merge(float na, float& ma, float& qa, float nb, float mb, float qb) {
   if (nb == 0.f) return;
@@ -239,8 +253,9 @@ __global__ __launch_bounds__(256) void dtw_rowcol_kernel(DtwArgs a) {
   const int rows_valid = len < a.T ? len : a.T;
   const int64_t bh = (int64_t)b * a.H + h;
   const float* base = a.w + b * a.ws[0] + h * a.ws[1];
-  const int t_first = chunk * kRcRows + wave * kRcRowsPerWave;
-  const int t_end = min(t_first + kRcRowsPerWave, a.T);
+  const int rpw = a.rc_rows / kRcWaves;  // rows per wave
+  const int t_first = chunk * a.rc_rows + wave * rpw;
+  const int t_end = min(t_first + rpw, a.T);
 
   float cm[NK][4], cq[NK][4];
 #pragma unroll
@@ -248,27 +263,34 @@ __global__ __launch_bounds__(256) void dtw_rowcol_kernel(DtwArgs a) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) cm[j][i] = cq[j][i] = 0.f;
 
-  auto load_row = [&](int t, float (&x)[NK][4]) {
-    const float* src = base + (int64_t)t * a.ws[2];
+  // Loads are straight-line code at clamped (always valid) addresses, masked after the load,
+  // so the compiler can wait for exactly the row it consumes: with A % 4 == 0 every float4
+  // column 4*(lane + 64 j) clamped to A - 4 lies inside the row.
+  bool colv[NK][4];
+  int colc[NK];
+#pragma unroll
+  for (int j = 0; j < NK; ++j) {
+    const int col = 4 * (lane + 64 * j);
+    colc[j] = min(col, a.A - 4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) colv[j][i] = col + i < cap;
+  }
+  auto load_row = [&](int t, float (&x)[NK][4]) __attribute__((always_inline)) {
+    const float* src = base + (int64_t)min(t, t_end - 1) * a.ws[2];
 #pragma unroll
     for (int j = 0; j < NK; ++j) {
-      const int col = 4 * (lane + 64 * j);
-      if (col + 4 <= cap) {
-        const f32x4 v = *reinterpret_cast<const f32x4*>(src + col);
+      const f32x4 v = *reinterpret_cast<const f32x4*>(src + colc[j]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) x[j][i] = v[i];
-      } else {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) x[j][i] = col + i < cap ? src[col + i] : -INFINITY;
-      }
+      for (int i = 0; i < 4; ++i) x[j][i] = v[i];
     }
   };
 
-  float x[NK][4], xn[NK][4];
-  if (t_first < t_end) load_row(t_first, x);
   int k = 0;  // valid rows folded in by this wave
-  for (int t = t_first; t < t_end; ++t) {
-    if (t + 1 < t_end) load_row(t + 1, xn);
+  auto row_step = [&](int t, float (&x)[NK][4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < NK; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[j][i] = colv[j][i] ? x[j][i] : -INFINITY;
     // max(x) * log2e == max(x * log2e): the scaling is monotone, rounding included.
     float mx = -INFINITY;
 #pragma unroll
@@ -277,13 +299,14 @@ __global__ __launch_bounds__(256) void dtw_rowcol_kernel(DtwArgs a) {
       for (int i = 0; i < 4; ++i) mx = fmaxf(mx, x[j][i]);
     float2 st;
     st.x = wave_max(mx) * kLog2e;
-    // e = exp2(x*log2e - m) as softmax_value forms it; kept for the column update (-inf -> 0).
+    // e = exp2(x*log2e - m) exactly as softmax_value forms it; kept for the column update
+    // (-inf -> 0).
     float sum = 0.f;
 #pragma unroll
     for (int j = 0; j < NK; ++j)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        x[j][i] = exp2f(__builtin_fmaf(x[j][i], kLog2e, -st.x));
+        x[j][i] = softmax_exp(x[j][i], st.x);
         sum += x[j][i];
       }
     st.y = 1.f / wave_sum(sum);
@@ -301,17 +324,26 @@ __global__ __launch_bounds__(256) void dtw_rowcol_kernel(DtwArgs a) {
           cq[j][i] += d * (p - cm[j][i]);
         }
     }
-#pragma unroll
-    for (int j = 0; j < NK; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) x[j][i] = xn[j][i];
+  };
+
+  // Two rows in flight while a row is processed: three row buffers in rotation, six rows per
+  // unrolled iteration so each buffer keeps its role across iterations.
+  float xb[3][NK][4];
+  load_row(t_first, xb[0]);
+  load_row(t_first + 1, xb[1]);
+  for (int t6 = t_first; t6 < t_end; t6 += 6) {
+    static_for<6>([&](int r) __attribute__((always_inline)) {
+      const int t = t6 + r;
+      load_row(t + 2, xb[(r + 2) % 3]);
+      if (t < t_end) row_step(t, xb[r % 3]);
+    });
   }
 
   // Merge the waves' accumulators: 2+3 into 0+1, then 1 into 0.
   __shared__ f32x4 red[2][NK * 64][2];  // [wave slot][lane j][mean4 | M2 4]
   auto wave_rows = [&](int w) {
-    const int lo = chunk * kRcRows + w * kRcRowsPerWave;
-    const int hi = min(lo + kRcRowsPerWave, rows_valid);
+    const int lo = chunk * a.rc_rows + w * rpw;
+    const int hi = min(lo + rpw, rows_valid);
     return (float)(hi > lo ? hi - lo : 0);
   };
   float n_self = (float)k;
@@ -341,7 +373,7 @@ __global__ __launch_bounds__(256) void dtw_rowcol_kernel(DtwArgs a) {
     __syncthreads();
   }
   if (wave == 0 && n_self > 0.f) {
-    const int n_chunks = (a.T + kRcRows - 1) / kRcRows;
+    const int n_chunks = (a.T + a.rc_rows - 1) / a.rc_rows;
     float2* part = a.part + (bh * n_chunks + chunk) * a.cpitch;
 #pragma unroll
     for (int j = 0; j < NK; ++j) {
@@ -366,12 +398,12 @@ __global__ __launch_bounds__(256) void dtw_col_merge_kernel(DtwArgs a, int need)
   const int len = a.lens[b];
   if (cap <= 0 || len <= 0 || c >= cap || c >= need) return;
   const int rows_valid = len < a.T ? len : a.T;
-  const int n_chunks = (a.T + kRcRows - 1) / kRcRows;
+  const int n_chunks = (a.T + a.rc_rows - 1) / a.rc_rows;
   const int64_t bh = (int64_t)b * a.H + h;
   const float2* part = a.part + bh * n_chunks * a.cpitch + c;
   float n = 0.f, mean = 0.f, m2 = 0.f;
-  for (int i = 0; i * kRcRows < rows_valid; ++i) {
-    const int rows_i = min(rows_valid - i * kRcRows, kRcRows);
+  for (int i = 0; i * a.rc_rows < rows_valid; ++i) {
+    const int rows_i = min(rows_valid - i * a.rc_rows, a.rc_rows);
     const float2 pi = part[(int64_t)i * a.cpitch];
     chan_merge(n, mean, m2, (float)rows_i, pi.x, pi.y);
     n += (float)rows_i;
@@ -629,157 +661,162 @@ __global__ __launch_bounds__(256) void dtw_filter_kernel(DtwArgs a) {
 }
 
 // ---------------------------------------------------------------------------------------------
-// Normalise + median filter + head mean over whole rows (rows 16-byte aligned, A <= 2048):
-// one workgroup per (4 rows, b), 256 threads. Per head, the 4 rows are read as contiguous
-// 16-byte vectors (the next head's loads are issued before this head is filtered), normalised
-// into an LDS tile with PAD reflected columns on each side, and each thread accumulates the
-// medians of its groups of 4 output columns. Reading whole rows keeps every HBM line fetched
-// exactly once; a column strip of the rows would fetch its edge lines twice.
+// Normalise + median filter + head mean over whole rows (rows 16-byte aligned, A % 4 == 0,
+// A <= 2048): one workgroup per (4 rows, b), NT = 128 * ceil(A / 512) threads, one float4
+// column each. Per head, the 4 rows are read as contiguous 16-byte vectors, normalised into an
+// LDS tile with PAD reflected columns on each side, and each thread accumulates the medians of
+// its 4 output columns in the 4 rows. Reading whole rows fetches every HBM line once.
+//
+// Latency: two heads' loads are in flight while a head is filtered. The loads are
+// straight-line code at clamped (always valid) addresses, with out-of-range data masked after
+// the load, so the compiler waits for exactly the head it consumes.
 // ---------------------------------------------------------------------------------------------
 constexpr int kBandRows = 4;
-constexpr int kBandMaxA4 = 512;                  // float4 columns per row (A <= 2048)
-constexpr int kBandLoads = kBandMaxA4 / 256;      // float4 columns per thread per row
-constexpr int kBandPitch = 4 * kBandMaxA4 + 16;  // floats: 8 halo columns each side
+constexpr int kBandMaxA4 = 512;    // float4 columns per row (A <= 2048)
+constexpr int kBandMaxHeads = 16;  // heads per call on this path (large-v3 aligns on 10)
 
-template <int PAD>
-__global__ __launch_bounds__(256) void dtw_band_kernel(DtwArgs a) {
-  const int b = blockIdx.y;
-  const int t0 = blockIdx.x * kBandRows;
+template <int PAD, int NT>
+__global__ __launch_bounds__(NT) void dtw_band_kernel(DtwArgs a) {
+  // Last batch row first: the statistics pass ended there, so its scores are the ones still
+  // held in the device-wide (infinity) cache.
+  const int b = a.B - 1 - (int)blockIdx.y;
+  const int t0 = (gridDim.x - 1 - blockIdx.x) * kBandRows;
   const int tid = threadIdx.x;
   const int cap = clamp_cap(a.caps[b], a.A);
   const int len = a.lens[b];
-  const int A4 = (a.A + 3) >> 2;
-  const int C4 = (a.C + 3) >> 2;
+  const int A4 = a.A >> 2;
   const int n_rows = min(kBandRows, a.T - t0);
 
   if (cap <= 0 || len <= 0) {  // 0/0 in the reference: the whole batch row is NaN
     for (int r = 0; r < n_rows; ++r)
-      for (int c = tid; c < a.C; c += 256) a.out[b * a.os[0] + (int64_t)(t0 + r) * a.os[1] + c] = __builtin_nanf("");
+      for (int c = tid; c < a.C; c += NT) a.out[b * a.os[0] + (int64_t)(t0 + r) * a.os[1] + c] = __builtin_nanf("");
     return;
   }
 
+  constexpr int kBandPitch = 4 * NT + 16;  // floats: 8 halo columns each side
   __shared__ f32x4 tile4[kBandRows * kBandPitch / 4];
   float* tile = reinterpret_cast<float*>(tile4);
 
+  const bool active = tid < A4;
+  const int col = 4 * (active ? tid : A4 - 1);  // clamped: every load address is valid
+  bool valid[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) valid[i] = active && col + i < cap;
+
   struct Prefetch {
-    f32x4 x[kBandRows][kBandLoads];
-    f32x4 c[kBandLoads][2];  // (mean, 1/std) of the 4 columns of each float4 column
+    f32x4 x[kBandRows];
+    f32x4 c[2];  // (mean, 1/std) of the 4 columns
     float2 r[kBandRows];
   };
-  Prefetch pf;
+  Prefetch pf[2];
 
-  auto issue = [&](int h, Prefetch& q) {
+  auto issue = [&](int h, Prefetch& q) __attribute__((always_inline)) {
+    h = min(h, a.H - 1);
     const int64_t bh = (int64_t)b * a.H + h;
     const float* src = a.w + b * a.ws[0] + h * a.ws[1];
-    const float2* cs = a.cs + bh * a.cpitch;
+    const float2* cs = a.cs + bh * a.cpitch + col;
+    q.c[0] = *reinterpret_cast<const f32x4*>(cs);
+    q.c[1] = *reinterpret_cast<const f32x4*>(cs + 2);
 #pragma unroll
-    for (int r = 0; r < kBandRows; ++r) q.r[r] = r < n_rows ? a.rs[bh * a.T + t0 + r] : make_float2(0.f, 0.f);
-#pragma unroll
-    for (int k = 0; k < kBandLoads; ++k) {
-      const int col = 4 * (tid + 256 * k);
-      q.c[k][0] = q.c[k][1] = f32x4{0.f, 0.f, 0.f, 0.f};
-      if (col < cap) {
-        q.c[k][0] = *reinterpret_cast<const f32x4*>(cs + col);
-        q.c[k][1] = *reinterpret_cast<const f32x4*>(cs + col + 2);
-      }
-#pragma unroll
-      for (int r = 0; r < kBandRows; ++r) {
-        const float* rowp = src + (int64_t)(t0 + r) * a.ws[2];
-        f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
-        if (r < n_rows) {
-          if (col + 4 <= cap) {
-            v = *reinterpret_cast<const f32x4*>(rowp + col);
-          } else if (col < cap) {
-#pragma unroll
-            for (int i = 0; i < 4; ++i) v[i] = col + i < cap ? rowp[col + i] : 0.f;
-          }
-        }
-        q.x[r][k] = v;
-      }
+    for (int r = 0; r < kBandRows; ++r) {
+      const int t = min(t0 + r, a.T - 1);
+      q.r[r] = a.rs[bh * a.T + t];
+      q.x[r] = *reinterpret_cast<const f32x4*>(src + (int64_t)t * a.ws[2] + col);
     }
   };
 
-  float acc[kBandRows][kBandLoads][4];
+  float acc[kBandRows][4];
 #pragma unroll
   for (int r = 0; r < kBandRows; ++r)
 #pragma unroll
-    for (int k = 0; k < kBandLoads; ++k)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) acc[r][k][i] = 0.f;
+    for (int i = 0; i < 4; ++i) acc[r][i] = 0.f;
 
-  auto head = [&](int h, Prefetch& q) {
-    // Normalised rows: z = (softmax - mean) / std; 0 in masked columns (c >= cap).
+  auto head = [&](int h, Prefetch& q) __attribute__((always_inline)) {
+    // Normalised rows: z = (softmax - mean) / std; 0 in masked columns (c >= cap). Columns
+    // 1..PAD and A-1-PAD..A-2 are also written to their reflected positions -1..-PAD and
+    // A..A-1+PAD (torch's reflect padding).
+    const float cmean[4] = {q.c[0][0], q.c[0][2], q.c[1][0], q.c[1][2]};
+    const float crstd[4] = {q.c[0][1], q.c[0][3], q.c[1][1], q.c[1][3]};
 #pragma unroll
-    for (int k = 0; k < kBandLoads; ++k) {
-      const int q4 = tid + 256 * k;
-      if (q4 < A4) {
-        const int col = 4 * q4;
-        const float cmean[4] = {q.c[k][0][0], q.c[k][0][2], q.c[k][1][0], q.c[k][1][2]};
-        const float crstd[4] = {q.c[k][0][1], q.c[k][0][3], q.c[k][1][1], q.c[k][1][3]};
+    for (int r = 0; r < kBandRows; ++r) {
+      f32x4 z;
 #pragma unroll
-        for (int r = 0; r < kBandRows; ++r) {
-          f32x4 z = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int i = 0; i < 4; ++i) {
+        const float v = (softmax_value(q.x[r][i], q.r[r]) - cmean[i]) * crstd[i];
+        z[i] = valid[i] ? v : 0.f;
+      }
+      if (active) {
+        tile4[(r * kBandPitch + kHalo) / 4 + tid] = z;
+        if constexpr (PAD > 0) {
+          float* row = tile + r * kBandPitch + kHalo;
+          if (col <= PAD) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (col + i < cap) z[i] = (softmax_value(q.x[r][k][i], q.r[r]) - cmean[i]) * crstd[i];
-          tile4[(r * kBandPitch + kHalo) / 4 + q4] = z;
+            for (int i = 0; i < 4; ++i)
+              if (col + i >= 1 && col + i <= PAD) row[-(col + i)] = z[i];
+          }
+          if (col + 3 >= a.A - 1 - PAD) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int c = col + i;
+              if (c >= a.A - 1 - PAD && c <= a.A - 2) row[2 * (a.A - 1) - c] = z[i];
+            }
+          }
         }
       }
     }
     __syncthreads();
-    if (h + 1 < a.H) issue(h + 1, q);  // the next head's loads are in flight during the filter
-    if constexpr (PAD > 0) {
-      // Reflect padding: column -i is column i, column A-1+i is column A-1-i.
-      if (tid < kBandRows * 2 * PAD) {
-        const int r = tid / (2 * PAD), i = tid % (2 * PAD);
-        float* row = tile + r * kBandPitch + kHalo;
-        if (i < PAD) row[-1 - i] = row[1 + i];
-        else row[a.A + (i - PAD)] = row[a.A - 2 - (i - PAD)];
-      }
-      __syncthreads();
-    }
+    const bool live = h < a.H;  // a padding head (odd H) is computed but not accumulated
+    issue(h + 2, q);            // refill this slot; it is consumed two heads from now
+    {
+      constexpr int kJ0 = (kHalo - PAD) / 4, kJ1 = (kHalo + 3 + PAD) / 4;
+      constexpr int kOff = kHalo - PAD - 4 * kJ0;
 #pragma unroll
-    for (int k = 0; k < kBandLoads; ++k) {
-      const int g = tid + 256 * k;  // output columns 4g .. 4g+3
-      if (g < C4) {
+      for (int r = 0; r < kBandRows; ++r) {
+        float seg[4 * (kJ1 - kJ0 + 1)];
 #pragma unroll
-        for (int r = 0; r < kBandRows; ++r) {
-          constexpr int kJ0 = (kHalo - PAD) / 4, kJ1 = (kHalo + 3 + PAD) / 4;
-          constexpr int kOff = kHalo - PAD - 4 * kJ0;
-          float seg[4 * (kJ1 - kJ0 + 1)];
+        for (int j = kJ0; j <= kJ1; ++j) {
+          const f32x4 v = tile4[(r * kBandPitch) / 4 + tid + j];
 #pragma unroll
-          for (int j = kJ0; j <= kJ1; ++j) {
-            const f32x4 v = tile4[(r * kBandPitch) / 4 + g + j];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) seg[4 * (j - kJ0) + i] = v[i];
-          }
-          float win[4 + 2 * PAD];
-#pragma unroll
-          for (int i = 0; i < 4 + 2 * PAD; ++i) win[i] = seg[kOff + i];
-          float med[4];
-          window_medians<PAD>(win, med);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) acc[r][k][i] += med[i];
+          for (int i = 0; i < 4; ++i) seg[4 * (j - kJ0) + i] = v[i];
         }
+        float win[4 + 2 * PAD];
+#pragma unroll
+        for (int i = 0; i < 4 + 2 * PAD; ++i) win[i] = seg[kOff + i];
+        float med[4];
+        window_medians<PAD>(win, med);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[r][i] += live ? med[i] : 0.f;
       }
     }
     __syncthreads();  // the tile is rewritten for the next head
   };
 
-  issue(0, pf);
-  for (int h = 0; h < a.H; ++h) head(h, pf);
+  issue(0, pf[0]);
+  issue(1, pf[1]);
+  if constexpr (PAD == 3 && NT >= 384) {
+    // Whisper's shape (width 7, 1500 audio columns) fully unrolled: with no loop-carried load
+    // registers each wait covers exactly the head it consumes. (In a loop the compiler waits
+    // for every outstanding load at the top of each head.)
+    static_for<kBandMaxHeads / 2>([&](int i) __attribute__((always_inline)) {
+      if (2 * i < a.H) {
+        head(2 * i, pf[0]);
+        head(2 * i + 1, pf[1]);
+      }
+    });
+  } else {
+    for (int h = 0; h < a.H; h += 2) {
+      head(h, pf[0]);
+      head(h + 1, pf[1]);
+    }
+  }
+  if (tid < ((a.C + 3) >> 2)) {
 #pragma unroll
-  for (int k = 0; k < kBandLoads; ++k) {
-    const int g = tid + 256 * k;
-    if (g < C4) {
+    for (int r = 0; r < kBandRows; ++r) {
+      if (r < n_rows) {
+        float* dst = a.out + b * a.os[0] + (int64_t)(t0 + r) * a.os[1] + 4 * tid;
 #pragma unroll
-      for (int r = 0; r < kBandRows; ++r) {
-        if (r < n_rows) {
-          float* dst = a.out + b * a.os[0] + (int64_t)(t0 + r) * a.os[1] + 4 * g;
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (4 * g + i < a.C) dst[i] = acc[r][k][i] / (float)a.H;
-        }
+        for (int i = 0; i < 4; ++i)
+          if (4 * tid + i < a.C) dst[i] = acc[r][i] / (float)a.H;
       }
     }
   }
@@ -793,9 +830,19 @@ namespace {
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 }  // namespace
 
+// Rows per chunk of the fused statistics pass (a multiple of the 4 waves), from sizes only.
+int dtw_chunk_rows(int64_t B, int64_t H, int64_t T) {
+  int64_t n_chunks = kRcSlots / (B * H);
+  if (n_chunks < 1) n_chunks = 1;
+  int64_t rows = (T + n_chunks - 1) / n_chunks;
+  rows = (rows + kRcWaves - 1) / kRcWaves * kRcWaves;
+  return (int)(rows < kRcWaves ? kRcWaves : rows);
+}
+
 size_t dtw_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A) {
   const int64_t cpitch = (A + 3) & ~int64_t(3);
-  const int64_t n_chunks = (T + kRcRows - 1) / kRcRows;
+  const int64_t rows = dtw_chunk_rows(B, H, T);
+  const int64_t n_chunks = (T + rows - 1) / rows;
   return align256((size_t)(B * H * T) * sizeof(float2)) + align256((size_t)(B * H * cpitch) * sizeof(float2)) +
          (size_t)(B * H * n_chunks * cpitch) * sizeof(float2);
 }
@@ -803,6 +850,7 @@ size_t dtw_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A) {
 void dtw_workspace_layout(void* ws, DtwArgs* a) {
   char* p = static_cast<char*>(ws);
   a->cpitch = (a->A + 3) & ~3;
+  a->rc_rows = dtw_chunk_rows(a->B, a->H, a->T);
   const int64_t bh = (int64_t)a->B * a->H;
   a->rs = reinterpret_cast<float2*>(p);
   p += align256((size_t)(bh * a->T) * sizeof(float2));
@@ -818,8 +866,8 @@ hipError_t launch_dtw_prep(DtwArgs a, hipStream_t stream) {
           a.ws[2] % 4 == 0;
   // Columns the filter reads: [0, min(A, C + pad)).
   const int need = a.C + a.pad < a.A ? a.C + a.pad : a.A;
-  if (a.vec && a.A <= 2048) {
-    const dim3 grid((a.T + kRcRows - 1) / kRcRows, a.H, a.B);
+  if (a.vec && a.A % 4 == 0 && a.A <= 2048) {
+    const dim3 grid((a.T + a.rc_rows - 1) / a.rc_rows, a.H, a.B);
     if (a.A <= 512) hipLaunchKernelGGL(dtw_rowcol_kernel<2>, grid, dim3(256), 0, stream, a);
     else if (a.A <= 1024) hipLaunchKernelGGL(dtw_rowcol_kernel<4>, grid, dim3(256), 0, stream, a);
     else if (a.A <= 1536) hipLaunchKernelGGL(dtw_rowcol_kernel<6>, grid, dim3(256), 0, stream, a);
@@ -832,14 +880,22 @@ hipError_t launch_dtw_prep(DtwArgs a, hipStream_t stream) {
     hipLaunchKernelGGL(dtw_col_stats_kernel, dim3((need + kColBlock - 1) / kColBlock, a.H, a.B), dim3(512), 0,
                        stream, a);
   }
-  if (a.vec && a.A <= 4 * kBandMaxA4) {
+  if (a.vec && a.A % 4 == 0 && a.A <= 4 * kBandMaxA4 && a.H <= kBandMaxHeads) {
     const dim3 grid((a.T + kBandRows - 1) / kBandRows, a.B);
+    const int nt = 128 * ((((a.A + 3) / 4) + 127) / 128);  // one float4 column per thread
+    if (a.pad == 3) {  // the reference's width 7: a block size per width of the audio axis
+      if (nt == 128) hipLaunchKernelGGL((dtw_band_kernel<3, 128>), grid, dim3(128), 0, stream, a);
+      else if (nt == 256) hipLaunchKernelGGL((dtw_band_kernel<3, 256>), grid, dim3(256), 0, stream, a);
+      else if (nt == 384) hipLaunchKernelGGL((dtw_band_kernel<3, 384>), grid, dim3(384), 0, stream, a);
+      else hipLaunchKernelGGL((dtw_band_kernel<3, 512>), grid, dim3(512), 0, stream, a);
+      return hipGetLastError();
+    }
     switch (a.pad) {
 #define WDRZ_BAND(P) \
   case P:            \
-    hipLaunchKernelGGL(dtw_band_kernel<P>, grid, dim3(256), 0, stream, a); \
+    hipLaunchKernelGGL((dtw_band_kernel<P, 512>), grid, dim3(512), 0, stream, a); \
     break;
-      WDRZ_BAND(0) WDRZ_BAND(1) WDRZ_BAND(2) WDRZ_BAND(3) WDRZ_BAND(4) WDRZ_BAND(5) WDRZ_BAND(6) WDRZ_BAND(7)
+      WDRZ_BAND(0) WDRZ_BAND(1) WDRZ_BAND(2) WDRZ_BAND(4) WDRZ_BAND(5) WDRZ_BAND(6) WDRZ_BAND(7)
 #undef WDRZ_BAND
       default:
         return hipErrorInvalidValue;

@@ -63,7 +63,8 @@ struct DtwArgs {
   float2* cs;           // workspace: per-column (mean, 1/std), row pitch cpitch
   float2* part;         // workspace: per-64-row-chunk column partials (mean, M2), pitch cpitch
   int B, H, T, A, C, pad;
-  int cpitch;  // A rounded up to a multiple of 4
+  int cpitch;   // A rounded up to a multiple of 4
+  int rc_rows;  // rows per chunk of the fused statistics pass
   int vec;     // rows of W start 16-byte aligned (set by the launcher)
   int64_t ws[3];  // W strides b, h, t
   int64_t os[2];  // out strides b, t
