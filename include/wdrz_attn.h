@@ -123,6 +123,28 @@ int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, co
                       size_t workspace_bytes, void* stream);
 
 /*
+ * Raw cross-attention scores of the DTW alignment heads.
+ *
+ * Replaces: CrossAttnCapture.compute_attention(head_mask) (src/whisperdrz/dtw_align.py:553-586):
+ *           S[b, h, t, a] = sum_d (Q_h[b, t, d] * scale) * (K_h[b, a, d] * scale), no softmax,
+ *           scale = head_dim^-0.25 (dtw_align.py:561), fp32 result.
+ *
+ * q_heads[h]: device pointer to head h's query slice of the captured cross_attn.query output of
+ *             its layer (e.g. q_out[layer] + head*64 elements); rows (b, t) at
+ *             q_heads[h] + b*q_strides[0] + t*q_strides[1], the head_dim elements contiguous
+ *             (q_strides[2] == 1). Same for k_heads / k_strides over the 1500 audio rows.
+ *             q_heads and k_heads are HOST arrays of H device pointers; all heads share the
+ *             strides. bf16 or fp16 (the reference's GPU model dtype); 16-byte aligned.
+ * out:        fp32 [B, H, T, A], strides out_strides[4] (last one 1). The reference returns
+ *             [H, T, A] when B == 1; callers lift it back to 4-D (dtw_align.py:1185-1187).
+ * H <= 32, head_dim 64.
+ */
+int wdrz_dtw_qk(int dtype, const void* const* q_heads, const int64_t* q_strides,
+                const void* const* k_heads, const int64_t* k_strides, float* out,
+                const int64_t* out_strides, int64_t B, int64_t H, int64_t T, int64_t A,
+                int64_t D, float scale, void* stream);
+
+/*
  * Workspace (bytes) that wdrz_dtw_prep needs: one (max, 1/sum) pair per score row and one
  * (mean, 1/std) pair per score column, 8 * B*H*(T + A) bytes plus alignment.
  * No counterpart in the reference: torch allocates the intermediates of _dtw_prep_batch itself.

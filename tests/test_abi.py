@@ -161,3 +161,33 @@ def test_dtw_workspace_size(lib):
     # B*H*chunks <= 768: 4 chunks of 112 rows here), each 256-byte aligned
     assert n == 8 * B * H * (T + A + 4 * A)
     assert lib.wdrz_dtw_prep_workspace_size(0, H, T, A) == 0
+
+
+def call_qk(lib, **over):
+    H = over.pop("H", 2)
+    ptrs = (ctypes.c_void_p * max(H, 1))(*([FAKE] * max(H, 1)))
+    args = dict(dtype=2, q=ptrs, qs=(ctypes.c_int64 * 3)(40 * 1280, 1280, 1), k=ptrs,
+                ks=(ctypes.c_int64 * 3)(1500 * 1280, 1280, 1), out=FAKE,
+                os_=_strides(H * 40 * 1500, 40 * 1500, 1500, 1), B=1, T=40, A=1500, D=64, scale=64 ** -0.25)
+    args.update(over)
+    return lib.wdrz_dtw_qk(args["dtype"], args["q"], args["qs"], args["k"], args["ks"], args["out"], args["os_"],
+                           args["B"], H, args["T"], args["A"], args["D"], args["scale"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(dtype=0), 2, "only WDRZ_BF16 / WDRZ_F16"),
+    (dict(dtype=9), 1, "only WDRZ_BF16 / WDRZ_F16"),
+    (dict(D=128), 2, "head_dim"),
+    (dict(H=33), 2, "exceed the supported 32"),
+    (dict(qs=(ctypes.c_int64 * 3)(40 * 1280, 1283, 1)), 1, "not 16-byte aligned"),
+    (dict(ks=(ctypes.c_int64 * 3)(1500 * 1280, 1280, 2)), 1, "head_dim stride"),
+    (dict(out=None), 1, "out is NULL"),
+    (dict(scale=0.0), 1, "scale"),
+])
+def test_dtw_qk_rejects_bad_arguments(lib, over, code, msg):
+    assert call_qk(lib, **over) == code
+    assert msg in lib.wdrz_last_error().decode()
+
+
+def test_dtw_qk_empty_is_a_no_op(lib):
+    assert call_qk(lib, B=0) == 0

@@ -124,3 +124,80 @@ def test_bench_shape_matches_torch_ops(cuda):
     torch.cuda.synchronize()
     err = (out - ref).abs().max().item()
     assert err <= 1e-4 * ref.abs().max().item(), err
+
+
+# ---- CrossAttnCapture.compute_attention (dtw_align.py:553-586) ----------------------------
+
+
+def _captures(B, T, A, n_layers, n_heads, dtype, seed):
+    """Per-layer query / key projections as the capture hooks hold them ([B, T, n_heads*64])."""
+    g = torch.Generator().manual_seed(seed)
+    q_out = [torch.randn(B, T, n_heads * 64, generator=g).to(dtype) for _ in range(n_layers)]
+    k_out = [torch.randn(B, A, n_heads * 64, generator=g).to(dtype) for _ in range(n_layers)]
+    return q_out, k_out
+
+
+def _qk_ref(q_out, k_out, head_mask, n_heads):
+    from oracle.dtw_oracle import compute_attention_ref
+
+    sel = head_mask.nonzero().tolist()
+    qh = np.stack([q_out[l].float().view(q_out[l].shape[0], q_out[l].shape[1], n_heads, 64)[:, :, h].numpy()
+                   for l, h in sel])
+    kh = np.stack([k_out[l].float().view(k_out[l].shape[0], k_out[l].shape[1], n_heads, 64)[:, :, h].numpy()
+                   for l, h in sel])
+    return compute_attention_ref(qh, kh, 64)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,T,A", [(2, 37, 1500), (3, 64, 203), (1, 5, 70)])
+def test_compute_attention(cuda, dtype, B, T, A):
+    from whisperdrz_amd import compute_attention
+
+    n_layers, n_heads = 6, 20
+    q_out, k_out = _captures(B, T, A, n_layers, n_heads, dtype, seed=B * 100 + T + A)
+    head_mask = torch.zeros(n_layers, n_heads, dtype=torch.bool)
+    for l, h in [(1, 0), (1, 17), (3, 5), (4, 19), (5, 2), (5, 11)]:
+        head_mask[l, h] = True
+    print(f"compute_attention {dtype} B={B} T={T} A={A}", flush=True)
+    got = compute_attention([q.to(cuda) for q in q_out], [k.to(cuda) for k in k_out], head_mask)
+    torch.cuda.synchronize()
+    ref = _qk_ref(q_out, k_out, head_mask, n_heads)
+    if B == 1:
+        assert got.dim() == 3  # the reference drops the batch axis for one chunk
+        ref = ref[0]
+    _check(got, ref, f"compute_attention {dtype} B={B} T={T} A={A}")
+
+
+def test_compute_attention_mixed_layouts_and_prep_chain(cuda):
+    # one layer's projection is a column slice of a wider tensor (other strides): the heads are
+    # given one layout; then the scores go through the prep, against the oracle chain
+    from whisperdrz_amd import compute_attention, dtw_prep
+    from oracle.dtw_oracle import dtw_prep_ref
+
+    B, T, A, n_layers, n_heads = 2, 40, 1500, 3, 20
+    q_out, k_out = _captures(B, T, A, n_layers, n_heads, torch.bfloat16, seed=77)
+    wide = torch.randn(B, T, 2 * n_heads * 64, generator=torch.Generator().manual_seed(78)).to(torch.bfloat16)
+    q_out[2] = wide[:, :, : n_heads * 64]
+    head_mask = torch.zeros(n_layers, n_heads, dtype=torch.bool)
+    head_mask[0, 3] = head_mask[2, 7] = head_mask[2, 8] = True
+    print("compute_attention mixed layouts + prep", flush=True)
+    dev_q = [q.to(cuda) if i != 2 else wide.to(cuda)[:, :, : n_heads * 64] for i, q in enumerate(q_out)]
+    got = compute_attention(dev_q, [k.to(cuda) for k in k_out], head_mask)
+    ref = _qk_ref([q.contiguous() for q in q_out], k_out, head_mask, n_heads)
+    _check(got, ref, "compute_attention mixed layouts")
+    lens, caps = [40, 23], [1500, 1211]
+    out = dtw_prep(got, lens, caps)
+    torch.cuda.synchronize()
+    _check(out, dtw_prep_ref(got.cpu().numpy(), lens, caps, 7), "prep of computed scores")
+
+
+def test_compute_attention_rejects(cuda):
+    from whisperdrz_amd import compute_attention
+
+    q_out, k_out = _captures(1, 4, 8, 1, 20, torch.float32, seed=1)
+    mask = torch.zeros(1, 20, dtype=torch.bool)
+    with pytest.raises(ValueError):
+        compute_attention([q_out[0].to(cuda)], [k_out[0].to(cuda)], mask)  # no heads selected
+    mask[0, 0] = True
+    with pytest.raises(TypeError):
+        compute_attention([q_out[0].to(cuda)], [k_out[0].to(cuda)], mask)  # fp32 projections

@@ -13,12 +13,13 @@ from .attention import (
     qkv_attention,
     scaled_dot_product_attention,
 )
-from .dtw import dtw_prep, dtw_prep_batch, dtw_prep_workspace_size
+from .dtw import compute_attention, dtw_prep, dtw_prep_batch, dtw_prep_workspace_size
 
 HAS_WDRZ = _lib.available()
 
 __all__ = [
     "HAS_WDRZ",
+    "compute_attention",
     "dtw_prep",
     "dtw_prep_batch",
     "dtw_prep_workspace_size",

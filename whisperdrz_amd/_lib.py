@@ -21,6 +21,7 @@ EXPORTED_SYMBOLS = (
     "wdrz_attn_fwd",
     "wdrz_attn_kvcache_workspace_size",
     "wdrz_attn_kvcache",
+    "wdrz_dtw_qk",
     "wdrz_dtw_prep_workspace_size",
     "wdrz_dtw_prep",
 )
@@ -59,6 +60,13 @@ def _declare(lib: ctypes.CDLL) -> None:
         ctypes.c_float, ctypes.c_int,  # softmax_scale, causal
         _p, ctypes.c_size_t, _p,  # workspace, bytes, stream
     ]
+    lib.wdrz_dtw_qk.restype = ctypes.c_int
+    lib.wdrz_dtw_qk.argtypes = [
+        ctypes.c_int, _p, _i64p, _p, _i64p,  # dtype, q_heads (host array), q strides, k_heads, k strides
+        _p, _i64p,  # out, out strides
+        _i64, _i64, _i64, _i64, _i64,  # B, H, T, A, D
+        ctypes.c_float, _p,  # scale, stream
+    ]
     lib.wdrz_dtw_prep_workspace_size.restype = ctypes.c_size_t
     lib.wdrz_dtw_prep_workspace_size.argtypes = [_i64, _i64, _i64, _i64]
     lib.wdrz_dtw_prep.restype = ctypes.c_int
@@ -88,7 +96,11 @@ def load() -> ctypes.CDLL:
         except OSError as exc:  # pragma: no cover - depends on the environment
             _load_error = f"failed to load {LIB_PATH}: {exc}"
             raise RuntimeError(_load_error) from exc
-        _declare(lib)
+        try:
+            _declare(lib)
+        except AttributeError as exc:  # a library built from older sources
+            _load_error = f"{LIB_PATH} lacks {exc}; rebuild it (python -m whisperdrz_amd.build)"
+            raise RuntimeError(_load_error) from exc
         if lib.wdrz_abi_version() != ABI_VERSION:
             raise RuntimeError(
                 f"{LIB_PATH} has ABI {lib.wdrz_abi_version()}, expected {ABI_VERSION}; rebuild it"

@@ -18,7 +18,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libwdrz_attn.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["attn_kvcache.hip", "attn_dense.hip", "dtw_prep.hip", "wdrz_capi.cpp"]
+SOURCES = ["attn_kvcache.hip", "attn_dense.hip", "dtw_prep.hip", "dtw_qk.hip", "wdrz_capi.cpp"]
 ARCH = "gfx950"
 
 
@@ -51,6 +51,7 @@ def build_library(debug: bool = False, verbose: bool = False) -> Path:
         "attn_dense.hip": ["-fno-honor-nans"],
         "attn_kvcache.hip": ["-fno-honor-nans"],
         "dtw_prep.hip": ["-fno-honor-nans"],  # NaN outputs are written explicitly, never computed
+        "dtw_qk.hip": ["-fno-honor-nans"],
     }
     objs = []
     for src in SOURCES:

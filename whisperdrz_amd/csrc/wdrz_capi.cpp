@@ -224,6 +224,53 @@ int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, co
   return WDRZ_OK;
 }
 
+int wdrz_dtw_qk(int dtype, const void* const* q_heads, const int64_t* q_strides, const void* const* k_heads,
+                const int64_t* k_strides, float* out, const int64_t* out_strides, int64_t B, int64_t H, int64_t T,
+                int64_t A, int64_t D, float scale, void* stream) {
+  g_last_error.clear();
+  if (dtype != WDRZ_BF16 && dtype != WDRZ_F16)
+    return fail(dtype == WDRZ_F32 ? WDRZ_EUNSUPPORTED : WDRZ_EINVAL,
+                "dtype %d: only WDRZ_BF16 / WDRZ_F16 projections are supported", dtype);
+  if (D != 64) return fail(WDRZ_EUNSUPPORTED, "head_dim %lld is not supported (only 64)", (long long)D);
+  if (B < 0 || H <= 0 || T < 0 || A < 0)
+    return fail(WDRZ_EINVAL, "bad sizes B=%lld H=%lld T=%lld A=%lld", (long long)B, (long long)H, (long long)T,
+                (long long)A);
+  if (H > wdrz::kDtwMaxHeads)
+    return fail(WDRZ_EUNSUPPORTED, "%lld heads exceed the supported %d", (long long)H, wdrz::kDtwMaxHeads);
+  if (B * H > 65535 || T > (1 << 24) || A > (1 << 24)) return fail(WDRZ_EUNSUPPORTED, "sizes too large");
+  if (!(scale > 0.f) || scale != scale) return fail(WDRZ_EINVAL, "scale must be a positive finite number");
+  if (!q_heads || !k_heads) return fail(WDRZ_EINVAL, "q_heads / k_heads is NULL");
+  if (!q_strides || !k_strides || !out_strides) return fail(WDRZ_EINVAL, "strides pointer is NULL");
+  if (!out) return fail(WDRZ_EINVAL, "out is NULL");
+  if (q_strides[2] != 1 || k_strides[2] != 1) return fail(WDRZ_EINVAL, "q/k: head_dim stride must be 1");
+  if (out_strides[3] != 1) return fail(WDRZ_EINVAL, "out: last stride must be 1");
+  for (int i = 0; i < 2; ++i)
+    if (((q_strides[i] * 2) & 15) || ((k_strides[i] * 2) & 15))
+      return fail(WDRZ_EINVAL, "q/k: stride[%d] is not 16-byte aligned", i);
+  wdrz::DtwQkArgs a{};
+  for (int64_t h = 0; h < H; ++h) {
+    int rc;
+    if ((rc = check_ptr("q_heads[h]", q_heads[h])) || (rc = check_ptr("k_heads[h]", k_heads[h]))) return rc;
+    a.q[h] = q_heads[h];
+    a.k[h] = k_heads[h];
+  }
+  if (B == 0 || T == 0 || A == 0) return WDRZ_OK;
+  a.out = out;
+  a.B = (int)B;
+  a.H = (int)H;
+  a.T = (int)T;
+  a.A = (int)A;
+  a.qs[0] = q_strides[0];
+  a.qs[1] = q_strides[1];
+  a.ks[0] = k_strides[0];
+  a.ks[1] = k_strides[1];
+  for (int i = 0; i < 3; ++i) a.os[i] = out_strides[i];
+  a.scale2 = scale * scale;
+  hipError_t err = wdrz::launch_dtw_qk(dtype, a, reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(WDRZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  return WDRZ_OK;
+}
+
 size_t wdrz_dtw_prep_workspace_size(int64_t B, int64_t H, int64_t T, int64_t A) {
   if (B <= 0 || H <= 0 || T <= 0 || A <= 0) return 0;
   return wdrz::dtw_workspace_bytes(B, H, T, A);

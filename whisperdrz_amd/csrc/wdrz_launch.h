@@ -69,6 +69,20 @@ struct DtwArgs {
   int64_t ws[3];  // W strides b, h, t
   int64_t os[2];  // out strides b, t
 };
+// Raw Q K^T of the alignment heads (bf16 / fp16 in, fp32 out). Q head h: rows (b, t) at
+// q[h] + b*qs[0] + t*qs[1] (elements, head dims contiguous); K likewise with a for t.
+constexpr int kDtwMaxHeads = 32;
+struct DtwQkArgs {
+  const void* q[kDtwMaxHeads];
+  const void* k[kDtwMaxHeads];
+  float* out;  // [B, H, T, A]
+  int B, H, T, A;
+  int64_t qs[2], ks[2];  // b, row strides
+  int64_t os[3];         // b, h, t strides of out
+  float scale2;          // (head_dim^-0.25)^2 as the product of the two fp32 scales
+};
+hipError_t launch_dtw_qk(int dtype, const DtwQkArgs& a, hipStream_t stream);
+
 size_t dtw_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A);
 void dtw_workspace_layout(void* ws, DtwArgs* a);
 hipError_t launch_dtw_prep(DtwArgs a, hipStream_t stream);

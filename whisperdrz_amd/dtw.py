@@ -1,6 +1,10 @@
-"""DTW alignment prep on the GPU, backed by the gfx950 kernels in libwdrz_attn.so.
+"""DTW alignment inputs on the GPU, backed by the gfx950 kernels in libwdrz_attn.so.
 
-Mirrors the reference's batched prep ``_dtw_prep_batch(full_weights, actual_lens, audio_caps,
+:func:`compute_attention` mirrors ``CrossAttnCapture.compute_attention(head_mask)``
+(``src/whisperdrz/dtw_align.py:553-586``): the raw Q K^T of the selected alignment heads, read in
+place from the captured per-layer query / key projections.
+
+:func:`dtw_prep_batch` mirrors the reference's batched prep ``_dtw_prep_batch(full_weights, actual_lens, audio_caps,
 medfilt_width=7)`` (``src/whisperdrz/dtw_align.py:700-753``): capped row softmax, column
 mean/std normalisation over each chunk's valid text rows, width-``medfilt_width`` median filter
 along the audio axis (reflect padding), mean over the alignment heads, slice to the largest cap,
@@ -18,12 +22,66 @@ import torch
 from . import _lib
 from .attention import WorkspaceCache, _check_cuda, _raise, _stream_handle
 
-__all__ = ["dtw_prep", "dtw_prep_batch", "dtw_prep_workspace_size"]
+__all__ = ["compute_attention", "dtw_prep", "dtw_prep_batch", "dtw_prep_workspace_size"]
+
+_QK_DTYPES = {torch.bfloat16: _lib.WDRZ_BF16, torch.float16: _lib.WDRZ_F16}
 
 # The prep's workspace holds no state between calls; it is kept apart from the split-KV
 # workspace, whose counters must stay zero.
 _DTW_WORKSPACES = WorkspaceCache()
 _PINNED: dict[tuple, torch.Tensor] = {}
+
+
+def compute_attention(q_out, k_out, head_mask) -> torch.Tensor:
+    """Drop-in for ``CrossAttnCapture.compute_attention`` (dtw_align.py:553-586).
+
+    q_out / k_out: the captured ``cross_attn.query`` / ``cross_attn.key`` outputs per decoder
+    layer (``[B, T_text, n_heads*64]`` / ``[B, T_audio, n_heads*64]``, bf16 or fp16 on the GPU;
+    ``None`` for layers without a selected head). head_mask: bool ``[n_layers, n_heads]``.
+    Returns fp32 ``[B, n_selected, T_text, T_audio]``, or ``[n_selected, T_text, T_audio]`` when
+    B == 1, as the reference does. Each head's slice is read in place; no stacked copies.
+    """
+    mask = torch.as_tensor(head_mask)
+    n_heads = int(mask.shape[1])
+    sel = mask.nonzero().tolist()
+    if not sel:
+        raise ValueError("head_mask selects no heads")
+    q_views, k_views = [], []
+    for layer, head in sel:
+        q, k = q_out[layer], k_out[layer]
+        if q is None or k is None:
+            raise ValueError(f"layer {layer} has no captured projection")
+        B, T, width = q.shape
+        D = width // n_heads
+        q_views.append(q.view(B, T, n_heads, D)[:, :, head])
+        k_views.append(k.view(k.shape[0], k.shape[1], n_heads, D)[:, :, head])
+    q0, k0 = q_views[0], k_views[0]
+    device = q0.device
+    _check_cuda("q_out", q0, device)
+    if q0.dtype not in _QK_DTYPES:
+        raise TypeError(f"q_out: dtype {q0.dtype} is not supported (bfloat16, float16)")
+    B, T, D = (int(x) for x in q0.shape)
+    A = int(k0.shape[1])
+    same = all(v.stride() == q0.stride() and v.dtype == q0.dtype and v.device == device for v in q_views) and all(
+        v.stride() == k0.stride() and v.dtype == q0.dtype and v.device == device and v.shape[1] == A
+        for v in k_views
+    )
+    if not same:  # heads from differently laid-out captures: give them one layout
+        q_views = [v.contiguous() for v in q_views]
+        k_views = [v.to(q0.dtype).contiguous() for v in k_views]
+    H = len(sel)
+    out = torch.empty((B, H, T, A), dtype=torch.float32, device=device)
+    qp = (_lib.ctypes.c_void_p * H)(*[v.data_ptr() for v in q_views])
+    kp = (_lib.ctypes.c_void_p * H)(*[v.data_ptr() for v in k_views])
+    qs = (_lib.ctypes.c_int64 * 3)(*q_views[0].stride())
+    ks = (_lib.ctypes.c_int64 * 3)(*k_views[0].stride())
+    rc = _lib.load().wdrz_dtw_qk(
+        _QK_DTYPES[q0.dtype], qp, qs, kp, ks, out.data_ptr(), _lib.strides4(out.stride()),
+        B, H, T, A, D, float(D) ** -0.25, _stream_handle(),
+    )
+    if rc != _lib.WDRZ_OK:
+        _raise(rc, "compute_attention")
+    return out[0] if B == 1 else out
 
 
 def dtw_prep_workspace_size(B: int, H: int, T: int, A: int) -> int:
