@@ -312,6 +312,7 @@ def bench_dtw(dev, steps: int, warmup: int) -> dict:
     log(f"[bench] dtw prep: torch op sequence on the GPU {ms_torch * 1e3:.0f} us ({ms_torch / ms:.1f}x)")
     del inputs, outs
     torch.cuda.empty_cache()
+    qk = bench_dtw_qk(dev, steps, warmup)
     return {
         "workload": f"_dtw_prep_batch: B={DTW_B} chunks x H={DTW_H} alignment heads x T_text={DTW_T} x "
         f"T_audio={DTW_A} fp32 scores, caps={DTW_A}, lens ~ U[{DTW_T // 2},{DTW_T}], median width 7; "
@@ -330,6 +331,62 @@ def bench_dtw(dev, steps: int, warmup: int) -> dict:
             "kernels": list(DTW_KERNELS),
         },
         "torch_ops_gpu_us": round(ms_torch * 1e3, 1),
+        "compute_attention": qk,
+    }
+
+
+# large-v3 alignment heads (layer, head), decoded from the reference's LARGE_V3_ALIGNMENT_HEADS
+# bitmask (dtw_align.py:43-60): one head in each of 10 layers.
+DTW_HEADS = [(7, 0), (10, 17), (12, 18), (13, 12), (16, 1), (17, 14), (19, 11), (21, 4), (24, 1), (25, 6)]
+
+
+def bench_dtw_qk(dev, steps: int, warmup: int) -> dict:
+    """compute_attention at the bench shape: the 10 alignment heads' Q/K slices read in place from
+    per-layer captures [16, 448, 1280] / [16, 1500, 1280] bf16, fp32 scores written."""
+    from whisperdrz_amd import compute_attention
+
+    n_layers, n_heads = 32, H
+    mask = torch.zeros(n_layers, n_heads, dtype=torch.bool)
+    for l, h in DTW_HEADS:
+        mask[l, h] = True
+    g = torch.Generator(device=dev).manual_seed(6000)
+    q_out = [None] * n_layers
+    k_out = [None] * n_layers
+    for l, _ in DTW_HEADS:
+        q_out[l] = torch.randn((DTW_B, DTW_T, n_heads * D), generator=g, device=dev).to(torch.bfloat16)
+        k_out[l] = torch.randn((DTW_B, DTW_A, n_heads * D), generator=g, device=dev).to(torch.bfloat16)
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        compute_attention(q_out, k_out, mask)
+    ms = timed_events(lambda: compute_attention(q_out, k_out, mask), steps, stream)
+    nbytes = 4 * DTW_B * DTW_H * DTW_T * DTW_A + 2 * DTW_B * DTW_H * (DTW_T + DTW_A) * D
+    gbs = nbytes / (ms * 1e-3) / 1e9
+
+    def torch_ref():  # the reference's gather + fp32 batched matmul (dtw_align.py:565-585)
+        s = D ** -0.25
+        qs = torch.stack([q_out[l].view(DTW_B, DTW_T, n_heads, D)[:, :, h] for l, h in DTW_HEADS]).float() * s
+        ks = torch.stack([k_out[l].view(DTW_B, DTW_A, n_heads, D)[:, :, h] for l, h in DTW_HEADS]).float() * s
+        return (qs @ ks.transpose(-1, -2)).transpose(0, 1).contiguous()
+
+    torch_ref()
+    ms_torch = timed_events(torch_ref, 3, stream)
+    log(f"[bench] compute_attention: {ms * 1e3:.1f} us, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM); "
+        f"torch gather + fp32 matmul {ms_torch * 1e3:.0f} us")
+    del q_out, k_out
+    torch.cuda.empty_cache()
+    return {
+        "us": round(ms * 1e3, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4),
+            "traffic": measured_traffic("dtw_qk_kernel<wdrz::Bf16>"),
+            "bytes_per_call": nbytes,
+            "kernel": "dtw_qk_kernel<Bf16>",
+        },
+        "torch_gpu_us": round(ms_torch * 1e3, 1),
     }
 
 

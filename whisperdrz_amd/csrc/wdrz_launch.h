@@ -80,8 +80,9 @@ struct DtwQkArgs {
   int64_t qs[2], ks[2];  // b, row strides
   int64_t os[3];         // b, h, t strides of out
   float scale2;          // (head_dim^-0.25)^2 as the product of the two fp32 scales
+  int vec;               // out rows 16-byte aligned (set by the launcher)
 };
-hipError_t launch_dtw_qk(int dtype, const DtwQkArgs& a, hipStream_t stream);
+hipError_t launch_dtw_qk(int dtype, DtwQkArgs a, hipStream_t stream);
 
 size_t dtw_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A);
 void dtw_workspace_layout(void* ws, DtwArgs* a);
