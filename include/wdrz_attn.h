@@ -123,6 +123,31 @@ int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, co
                       size_t workspace_bytes, void* stream);
 
 /*
+ * Workspace (bytes) for wdrz_log_mel: the [202, n_mels] filterbank and one maximum per window.
+ * No counterpart in the reference (torchaudio keeps the filterbank in a module buffer).
+ */
+size_t wdrz_log_mel_workspace_size(int64_t B, int64_t n_mels);
+
+/*
+ * Whisper log-mel spectrogram of B waveforms.
+ *
+ * Replaces: LogMelSpectrogram.forward / _process_single_audio (src/whisperdrz/audio.py:108-156),
+ *           which the reference computes on the CPU per 30-s window (transcriber.py:1091-1092).
+ *           torch.stft(n_fft 400, hop 160, periodic Hann, center, reflect) -> |X|^2 without the
+ *           last frame -> slaney mel filterbank -> log10(max(., 1e-10)) -> max(., max - 8) over
+ *           each window -> (x + 4) / 4 -> pad with -1.5 or truncate to out_frames.
+ *
+ * audio:      fp32 [B, n_samples], row stride audio_stride (elements); n_samples > 200.
+ * out:        fp32 [B, n_mels, out_frames], strides out_strides[3] (frame stride 1).
+ * out_frames: the reference's target_frames, or -1 for n_samples / 160 frames (no padding).
+ * n_mels <= 128 (Whisper uses 80 or 128). workspace: wdrz_log_mel_workspace_size(B, n_mels)
+ * bytes, 256-byte aligned; no state is kept in it between calls.
+ */
+int wdrz_log_mel(const float* audio, int64_t B, int64_t n_samples, int64_t audio_stride,
+                 float* out, const int64_t* out_strides, int64_t n_mels, int64_t out_frames,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Raw cross-attention scores of the DTW alignment heads.
  *
  * Replaces: CrossAttnCapture.compute_attention(head_mask) (src/whisperdrz/dtw_align.py:553-586):

@@ -191,3 +191,19 @@ def test_dtw_qk_rejects_bad_arguments(lib, over, code, msg):
 
 def test_dtw_qk_empty_is_a_no_op(lib):
     assert call_qk(lib, B=0) == 0
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(n=200), 1, "reflect padding"),
+    (dict(n_mels=129), 2, "exceeds the supported 128"),
+    (dict(audio=None), 1, "is NULL"),
+    (dict(), 4, "workspace"),
+])
+def test_log_mel_rejects_bad_arguments(lib, over, code, msg):
+    args = dict(audio=FAKE, B=2, n=480000, stride=480000, out=FAKE, n_mels=128, frames=3000)
+    args.update(over)
+    os3 = (ctypes.c_int64 * 3)(args["n_mels"] * 3000, 3000, 1)
+    rc = lib.wdrz_log_mel(args["audio"], args["B"], args["n"], args["stride"], args["out"], os3, args["n_mels"],
+                          args["frames"], None, 0, None)
+    assert rc == code
+    assert msg in lib.wdrz_last_error().decode()

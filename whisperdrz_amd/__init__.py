@@ -2,8 +2,8 @@
 
 Drop-in entry points for the reference's two attention seams (src/whisperdrz/model.py:88-95 and
 model.py:288-296), backed by hand-written HIP kernels in libwdrz_attn.so, plus the slot KV cache
-(model.py:98-192), the decode-step plumbing around them, and the DTW alignment prep
-(dtw_align.py:700-753).
+(model.py:98-192), the decode-step plumbing around them, the DTW alignment inputs
+(dtw_align.py:553-586, 700-753) and the log-mel front end (audio.py:81-156).
 """
 from . import _lib
 from .attention import (
@@ -13,12 +13,15 @@ from .attention import (
     qkv_attention,
     scaled_dot_product_attention,
 )
+from .audio import LogMelSpectrogram, log_mel_spectrogram
 from .dtw import compute_attention, dtw_prep, dtw_prep_batch, dtw_prep_workspace_size
 
 HAS_WDRZ = _lib.available()
 
 __all__ = [
     "HAS_WDRZ",
+    "LogMelSpectrogram",
+    "log_mel_spectrogram",
     "compute_attention",
     "dtw_prep",
     "dtw_prep_batch",

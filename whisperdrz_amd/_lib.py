@@ -21,6 +21,8 @@ EXPORTED_SYMBOLS = (
     "wdrz_attn_fwd",
     "wdrz_attn_kvcache_workspace_size",
     "wdrz_attn_kvcache",
+    "wdrz_log_mel_workspace_size",
+    "wdrz_log_mel",
     "wdrz_dtw_qk",
     "wdrz_dtw_prep_workspace_size",
     "wdrz_dtw_prep",
@@ -59,6 +61,13 @@ def _declare(lib: ctypes.CDLL) -> None:
         _i64p, _i64p, _i64p, _i64p, _i64p, _i64p,  # strides
         ctypes.c_float, ctypes.c_int,  # softmax_scale, causal
         _p, ctypes.c_size_t, _p,  # workspace, bytes, stream
+    ]
+    lib.wdrz_log_mel_workspace_size.restype = ctypes.c_size_t
+    lib.wdrz_log_mel_workspace_size.argtypes = [_i64, _i64]
+    lib.wdrz_log_mel.restype = ctypes.c_int
+    lib.wdrz_log_mel.argtypes = [
+        _p, _i64, _i64, _i64, _p, _i64p,  # audio, B, n_samples, audio_stride, out, out strides
+        _i64, _i64, _p, ctypes.c_size_t, _p,  # n_mels, out_frames, workspace, bytes, stream
     ]
     lib.wdrz_dtw_qk.restype = ctypes.c_int
     lib.wdrz_dtw_qk.argtypes = [

@@ -271,6 +271,49 @@ int wdrz_dtw_qk(int dtype, const void* const* q_heads, const int64_t* q_strides,
   return WDRZ_OK;
 }
 
+size_t wdrz_log_mel_workspace_size(int64_t B, int64_t n_mels) {
+  if (B <= 0 || n_mels <= 0) return 0;
+  return wdrz::logmel_workspace_bytes(B, n_mels);
+}
+
+int wdrz_log_mel(const float* audio, int64_t B, int64_t n_samples, int64_t audio_stride, float* out,
+                 const int64_t* out_strides, int64_t n_mels, int64_t out_frames, void* workspace,
+                 size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  if (B < 0 || n_mels <= 0) return fail(WDRZ_EINVAL, "bad sizes B=%lld n_mels=%lld", (long long)B, (long long)n_mels);
+  if (n_mels > 128) return fail(WDRZ_EUNSUPPORTED, "n_mels=%lld exceeds the supported 128", (long long)n_mels);
+  if (n_samples <= 200)
+    return fail(WDRZ_EINVAL, "n_samples=%lld: the reflect padding of 200 needs more samples (as torch.stft)",
+                (long long)n_samples);
+  if (n_samples > (1 << 30) || B > 65535) return fail(WDRZ_EUNSUPPORTED, "sizes too large");
+  if (!audio || !out || !out_strides) return fail(WDRZ_EINVAL, "audio / out / out_strides is NULL");
+  if (audio_stride < n_samples && B > 1) return fail(WDRZ_EINVAL, "audio_stride is smaller than n_samples");
+  if (out_strides[2] != 1) return fail(WDRZ_EINVAL, "out: frame stride must be 1");
+  const int64_t n_frames = n_samples / 160;
+  if (out_frames < 0) out_frames = n_frames;
+  if (out_frames > (1 << 24)) return fail(WDRZ_EUNSUPPORTED, "out_frames too large");
+  if (B == 0 || out_frames == 0) return WDRZ_OK;
+  const size_t need = wdrz::logmel_workspace_bytes(B, n_mels);
+  if (!workspace || workspace_bytes < need)
+    return fail(WDRZ_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace ? workspace_bytes : 0);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+    return fail(WDRZ_EINVAL, "workspace is not 256-byte aligned");
+  wdrz::LogMelArgs a{};
+  a.audio = audio;
+  a.audio_stride = audio_stride;
+  a.out = out;
+  a.os[0] = out_strides[0];
+  a.os[1] = out_strides[1];
+  a.B = (int)B;
+  a.n_samples = (int)n_samples;
+  a.n_mels = (int)n_mels;
+  a.n_frames = (int)n_frames;
+  a.out_frames = (int)out_frames;
+  hipError_t err = wdrz::launch_logmel(a, workspace, reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(WDRZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  return WDRZ_OK;
+}
+
 size_t wdrz_dtw_prep_workspace_size(int64_t B, int64_t H, int64_t T, int64_t A) {
   if (B <= 0 || H <= 0 || T <= 0 || A <= 0) return 0;
   return wdrz::dtw_workspace_bytes(B, H, T, A);

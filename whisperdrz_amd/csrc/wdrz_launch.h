@@ -84,6 +84,19 @@ struct DtwQkArgs {
 };
 hipError_t launch_dtw_qk(int dtype, DtwQkArgs a, hipStream_t stream);
 
+// Log-mel front end over fp32 waveforms [B, n_samples] (row stride audio_stride elements).
+struct LogMelArgs {
+  const float* audio;
+  int64_t audio_stride;
+  float* out;         // [B, n_mels, out_frames], frames contiguous
+  int64_t os[2];      // b, mel strides of out
+  float* fb;          // workspace: [202, n_mels] filterbank
+  uint32_t* gmax;     // workspace: [B] ordered-encoded window maxima
+  int B, n_samples, n_mels, n_frames, out_frames;
+};
+size_t logmel_workspace_bytes(int64_t B, int64_t n_mels);
+hipError_t launch_logmel(LogMelArgs a, void* ws, hipStream_t stream);
+
 size_t dtw_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A);
 void dtw_workspace_layout(void* ws, DtwArgs* a);
 hipError_t launch_dtw_prep(DtwArgs a, hipStream_t stream);
