@@ -9,10 +9,11 @@ The same line carries, under ``decode``, the decoder paths (configs 3, 4, 5) in 
 algorithmic HBM bytes (only valid K/V rows are counted), each with 32 distinct per-layer caches
 captured into one hipGraph and replayed, and under ``cpu_baseline`` the reference's CPU torch
 path (torch SDPA, fp32) timed on this host's cores on a bounded sample. Under ``dtw_prep`` it
-carries the DTW alignment prep (_dtw_prep_batch) in GB/s of algorithmic HBM bytes, with its own
-roofline and CPU baseline.
+carries the DTW alignment inputs (compute_attention and _dtw_prep_batch) in GB/s of algorithmic
+HBM bytes, and under ``log_mel`` the GPU log-mel front end in TFLOP/s of fp32 matrix work, each
+with its own roofline and CPU baseline.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only enc|dec|dtw]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only enc|dec|dtw|mel]
 """
 from __future__ import annotations
 
@@ -390,6 +391,79 @@ def bench_dtw_qk(dev, steps: int, warmup: int) -> dict:
     }
 
 
+# --------------------------------------------------------------------------------------------
+# log-mel front end (LogMelSpectrogram, audio.py:81-156)
+# --------------------------------------------------------------------------------------------
+
+MEL_B, MEL_N, MEL_MELS = 16, 480000, 128
+PEAK_FP32_TFLOPS = 157.3
+
+
+def mel_flop(n_frames: int) -> float:
+    """Algorithmic matrix-core work per window: the windowed DFT of the 201 kept bins (real and
+    imaginary parts, 400 samples) and the mel projection (201 bins -> 128 mels), 2 flops per MAC."""
+    return n_frames * (2.0 * 400 * 2 * 201 + 2.0 * 201 * MEL_MELS)
+
+
+def bench_logmel(dev, steps: int, warmup: int) -> dict:
+    from whisperdrz_amd import log_mel_spectrogram
+
+    g = torch.Generator(device=dev).manual_seed(7000)
+    audio = [0.1 * torch.randn((MEL_B, MEL_N), generator=g, device=dev) for _ in range(2)]
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        for x in audio:
+            log_mel_spectrogram(x, MEL_MELS, 3000)
+    ms = timed_events(lambda: [log_mel_spectrogram(x, MEL_MELS, 3000) for x in audio], steps, stream) / len(audio)
+    flop = MEL_B * mel_flop(MEL_N // 160)
+    tflops = flop / (ms * 1e-3) / 1e12
+    log(f"[bench] log-mel: {ms * 1e3:.1f} us per {MEL_B} x 30 s windows ({MEL_B / ms * 1e3:.0f} windows/s), "
+        f"{tflops:.1f} TFLOP/s fp32 ({100 * tflops / PEAK_FP32_TFLOPS:.1f}% of the fp32 matrix peak)")
+    del audio
+    return {
+        "workload": f"LogMelSpectrogram: {MEL_B} windows of 30 s (480000 samples, fp32, on the GPU) -> "
+        f"[{MEL_B}, {MEL_MELS}, 3000]",
+        "us_per_batch": round(ms * 1e3, 2),
+        "windows_per_s": round(MEL_B / ms * 1e3, 1),
+        "roofline": {
+            "bound": "mfma",
+            "achieved": round(tflops, 2),
+            "peak": PEAK_FP32_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / PEAK_FP32_TFLOPS, 4),
+            "flop_per_batch": flop,
+            "kernel": "logmel_spec_kernel (fp32 MFMA)",
+        },
+    }
+
+
+def logmel_cpu_baseline(budget_s: float = 8.0) -> dict:
+    """The reference's op sequence (torch.stft + filterbank + log) on the host cores, one window."""
+    from oracle.mel_oracle import log_mel_torch, mel_filterbank
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    fb = mel_filterbank(MEL_MELS)
+    x = 0.1 * torch.randn(MEL_N, generator=torch.Generator().manual_seed(1))
+    log_mel_torch(x, fb, 3000)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 200):
+        t0 = time.perf_counter()
+        log_mel_torch(x, fb, 3000)
+        times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    log(f"[bench] log-mel cpu baseline: {med * 1e3:.2f} ms per window on {cores} threads")
+    return {
+        "value": round(1.0 / med, 1),
+        "unit": "windows/s",
+        "cores": cores,
+        "kind": "port",
+        "sample": f"torch CPU fp32 op sequence of LogMelSpectrogram (audio.py:141-156, torch.stft) on one 30-s "
+        f"window, median of {len(times)} runs ({med * 1e3:.2f} ms each)",
+    }
+
+
 DTW_KERNELS = ("dtw_row_stats_kernel<true>", "dtw_col_stats_kernel", "dtw_filter_kernel<3>")
 
 
@@ -508,7 +582,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["enc", "dec", "dtw"], default=None)
+    ap.add_argument("--only", choices=["enc", "dec", "dtw", "mel"], default=None)
     ap.add_argument("--pmc-sample", action="store_true",
                     help="run the short fixed kernel sequence used for rocprofv3 --pmc passes and exit")
     args = ap.parse_args()
@@ -534,9 +608,12 @@ def main() -> int:
     enc = bench_encoder(dev, args.steps, args.warmup) if args.only in (None, "enc") else None
     dec = bench_decode(dev, args.steps, args.warmup) if args.only in (None, "dec") else None
     dtw = bench_dtw(dev, args.steps, args.warmup) if args.only in (None, "dtw") else None
+    mel = bench_logmel(dev, args.steps, args.warmup) if args.only in (None, "mel") else None
     cpu = None if args.no_cpu else cpu_baseline()
     if dtw is not None and not args.no_cpu:
         dtw["cpu_baseline"] = dtw_cpu_baseline()
+    if mel is not None and not args.no_cpu:
+        mel["cpu_baseline"] = logmel_cpu_baseline()
 
     line = {
         "metric": METRIC,
@@ -565,6 +642,7 @@ def main() -> int:
         "cpu_baseline": cpu,
         "decode": dec,
         "dtw_prep": dtw,
+        "log_mel": mel,
     }
     print(json.dumps(line), flush=True)
     return 0

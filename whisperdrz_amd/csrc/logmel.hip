@@ -8,11 +8,12 @@
 //   truncate to target_frames.
 //
 // Three launches:
-//   logmel_init_kernel   the [201, n_mels] filterbank (computed in double, stored fp32) and each
-//                        window's running maximum, into the workspace
+//   logmel_init_kernel   the [201, n_mels] filterbank and the cosine / Hann tables (computed in
+//                        double, stored fp32) and each window's running maximum, into the
+//                        workspace
 //   logmel_spec_kernel   one workgroup per (32 frames, window), 4 wavefronts. The frames' samples
 //                        (overlapping by 240) are staged once in LDS with the reflect padding;
-//                        the windowed DFT is a [32 frames x 400 samples] x [400 x 224 bins]
+//                        the windowed DFT is a [32 frames x 400 samples] x [400 x 256 bins]
 //                        product on the fp32 matrix cores (v_mfma_f32_32x32x2_f32: real and
 //                        imaginary parts as two accumulators over the same A operand; cosines
 //                        from a 400-entry LDS table indexed by i*k mod 400). The power spectrum
@@ -33,11 +34,15 @@ namespace {
 constexpr int kNfft = 400;
 constexpr int kHop = 160;
 constexpr int kBins = kNfft / 2 + 1;     // 201
-constexpr int kBinTiles = 7;             // 224 bins computed, 201 kept
+constexpr int kBinTiles = 8;             // 256 bins computed (2 tiles per wavefront), 201 kept
 constexpr int kFrames = 32;              // frames per workgroup
 constexpr int kSeg = (kFrames - 1) * kHop + kNfft;  // 5360 samples
 constexpr int kPPitch = 225;             // power tile pitch (odd: conflict-free column reads)
 constexpr int kKMel = 202;               // filterbank rows incl. one zero row (K multiple of 2)
+// Samples are stored with one pad float per 32 (position j + j/32): the 32 frames a wavefront
+// reads at once are 160 samples apart, which would otherwise fall into 2 of the 64 LDS banks.
+constexpr int kSegStored = kSeg + kSeg / 32 + 1;
+__device__ __forceinline__ int seg_pos(int j) { return j + (j >> 5); }
 
 typedef float f32x16v __attribute__((ext_vector_type(16)));
 
@@ -66,10 +71,17 @@ __device__ double mel_to_hz(double m) {
   return 1000.0 * exp(log(6.4) / 27.0 * (m - min_log_mel));
 }
 
-// fb[k][m] (row k = frequency bin, kKMel rows, row 201 zero) and the window maxima.
+// fb[k][m] (row k = frequency bin, kKMel rows, row 201 zero), the window maxima, and the
+// cosine / Hann tables (400 entries each, computed in double).
 __global__ __launch_bounds__(256) void logmel_init_kernel(LogMelArgs a) {
   const int idx = blockIdx.x * 256 + threadIdx.x;
   if (idx < a.B) a.gmax[idx] = order_key(-INFINITY);
+  if (idx < kNfft) {
+    double sn, c;
+    sincospi(2.0 * idx / kNfft, &sn, &c);
+    a.tables[idx] = (float)c;
+    a.tables[kNfft + idx] = (float)(0.5 - 0.5 * c);  // periodic Hann
+  }
   if (idx >= kKMel * a.n_mels) return;
   const int k = idx / a.n_mels, m = idx % a.n_mels;
   float v = 0.f;
@@ -94,6 +106,7 @@ __global__ __launch_bounds__(256) void logmel_spec_kernel(LogMelArgs a) {
   const int tid = threadIdx.x;
   const int N = a.n_samples;
 
+  static_assert(kSegStored <= kFrames * kPPitch, "sample buffer");
   __shared__ float seg_p[kFrames * kPPitch];  // samples during the DFT, then the power tile
   __shared__ float win[kNfft];
   __shared__ float ctab[kNfft];
@@ -106,23 +119,21 @@ __global__ __launch_bounds__(256) void logmel_spec_kernel(LogMelArgs a) {
     if (o < 0) o = -o;
     if (o >= N) o = 2 * (N - 1) - o;
     o = o < 0 ? 0 : (o >= N ? N - 1 : o);  // frames past the end only
-    seg_p[j] = x[o];
+    seg_p[seg_pos(j)] = x[o];
   }
   for (int j = tid; j < kNfft; j += 256) {
-    double s, c;
-    sincospi(2.0 * j / kNfft, &s, &c);
-    ctab[j] = (float)c;
-    win[j] = (float)(0.5 - 0.5 * c);  // periodic Hann
+    ctab[j] = a.tables[j];
+    win[j] = a.tables[kNfft + j];
   }
   __syncthreads();
 
-  // ---- windowed DFT: wave w computes bin tiles w and w + 4 (< 7) for the 32 frames ----
+  // ---- windowed DFT: wave w computes bin tiles w and w + 4 for the 32 frames (tile 7 is past
+  // the 201 bins; computing it keeps every wavefront on the same straight-line code) ----
   const int fr = lane & 31;  // frame of this lane's A element / bin of its B element
   const int kk = lane >> 5;  // which of the 2 samples of a step
   f32x16v re[2], im[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) re[u] = im[u] = f32x16v{};
-  const int tiles = wave + 4 < kBinTiles ? 2 : 1;
   int idx[2], step[2];
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
@@ -130,35 +141,31 @@ __global__ __launch_bounds__(256) void logmel_spec_kernel(LogMelArgs a) {
     idx[u] = (kk * n) % kNfft;               // (i * n) mod 400 for i = kk
     step[u] = (2 * n) % kNfft;
   }
-  const float* srow = seg_p + kHop * fr;
+#pragma unroll 8
   for (int s = 0; s < kNfft / 2; ++s) {
     const int i = 2 * s + kk;
-    const float av = srow[i] * win[i];
+    const float av = seg_p[seg_pos(kHop * fr + i)] * win[i];
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      if (u < tiles) {
-        const float c = ctab[idx[u]];
-        int is = idx[u] + 300;  // sin(t) = cos(t - pi/2): index - 100 mod 400
-        is = is >= kNfft ? is - kNfft : is;
-        const float sn = ctab[is];
-        re[u] = mfma32x2(av, c, re[u]);
-        im[u] = mfma32x2(av, sn, im[u]);
-        idx[u] += step[u];
-        idx[u] = idx[u] >= kNfft ? idx[u] - kNfft : idx[u];
-      }
+      const float c = ctab[idx[u]];
+      int is = idx[u] + 300;  // sin(t) = cos(t - pi/2): index - 100 mod 400
+      is = is >= kNfft ? is - kNfft : is;
+      const float sn = ctab[is];
+      re[u] = mfma32x2(av, c, re[u]);
+      im[u] = mfma32x2(av, sn, im[u]);
+      idx[u] += step[u];
+      idx[u] = idx[u] >= kNfft ? idx[u] - kNfft : idx[u];
     }
   }
   __syncthreads();  // every wavefront is done with the samples: the buffer becomes the power tile
 #pragma unroll
   for (int u = 0; u < 2; ++u) {
-    if (u < tiles) {
-      const int n = 32 * (wave + 4 * u) + fr;
+    const int n = 32 * (wave + 4 * u) + fr;
 #pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        const int row = 8 * (e / 4) + 4 * kk + (e % 4);  // frame within the tile
-        const float p = re[u][e] * re[u][e] + im[u][e] * im[u][e];
-        if (n < kKMel) seg_p[row * kPPitch + n] = n < kBins ? p : 0.f;
-      }
+    for (int e = 0; e < 16; ++e) {
+      const int row = 8 * (e / 4) + 4 * kk + (e % 4);  // frame within the tile
+      const float p = re[u][e] * re[u][e] + im[u][e] * im[u][e];
+      if (n < kKMel) seg_p[row * kPPitch + n] = n < kBins ? p : 0.f;
     }
   }
   __syncthreads();
@@ -170,6 +177,7 @@ __global__ __launch_bounds__(256) void logmel_spec_kernel(LogMelArgs a) {
     const int mel = 32 * wave + fr;
     const int melc = mel < a.n_mels ? mel : a.n_mels - 1;
     f32x16v acc = f32x16v{};
+#pragma unroll 8
     for (int s = 0; s < kKMel / 2; ++s) {
       const int k = 2 * s + kk;
       const float av = seg_p[fr * kPPitch + k];
@@ -215,15 +223,23 @@ __global__ __launch_bounds__(256) void logmel_finish_kernel(LogMelArgs a) {
 
 }  // namespace
 
+// Workspace: filterbank [202, n_mels], cosine + Hann tables [2, 400], window maxima [B].
+namespace {
+size_t fb_bytes(int64_t n_mels) { return ((size_t)(kKMel * n_mels) * sizeof(float) + 255) / 256 * 256; }
+constexpr size_t kTableBytes = 2 * kNfft * sizeof(float);
+}  // namespace
+
 size_t logmel_workspace_bytes(int64_t B, int64_t n_mels) {
-  return ((size_t)(kKMel * n_mels) * sizeof(float) + 255) / 256 * 256 + (size_t)B * sizeof(uint32_t);
+  return fb_bytes(n_mels) + kTableBytes + (size_t)B * sizeof(uint32_t);
 }
 
 hipError_t launch_logmel(LogMelArgs a, void* ws, hipStream_t stream) {
   char* p = static_cast<char*>(ws);
   a.fb = reinterpret_cast<float*>(p);
-  a.gmax = reinterpret_cast<uint32_t*>(p + ((size_t)(kKMel * a.n_mels) * sizeof(float) + 255) / 256 * 256);
-  const int init_n = kKMel * a.n_mels > a.B ? kKMel * a.n_mels : a.B;
+  a.tables = reinterpret_cast<float*>(p + fb_bytes(a.n_mels));
+  a.gmax = reinterpret_cast<uint32_t*>(p + fb_bytes(a.n_mels) + kTableBytes);
+  int init_n = kKMel * a.n_mels > a.B ? kKMel * a.n_mels : a.B;
+  init_n = init_n > kNfft ? init_n : kNfft;
   hipLaunchKernelGGL(logmel_init_kernel, dim3((init_n + 255) / 256), dim3(256), 0, stream, a);
   hipLaunchKernelGGL(logmel_spec_kernel, dim3((a.n_frames + kFrames - 1) / kFrames, a.B), dim3(256), 0, stream, a);
   hipLaunchKernelGGL(logmel_finish_kernel, dim3((a.out_frames + 255) / 256, a.n_mels, a.B), dim3(256), 0, stream, a);

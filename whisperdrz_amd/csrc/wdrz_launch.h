@@ -91,6 +91,7 @@ struct LogMelArgs {
   float* out;         // [B, n_mels, out_frames], frames contiguous
   int64_t os[2];      // b, mel strides of out
   float* fb;          // workspace: [202, n_mels] filterbank
+  float* tables;      // workspace: cos(2 pi j / 400), then the periodic Hann window
   uint32_t* gmax;     // workspace: [B] ordered-encoded window maxima
   int B, n_samples, n_mels, n_frames, out_frames;
 };
