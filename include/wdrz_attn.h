@@ -123,6 +123,37 @@ int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, co
                       size_t workspace_bytes, void* stream);
 
 /*
+ * Residual add + LayerNorm of the decode step.
+ *
+ * Replaces: the residual add closing a sub-layer and the LayerNorm opening the next
+ *           (src/whisperdrz/model.py:420-433, ResidualAttentionBlock.forward_flash; the final
+ *           ln before the logits, model.py:609-613; LayerNorm model.py:195-200 in eval mode).
+ * x:      16-bit rows [rows, n], row stride x_stride; when delta != NULL it is updated in place to
+ *         x + delta (rounded to the storage type, as torch's add), the new residual.
+ * y:      LayerNorm(x) rows, fp32 statistics, eps, affine weight / bias (16-bit, [n]).
+ * n a multiple of 8, <= 4096; 16-byte aligned pointers and row strides.
+ */
+int wdrz_add_layernorm(int dtype, void* x, int64_t x_stride, const void* delta,
+                       int64_t delta_stride, const void* weight, const void* bias, void* y,
+                       int64_t y_stride, int64_t rows, int64_t n, float eps, void* stream);
+
+/*
+ * Greedy sampling with the decode step's token constraints.
+ *
+ * Replaces: decode_batch's sampling tail (src/whisperdrz/decoding.py:1729-1761):
+ *           masked = logits + (-65504 where blocked[row, v]); where penalty[row, v]:
+ *           masked > 0 ? masked / 1.2 : masked * 1.2; out[row] = argmax (temperature 0,
+ *           sample_logits decoding.py:854-855). Every step rounds to the logits' type as the
+ *           torch ops do; ties go to the lowest index, as torch.argmax.
+ * logits: [rows, V] (f32 / f16 / bf16), row stride logits_stride (elements).
+ * blocked, penalty: bool [rows, V] as bytes (row strides in bytes), either may be NULL.
+ * out: int64 [rows].
+ */
+int wdrz_masked_argmax(int dtype, const void* logits, int64_t logits_stride,
+                       const uint8_t* blocked, int64_t blocked_stride, const uint8_t* penalty,
+                       int64_t penalty_stride, int64_t* out, int64_t rows, int64_t V, void* stream);
+
+/*
  * Workspace (bytes) for wdrz_log_mel: the [202, n_mels] filterbank and one maximum per window.
  * No counterpart in the reference (torchaudio keeps the filterbank in a module buffer).
  */

@@ -35,6 +35,7 @@ def _make(cuda, dtype, seed=0):
     torch.manual_seed(seed)
     hip = TextDecoderStack(N_VOCAB, N_CTX, N_STATE, N_HEAD, N_LAYER).to(cuda, dtype).eval()
     ref = copy.deepcopy(hip)
+    ref.fused_small_ops = False  # the reference's separate add and LayerNorm
     for blk in ref.blocks:
         for m in (blk.attn, blk.cross_attn):
             m.attn_kvcache = _ref_kvcache

@@ -14,6 +14,7 @@ from .attention import (
     scaled_dot_product_attention,
 )
 from .audio import LogMelSpectrogram, log_mel_spectrogram
+from .decode_ops import add_layernorm_, layer_norm, masked_argmax
 from .dtw import compute_attention, dtw_prep, dtw_prep_batch, dtw_prep_workspace_size
 
 HAS_WDRZ = _lib.available()
@@ -21,6 +22,9 @@ HAS_WDRZ = _lib.available()
 __all__ = [
     "HAS_WDRZ",
     "LogMelSpectrogram",
+    "add_layernorm_",
+    "layer_norm",
+    "masked_argmax",
     "log_mel_spectrogram",
     "compute_attention",
     "dtw_prep",

@@ -21,6 +21,8 @@ EXPORTED_SYMBOLS = (
     "wdrz_attn_fwd",
     "wdrz_attn_kvcache_workspace_size",
     "wdrz_attn_kvcache",
+    "wdrz_add_layernorm",
+    "wdrz_masked_argmax",
     "wdrz_log_mel_workspace_size",
     "wdrz_log_mel",
     "wdrz_dtw_qk",
@@ -61,6 +63,17 @@ def _declare(lib: ctypes.CDLL) -> None:
         _i64p, _i64p, _i64p, _i64p, _i64p, _i64p,  # strides
         ctypes.c_float, ctypes.c_int,  # softmax_scale, causal
         _p, ctypes.c_size_t, _p,  # workspace, bytes, stream
+    ]
+    lib.wdrz_add_layernorm.restype = ctypes.c_int
+    lib.wdrz_add_layernorm.argtypes = [
+        ctypes.c_int, _p, _i64, _p, _i64,  # dtype, x, x stride, delta, delta stride
+        _p, _p, _p, _i64, _i64, _i64,  # weight, bias, y, y stride, rows, n
+        ctypes.c_float, _p,  # eps, stream
+    ]
+    lib.wdrz_masked_argmax.restype = ctypes.c_int
+    lib.wdrz_masked_argmax.argtypes = [
+        ctypes.c_int, _p, _i64, _p, _i64, _p, _i64,  # dtype, logits, stride, blocked, stride, penalty, stride
+        _p, _i64, _i64, _p,  # out, rows, V, stream
     ]
     lib.wdrz_log_mel_workspace_size.restype = ctypes.c_size_t
     lib.wdrz_log_mel_workspace_size.argtypes = [_i64, _i64]

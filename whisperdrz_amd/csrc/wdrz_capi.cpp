@@ -271,6 +271,66 @@ int wdrz_dtw_qk(int dtype, const void* const* q_heads, const int64_t* q_strides,
   return WDRZ_OK;
 }
 
+int wdrz_add_layernorm(int dtype, void* x, int64_t x_stride, const void* delta, int64_t delta_stride,
+                       const void* weight, const void* bias, void* y, int64_t y_stride, int64_t rows, int64_t n,
+                       float eps, void* stream) {
+  g_last_error.clear();
+  if (dtype != WDRZ_BF16 && dtype != WDRZ_F16)
+    return fail(dtype == WDRZ_F32 ? WDRZ_EUNSUPPORTED : WDRZ_EINVAL, "dtype %d: only WDRZ_BF16 / WDRZ_F16", dtype);
+  if (rows < 0 || n <= 0 || n % 8 != 0)
+    return fail(WDRZ_EINVAL, "bad sizes rows=%lld n=%lld (n must be a positive multiple of 8)", (long long)rows,
+                (long long)n);
+  if (n > 4096) return fail(WDRZ_EUNSUPPORTED, "n=%lld exceeds the supported 4096", (long long)n);
+  if (!(eps >= 0.f)) return fail(WDRZ_EINVAL, "eps must be >= 0");
+  int rc;
+  if ((rc = check_ptr("x", x)) || (rc = check_ptr("weight", weight)) || (rc = check_ptr("bias", bias)) ||
+      (rc = check_ptr("y", y)))
+    return rc;
+  if (delta && (rc = check_ptr("delta", delta))) return rc;
+  if ((x_stride * 2) % 16 || (y_stride * 2) % 16 || (delta && (delta_stride * 2) % 16))
+    return fail(WDRZ_EINVAL, "row strides must be 16-byte aligned");
+  if (rows == 0) return WDRZ_OK;
+  wdrz::AddLnArgs a{};
+  a.x = x;
+  a.delta = delta;
+  a.weight = weight;
+  a.bias = bias;
+  a.y = y;
+  a.rows = rows;
+  a.n = (int)n;
+  a.x_stride = x_stride;
+  a.d_stride = delta_stride;
+  a.y_stride = y_stride;
+  a.eps = eps;
+  hipError_t err = wdrz::launch_add_layernorm(dtype, a, reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(WDRZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  return WDRZ_OK;
+}
+
+int wdrz_masked_argmax(int dtype, const void* logits, int64_t logits_stride, const uint8_t* blocked,
+                       int64_t blocked_stride, const uint8_t* penalty, int64_t penalty_stride, int64_t* out,
+                       int64_t rows, int64_t V, void* stream) {
+  g_last_error.clear();
+  if (!elem_bytes(dtype)) return fail(WDRZ_EINVAL, "dtype %d is not one of WDRZ_F32/F16/BF16", dtype);
+  if (rows < 0 || V <= 0) return fail(WDRZ_EINVAL, "bad sizes rows=%lld V=%lld", (long long)rows, (long long)V);
+  if (rows > (1 << 24) || V > (1 << 30)) return fail(WDRZ_EUNSUPPORTED, "sizes too large");
+  if (!logits || !out) return fail(WDRZ_EINVAL, "logits / out is NULL");
+  if (rows == 0) return WDRZ_OK;
+  wdrz::ArgmaxArgs a{};
+  a.logits = logits;
+  a.l_stride = logits_stride;
+  a.blocked = blocked;
+  a.m_stride = blocked_stride;
+  a.penalty = penalty;
+  a.p_stride = penalty_stride;
+  a.out = out;
+  a.rows = (int)rows;
+  a.V = (int)V;
+  hipError_t err = wdrz::launch_masked_argmax(dtype, a, reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(WDRZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  return WDRZ_OK;
+}
+
 size_t wdrz_log_mel_workspace_size(int64_t B, int64_t n_mels) {
   if (B <= 0 || n_mels <= 0) return 0;
   return wdrz::logmel_workspace_bytes(B, n_mels);

@@ -84,6 +84,33 @@ struct DtwQkArgs {
 };
 hipError_t launch_dtw_qk(int dtype, DtwQkArgs a, hipStream_t stream);
 
+// Residual add + LayerNorm over 16-bit rows (strides in elements).
+struct AddLnArgs {
+  void* x;            // residual rows, updated in place to x + delta (when delta is given)
+  const void* delta;  // nullptr: LayerNorm of x only
+  const void* weight;
+  const void* bias;
+  void* y;            // LayerNorm output rows
+  int64_t rows;
+  int n;
+  int64_t x_stride, d_stride, y_stride;
+  float eps;
+};
+hipError_t launch_add_layernorm(int dtype, const AddLnArgs& a, hipStream_t stream);
+
+// Masked greedy sampling over logits rows (strides in elements / bytes for the masks).
+struct ArgmaxArgs {
+  const void* logits;
+  int64_t l_stride;
+  const uint8_t* blocked;  // bool [rows, V] or nullptr
+  int64_t m_stride;
+  const uint8_t* penalty;  // bool [rows, V] or nullptr
+  int64_t p_stride;
+  int64_t* out;
+  int rows, V;
+};
+hipError_t launch_masked_argmax(int dtype, const ArgmaxArgs& a, hipStream_t stream);
+
 // Log-mel front end over fp32 waveforms [B, n_samples] (row stride audio_stride elements).
 struct LogMelArgs {
   const float* audio;

@@ -1,0 +1,92 @@
+"""Fused small operations of the decode step, backed by the gfx950 kernels in libwdrz_attn.so.
+
+* :func:`add_layernorm_` — ``x += delta; return ln(x)``: the residual add closing a sub-layer
+  and the LayerNorm opening the next (reference ``src/whisperdrz/model.py:420-433``, the final
+  ``ln`` at ``model.py:609-613``), one launch instead of two.
+* :func:`masked_argmax` — ``decode_batch``'s greedy sampling tail (``decoding.py:1729-1761``):
+  additive -65504 mask, repetition penalty, argmax, one launch instead of six.
+
+There is no fallback: CPU tensors, fp32 LayerNorm inputs and a missing library raise.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+import torch.nn as nn
+
+from . import _lib
+from .attention import _check_cuda, _dtype_code, _raise, _stream_handle
+
+__all__ = ["add_layernorm_", "layer_norm", "masked_argmax"]
+
+_LN16 = {torch.bfloat16: _lib.WDRZ_BF16, torch.float16: _lib.WDRZ_F16}
+
+
+def _rows(t: torch.Tensor, name: str) -> torch.Tensor:
+    r = t.reshape(-1, t.shape[-1])
+    if r.stride(-1) != 1 or r.data_ptr() != t.data_ptr():
+        raise ValueError(f"{name} must have contiguous rows")
+    return r
+
+
+def add_layernorm_(x: torch.Tensor, delta: Optional[torch.Tensor], ln: nn.LayerNorm) -> torch.Tensor:
+    """In place ``x += delta`` (when ``delta`` is given), then returns ``ln(x)`` (fp32 statistics)."""
+    _check_cuda("x", x, x.device)
+    if x.dtype not in _LN16:
+        raise TypeError(f"x: dtype {x.dtype} is not supported (bfloat16, float16)")
+    xr = _rows(x, "x")
+    dr = None
+    if delta is not None:
+        _check_cuda("delta", delta, x.device)
+        if delta.dtype != x.dtype or delta.shape != x.shape:
+            raise ValueError("delta must match x in shape and dtype")
+        dr = delta.reshape(xr.shape) if delta.is_contiguous() else delta.contiguous().reshape(xr.shape)
+    w = ln.weight.detach()
+    b = ln.bias.detach()
+    if w.dtype != x.dtype:
+        raise TypeError("the LayerNorm parameters must have the activations' dtype")
+    y = torch.empty_like(xr)
+    rc = _lib.load().wdrz_add_layernorm(
+        _LN16[x.dtype], xr.data_ptr(), xr.stride(0), dr.data_ptr() if dr is not None else None,
+        dr.stride(0) if dr is not None else 0, w.data_ptr(), b.data_ptr(), y.data_ptr(), y.stride(0),
+        xr.shape[0], xr.shape[1], float(ln.eps), _stream_handle(),
+    )
+    if rc != _lib.WDRZ_OK:
+        _raise(rc, "add_layernorm_")
+    return y.view(x.shape)
+
+
+def layer_norm(x: torch.Tensor, ln: nn.LayerNorm) -> torch.Tensor:
+    return add_layernorm_(x, None, ln)
+
+
+def masked_argmax(logits: torch.Tensor, blocked: Optional[torch.Tensor] = None,
+                  penalty: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Greedy token per row of ``logits [rows, V]`` under the bool ``blocked`` mask (additive
+    -65504) and the bool ``penalty`` mask (repetition penalty 1.2), as decode_batch computes it."""
+    _check_cuda("logits", logits, logits.device)
+    if logits.dim() == 3:
+        logits = logits[:, -1, :]
+    if logits.stride(-1) != 1:
+        logits = logits.contiguous()
+    rows, V = (int(v) for v in logits.shape)
+    out = torch.empty(rows, dtype=torch.long, device=logits.device)
+    masks = []
+    for name, m in (("blocked", blocked), ("penalty", penalty)):
+        if m is None:
+            masks.append((None, 0))
+            continue
+        _check_cuda(name, m, logits.device)
+        if m.dtype != torch.bool or m.shape[-1] < V or m.dim() != 2 or m.stride(-1) != 1:
+            raise ValueError(f"{name} must be a bool [rows, >= V] tensor with contiguous rows")
+        masks.append((m, m.stride(0)))
+    rc = _lib.load().wdrz_masked_argmax(
+        _dtype_code(logits, "logits"), logits.data_ptr(), logits.stride(0),
+        masks[0][0].data_ptr() if masks[0][0] is not None else None, masks[0][1],
+        masks[1][0].data_ptr() if masks[1][0] is not None else None, masks[1][1],
+        out.data_ptr(), rows, V, _stream_handle(),
+    )
+    if rc != _lib.WDRZ_OK:
+        _raise(rc, "masked_argmax")
+    return out

@@ -12,6 +12,8 @@ cached attention, so the HIP kernels can be exercised exactly as WhisperDRZ driv
 * ``TextDecoderStack.forward_flash`` / ``prefill_flash`` — embeddings, the blocks, the
   ``seq_lens`` bump after all layers, final LN and tied-embedding logits (model.py:570-617,
   824-869).
+* ``TextDecoderStack._fused_blocks`` — the same blocks with each residual add fused into the
+  next LayerNorm (``decode_ops.add_layernorm_``), the default for 16-bit GPU activations.
 * ``BucketedDecodeGraphs`` — one captured decode step per batch bucket, replayed with static
   token / position / slot buffers (reference ``transcriber.py:18-173``); on ROCm
   ``torch.cuda.CUDAGraph`` is a hipGraph.
@@ -30,6 +32,7 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from .attention import flash_attn_with_kvcache, scaled_dot_product_attention
+from .decode_ops import add_layernorm_, layer_norm
 from .kv_cache import FlashKVCache, KVSlotPool
 
 # Batch buckets of the captured decode step (reference transcriber.py:18).
@@ -118,6 +121,9 @@ class TextDecoderStack(nn.Module):
         self.positional_embedding = nn.Parameter(torch.randn(n_ctx, n_state) * 0.02)
         self.blocks = nn.ModuleList([ResidualAttentionBlock(n_state, n_head, **attn_kw) for _ in range(n_layer)])
         self.ln = nn.LayerNorm(n_state)
+        # Cached steps on 16-bit GPU activations fuse every residual add with the LayerNorm that
+        # follows it (one kernel instead of two); False keeps torch's separate ops.
+        self.fused_small_ops = True
 
     def forward(self, tokens: Tensor, xa: Tensor) -> Tensor:
         """Uncached forward over all tokens (the DTW-alignment path, model.py:547-568)."""
@@ -132,15 +138,34 @@ class TextDecoderStack(nn.Module):
         if positions.dim() == 1:
             positions = positions.unsqueeze(1).expand(B, seq_len)
         x = self.token_embedding(tokens) + self.positional_embedding[positions]
-        for block, s_kv, c_kv in zip(self.blocks, self_kv, cross_kv, strict=True):
-            x = block.forward_flash(x, s_kv, c_kv, slot_indices=slot_indices)
+        if self.fused_small_ops and x.is_cuda and x.dtype in (torch.bfloat16, torch.float16):
+            h = self._fused_blocks(x.contiguous(), self_kv, cross_kv, slot_indices)
+        else:
+            for block, s_kv, c_kv in zip(self.blocks, self_kv, cross_kv, strict=True):
+                x = block.forward_flash(x, s_kv, c_kv, slot_indices=slot_indices)
+            h = self.ln(x)
         # the attention never bumps lengths; the caller does, after all layers
         for s_kv in self_kv:
             if slot_indices is not None:
                 s_kv.seq_lens[slot_indices] += seq_len
             else:
                 s_kv.seq_lens[:B] += seq_len
-        return self.ln(x) @ self.token_embedding.weight.to(x.dtype).T
+        return h @ self.token_embedding.weight.to(h.dtype).T
+
+    def _fused_blocks(self, x: Tensor, self_kv: list[FlashKVCache], cross_kv: list[FlashKVCache],
+                      slot_indices: Optional[Tensor]) -> Tensor:
+        """The blocks of ``forward_flash`` with each residual add fused into the next LayerNorm
+        (model.py:420-433): x is the residual stream, updated in place; returns ln(x)."""
+        blocks = list(self.blocks)
+        h = layer_norm(x, blocks[0].attn_ln)
+        for i, (block, s_kv, c_kv) in enumerate(zip(blocks, self_kv, cross_kv, strict=True)):
+            d = block.attn.forward_flash(h, s_kv, is_cross_attn=False, slot_indices=slot_indices)
+            h = add_layernorm_(x, d, block.cross_attn_ln)
+            d = block.cross_attn.forward_flash(h, c_kv, is_cross_attn=True, slot_indices=slot_indices)
+            h = add_layernorm_(x, d, block.mlp_ln)
+            d = block.mlp(h)
+            h = add_layernorm_(x, d, blocks[i + 1].attn_ln if i + 1 < len(blocks) else self.ln)
+        return h
 
     def prefill_flash(self, tokens: Tensor, xa: Tensor, self_kv: list[FlashKVCache], cross_kv: list[FlashKVCache],
                       slot_indices: Optional[Tensor] = None) -> Tensor:
