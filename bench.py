@@ -13,7 +13,10 @@ carries the DTW alignment inputs (compute_attention and _dtw_prep_batch) in GB/s
 HBM bytes, and under ``log_mel`` the GPU log-mel front end in TFLOP/s of fp32 matrix work, each
 with its own roofline and CPU baseline.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only enc|dec|dtw|mel]
+Under ``decode_step`` it times a whole captured large-v3 decode step (64 streams) with and without
+the fused add + LayerNorm.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only enc|dec|dtw|mel|step]
 """
 from __future__ import annotations
 
@@ -392,6 +395,55 @@ def bench_dtw_qk(dev, steps: int, warmup: int) -> dict:
 
 
 # --------------------------------------------------------------------------------------------
+# a whole decode step (large-v3 decoder, random weights, 64 streams, one captured hipGraph)
+# --------------------------------------------------------------------------------------------
+
+
+def bench_decode_step(dev, steps: int, warmup: int) -> dict:
+    from whisperdrz_amd.decoder import BucketedDecodeGraphs, TextDecoderStack
+    from whisperdrz_amd.kv_cache import KVSlotPool
+
+    Bs, n_vocab, n_layer = 64, 51866, 32
+    steps = min(steps, 20)
+    torch.manual_seed(0)
+    log("[bench] decode step: large-v3 decoder (random weights, bf16), 64 streams, 32 layers")
+    with torch.device(dev):
+        dec = TextDecoderStack(n_vocab, 448, H * D, H, n_layer).to(torch.bfloat16).eval()
+    pool = KVSlotPool(n_layer, Bs, H, D, self_len=448, cross_len=1500, dtype=torch.bfloat16, device=dev)
+    pool.arena.view(torch.bfloat16).normal_()
+    lens0 = torch.from_numpy(_lengths(8, Bs, 1, 400).astype(np.int32)).to(dev)
+    tokens = torch.randint(0, n_vocab, (Bs, 1), device=dev)
+    slots = torch.arange(Bs, device=dev)
+    res = {}
+    for fused in (True, False):
+        dec.fused_small_ops = fused
+        for c in pool.self_kv:
+            c.seq_lens.copy_(lens0)
+        graphs = BucketedDecodeGraphs(dec, pool, n_vocab, buckets=[Bs])
+        with torch.no_grad():
+            graphs.capture(Bs)
+            positions = lens0.long()
+            for c in pool.self_kv:
+                c.seq_lens.copy_(lens0)
+            for _ in range(warmup):
+                graphs.forward(tokens, positions, slots)
+            ms = timed_events(lambda: graphs.forward(tokens, positions, slots), steps, torch.cuda.current_stream())
+        res["fused" if fused else "unfused"] = ms
+        log(f"[bench] decode step ({'fused add+LayerNorm' if fused else 'torch add, LayerNorm'}): {ms:.3f} ms "
+            f"per step, {Bs / ms * 1e3:.0f} tokens/s")
+        del graphs
+    del dec, pool
+    torch.cuda.empty_cache()
+    return {
+        "workload": "one cached decode step of the large-v3 decoder (random bf16 weights, 32 layers, vocab "
+        "51866), 64 streams, self lengths U[1,400], cross 1500, captured in one hipGraph",
+        "ms_per_step": round(res["fused"], 4),
+        "tokens_per_s": round(Bs / res["fused"] * 1e3, 1),
+        "ms_per_step_unfused_small_ops": round(res["unfused"], 4),
+    }
+
+
+# --------------------------------------------------------------------------------------------
 # log-mel front end (LogMelSpectrogram, audio.py:81-156)
 # --------------------------------------------------------------------------------------------
 
@@ -464,7 +516,7 @@ def logmel_cpu_baseline(budget_s: float = 8.0) -> dict:
     }
 
 
-DTW_KERNELS = ("dtw_row_stats_kernel<true>", "dtw_col_stats_kernel", "dtw_filter_kernel<3>")
+DTW_KERNELS = ("dtw_rowcol_kernel<6>", "dtw_col_merge_kernel", "dtw_band_kernel<3, 384>")
 
 
 def dtw_cpu_baseline(budget_s: float = 12.0) -> dict:
@@ -530,7 +582,8 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
 def pmc_sample(dev) -> None:
     """A short, fixed kernel sequence for hardware-counter passes (rocprofv3 --pmc):
     a calibration copy of 1 GiB (known HBM bytes), then 3 launches of the encoder kernel, of
-    each decode kernel and of the DTW prep at the bench shapes (eager, distinct inputs)."""
+    each decode kernel, of the DTW prep, compute_attention and the log-mel front end at the
+    bench shapes (eager)."""
     from whisperdrz_amd import flash_attn_with_kvcache, scaled_dot_product_attention
 
     n = 1 << 30
@@ -566,13 +619,29 @@ def pmc_sample(dev) -> None:
         flash_attn_with_kvcache(q5, kv_x[0], kv_x[1], cache_batch_idx=slots, softmax_scale=0.125)
         torch.cuda.synchronize()
         del kv_s, kv_x
-    from whisperdrz_amd import dtw_prep
+    from whisperdrz_amd import compute_attention, dtw_prep, log_mel_spectrogram
 
     for i in range(3):
         w, lens, caps = _dtw_inputs(dev, 5000 + i)
         dtw_prep(w, lens, caps, 7)
         torch.cuda.synchronize()
         del w
+    mask = torch.zeros(32, H, dtype=torch.bool)
+    for l, h in DTW_HEADS:
+        mask[l, h] = True
+    g = torch.Generator(device=dev).manual_seed(6000)
+    q_out, k_out = [None] * 32, [None] * 32
+    for l, _ in DTW_HEADS:
+        q_out[l] = torch.randn((DTW_B, DTW_T, H * D), generator=g, device=dev).to(torch.bfloat16)
+        k_out[l] = torch.randn((DTW_B, DTW_A, H * D), generator=g, device=dev).to(torch.bfloat16)
+    for _ in range(3):
+        compute_attention(q_out, k_out, mask)
+        torch.cuda.synchronize()
+    del q_out, k_out
+    audio = 0.1 * torch.randn((MEL_B, MEL_N), generator=g, device=dev)
+    for _ in range(3):
+        log_mel_spectrogram(audio, MEL_MELS, 3000)
+        torch.cuda.synchronize()
     log("[bench] pmc sample done")
 
 
@@ -582,7 +651,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["enc", "dec", "dtw", "mel"], default=None)
+    ap.add_argument("--only", choices=["enc", "dec", "dtw", "mel", "step"], default=None)
     ap.add_argument("--pmc-sample", action="store_true",
                     help="run the short fixed kernel sequence used for rocprofv3 --pmc passes and exit")
     args = ap.parse_args()
@@ -609,6 +678,7 @@ def main() -> int:
     dec = bench_decode(dev, args.steps, args.warmup) if args.only in (None, "dec") else None
     dtw = bench_dtw(dev, args.steps, args.warmup) if args.only in (None, "dtw") else None
     mel = bench_logmel(dev, args.steps, args.warmup) if args.only in (None, "mel") else None
+    step = bench_decode_step(dev, args.steps, args.warmup) if args.only in (None, "step") else None
     cpu = None if args.no_cpu else cpu_baseline()
     if dtw is not None and not args.no_cpu:
         dtw["cpu_baseline"] = dtw_cpu_baseline()
@@ -643,6 +713,7 @@ def main() -> int:
         "decode": dec,
         "dtw_prep": dtw,
         "log_mel": mel,
+        "decode_step": step,
     }
     print(json.dumps(line), flush=True)
     return 0
