@@ -51,7 +51,6 @@ constexpr int kBN = 64;               // key rows per LDS tile
 constexpr int kBS = 32;               // key rows per sub-step
 constexpr int kPitchK = kHeadDim + 8; // K tile row pitch in elements (16-byte pad)
 constexpr int kNumBuf = 3;            // LDS tile buffers
-constexpr int kNumXcd = 8;
 constexpr float kTau = 8.0f;          // lazy-rescale threshold (log2 units)
 
 template <typename T> struct Mfma;
@@ -74,11 +73,6 @@ template <> struct Mfma<F16> {
   static __device__ __forceinline__ float widen_hi(uint32_t w) { return f16_hi(w); }
 };
 
-__device__ __forceinline__ int remap_xcd(int id, int n) {
-  const int q = n / kNumXcd, rem = n % kNumXcd;
-  const int xcd = id % kNumXcd, local = id / kNumXcd;
-  return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
-}
 
 // max of x over the two 32-lane halves of the wavefront (every lane gets the result)
 __device__ __forceinline__ float half_swap_max(float x) {

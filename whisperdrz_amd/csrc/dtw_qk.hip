@@ -48,10 +48,14 @@ __global__ __launch_bounds__(256) void dtw_qk_kernel(DtwQkArgs a) {
   typedef typename Mfma32<T>::op_t op_t;
   __shared__ float stage[kQkRows * kQkPitch];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int bh = blockIdx.z;
+  // Logical order: row blocks fastest, then column blocks, then (b, h); remapped so that the
+  // row blocks reading one K block run on one XCD and share it through its L2.
+  const int n_rb = (a.T + kQkRows - 1) / kQkRows, n_cb = (a.A + kQkCols - 1) / kQkCols;
+  const int tile = remap_xcd(blockIdx.x, gridDim.x);
+  const int rb = tile % n_rb, cb = (tile / n_rb) % n_cb, bh = tile / (n_rb * n_cb);
   const int b = bh / a.H, h = bh % a.H;
-  const int r0 = blockIdx.y * kQkRows;
-  const int c0 = blockIdx.x * kQkCols;
+  const int r0 = rb * kQkRows;
+  const int c0 = cb * kQkCols;
   const int kh = 8 * (lane >> 5);  // this lane's 8 of every 16 head dimensions
 
   // Rows / columns past the end are clamped to the last one (valid addresses); their results
@@ -106,7 +110,9 @@ hipError_t launch_dtw_qk(int dtype, DtwQkArgs a, hipStream_t stream) {
   if (a.B == 0 || a.T == 0 || a.A == 0) return hipSuccess;
   a.vec = (reinterpret_cast<uintptr_t>(a.out) & 15) == 0 && a.os[0] % 4 == 0 && a.os[1] % 4 == 0 &&
           a.os[2] % 4 == 0;
-  const dim3 grid((a.A + kQkCols - 1) / kQkCols, (a.T + kQkRows - 1) / kQkRows, a.B * a.H);
+  const int64_t n = (int64_t)((a.A + kQkCols - 1) / kQkCols) * ((a.T + kQkRows - 1) / kQkRows) * a.B * a.H;
+  if (n > 0x7fffffff) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)n);
   if (dtype == 2) hipLaunchKernelGGL(dtw_qk_kernel<Bf16>, grid, dim3(256), 0, stream, a);
   else hipLaunchKernelGGL(dtw_qk_kernel<F16>, grid, dim3(256), 0, stream, a);
   return hipGetLastError();

@@ -159,4 +159,15 @@ template <int G> __device__ __forceinline__ float group_sum(float x) {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// ---- XCD-aware work order ----------------------------------------------------------------------
+// Work-group ids are dealt round-robin over the 8 XCDs. remap_xcd turns the id into a logical work
+// index such that each XCD gets one contiguous range of logical indices: neighbouring work items
+// (sharing inputs) then run on the same XCD and share its L2.
+constexpr int kNumXcd = 8;
+__device__ __forceinline__ int remap_xcd(int id, int n) {
+  const int q = n / kNumXcd, rem = n % kNumXcd;
+  const int xcd = id % kNumXcd, local = id / kNumXcd;
+  return xcd < rem ? xcd * (q + 1) + local : rem * (q + 1) + (xcd - rem) * q + local;
+}
+
 }  // namespace wdrz
