@@ -347,7 +347,7 @@ DTW_HEADS = [(7, 0), (10, 17), (12, 18), (13, 12), (16, 1), (17, 14), (19, 11), 
 def bench_dtw_qk(dev, steps: int, warmup: int) -> dict:
     """compute_attention at the bench shape: the 10 alignment heads' Q/K slices read in place from
     per-layer captures [16, 448, 1280] / [16, 1500, 1280] bf16, fp32 scores written."""
-    from whisperdrz_amd import compute_attention
+    from whisperdrz_amd import compute_attention, dtw_attention_prep, dtw_prep
 
     n_layers, n_heads = 32, H
     mask = torch.zeros(n_layers, n_heads, dtype=torch.bool)
@@ -376,6 +376,17 @@ def bench_dtw_qk(dev, steps: int, warmup: int) -> dict:
     ms_torch = timed_events(torch_ref, 3, stream)
     log(f"[bench] compute_attention: {ms * 1e3:.1f} us, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM); "
         f"torch gather + fp32 matmul {ms_torch * 1e3:.0f} us")
+    # The fused entry (scores recomputed inside both prep passes, never stored) against the
+    # two-call chain compute_attention -> dtw_prep, on the bench's lengths and caps.
+    rng = np.random.default_rng(5000)
+    lens = [int(x) for x in rng.integers(DTW_T // 2, DTW_T + 1, DTW_B)]
+    caps = [DTW_A] * DTW_B
+    for _ in range(warmup):
+        dtw_attention_prep(q_out, k_out, mask, lens, caps)
+    ms_fused = timed_events(lambda: dtw_attention_prep(q_out, k_out, mask, lens, caps), steps, stream)
+    ms_chain = timed_events(lambda: dtw_prep(compute_attention(q_out, k_out, mask), lens, caps), steps, stream)
+    log(f"[bench] fused attention+prep: {ms_fused * 1e3:.1f} us; chain compute_attention + dtw_prep "
+        f"{ms_chain * 1e3:.1f} us")
     del q_out, k_out
     torch.cuda.empty_cache()
     return {
@@ -391,6 +402,8 @@ def bench_dtw_qk(dev, steps: int, warmup: int) -> dict:
             "kernel": "dtw_qk_kernel<Bf16>",
         },
         "torch_gpu_us": round(ms_torch * 1e3, 1),
+        "fused_attention_prep_us": round(ms_fused * 1e3, 2),
+        "chain_attention_then_prep_us": round(ms_chain * 1e3, 2),
     }
 
 

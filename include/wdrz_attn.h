@@ -235,6 +235,28 @@ int wdrz_dtw_prep(const float* weights, const int64_t* w_strides, const int32_t*
                   int64_t H, int64_t T, int64_t A, int64_t C, int medfilt_width, void* workspace,
                   size_t workspace_bytes, void* stream);
 
+/*
+ * Fused DTW prep straight from the captured projections: wdrz_dtw_qk followed by wdrz_dtw_prep,
+ * without the [B, H, T, A] fp32 score tensor ever being written to or read from memory.
+ *
+ * Replaces: full_weights = cap.compute_attention(head_mask) and _dtw_prep_batch(full_weights,
+ *           actual_lens, audio_caps) (src/whisperdrz/dtw_align.py:1184 and 1197; the functions
+ *           at dtw_align.py:553-586 and 700-753) up to the device->host copy.
+ *
+ * q_heads / k_heads / strides / scale / dtype: as for wdrz_dtw_qk (H <= 32, head_dim 64).
+ * actual_lens / audio_caps / out / C / medfilt_width: as for wdrz_dtw_prep.
+ * workspace:  device buffer of wdrz_dtw_prep_workspace_size(B, H, T, A) bytes, 256-byte aligned.
+ * A <= 1536 (Whisper's 1500 audio frames); T <= 512. Each score is computed identically in the
+ * statistics pass and the filter pass, so the result equals wdrz_dtw_prep applied to
+ * wdrz_dtw_qk's output up to the fp32 rounding of the summation order of the dot products.
+ */
+int wdrz_dtw_attention_prep(int dtype, const void* const* q_heads, const int64_t* q_strides,
+                            const void* const* k_heads, const int64_t* k_strides, float scale,
+                            const int32_t* actual_lens, const int32_t* audio_caps, float* out,
+                            const int64_t* out_strides, int64_t B, int64_t H, int64_t T,
+                            int64_t A, int64_t D, int64_t C, int medfilt_width, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -193,6 +193,42 @@ def test_dtw_qk_empty_is_a_no_op(lib):
     assert call_qk(lib, B=0) == 0
 
 
+def call_attn_prep(lib, **over):
+    H = over.pop("H", 2)
+    ptrs = (ctypes.c_void_p * max(H, 1))(*([FAKE] * max(H, 1)))
+    args = dict(dtype=2, q=ptrs, qs=(ctypes.c_int64 * 3)(40 * 1280, 1280, 1), k=ptrs,
+                ks=(ctypes.c_int64 * 3)(1500 * 1280, 1280, 1), scale=64 ** -0.25, lens=FAKE, caps=FAKE, out=FAKE,
+                os_=(ctypes.c_int64 * 3)(40 * 1500, 1500, 1), B=1, T=40, A=1500, D=64, C=1500, width=7,
+                work=None, work_bytes=0)
+    args.update(over)
+    return lib.wdrz_dtw_attention_prep(args["dtype"], args["q"], args["qs"], args["k"], args["ks"], args["scale"],
+                                       args["lens"], args["caps"], args["out"], args["os_"], args["B"], H,
+                                       args["T"], args["A"], args["D"], args["C"], args["width"], args["work"],
+                                       args["work_bytes"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(A=1537, C=1537), 2, "exceed the supported 1536"),
+    (dict(dtype=0), 2, "only WDRZ_BF16 / WDRZ_F16"),
+    (dict(D=128), 2, "head_dim"),
+    (dict(H=33), 2, "exceed the supported 32"),
+    (dict(scale=float("nan")), 1, "scale"),
+    (dict(width=4), 1, "must be 1 or odd"),
+    (dict(T=513), 2, "exceed the supported 512"),
+    (dict(C=1501), 1, "exceeds A"),
+    (dict(lens=None), 1, "actual_lens"),
+    (dict(), 4, "workspace"),
+])
+def test_dtw_attention_prep_rejects_bad_arguments(lib, over, code, msg):
+    assert call_attn_prep(lib, **over) == code
+    assert msg in lib.wdrz_last_error().decode()
+
+
+def test_dtw_attention_prep_empty_is_a_no_op(lib):
+    assert call_attn_prep(lib, B=0) == 0
+    assert call_attn_prep(lib, C=0) == 0
+
+
 @pytest.mark.parametrize("over,code,msg", [
     (dict(n=200), 1, "reflect padding"),
     (dict(n_mels=129), 2, "exceeds the supported 128"),

@@ -201,3 +201,114 @@ def test_compute_attention_rejects(cuda):
     mask[0, 0] = True
     with pytest.raises(TypeError):
         compute_attention([q_out[0].to(cuda)], [k_out[0].to(cuda)], mask)  # fp32 projections
+
+
+# ---- fused: compute_attention + prep without the score tensor (dtw_align.py:1184-1197) ------
+# Against the float64 oracle chain dtw_prep_ref(compute_attention_ref(...)): the scores carry
+# fp32 accumulation error (about 1e-7 of |S|), which the column normalisation can amplify, so
+# the bound is 1e-4 * max |ref|; against the two-kernel GPU chain (the same fp32 products,
+# summed in another order) the same bound holds.
+FUSED_TOL_REL = 1e-4
+
+
+def _check_fused(got, ref, what):
+    got = got.detach().cpu().numpy().astype(np.float64)
+    ref = np.asarray(ref, dtype=np.float64)
+    assert got.shape == ref.shape, (what, got.shape, ref.shape)
+    nan_ref = np.isnan(ref)
+    assert np.array_equal(np.isnan(got), nan_ref), f"{what}: NaN pattern differs"
+    fin = ~nan_ref
+    if fin.any():
+        err = float(np.max(np.abs(got[fin] - ref[fin])))
+        bound = FUSED_TOL_REL * float(np.max(np.abs(ref[fin])))
+        assert err <= bound, f"{what}: max|diff|={err:.3e} > {bound:.3e}"
+
+
+def _mask(n_layers, n_heads, pairs):
+    m = torch.zeros(n_layers, n_heads, dtype=torch.bool)
+    for l, h in pairs:
+        m[l, h] = True
+    return m
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,T,A,lens,caps,width", [
+    (2, 37, 1500, [37, 20], [1500, 751], 7),     # Whisper's audio axis, ragged text / caps
+    (3, 64, 203, [64, 1, 30], [203, 100, 0], 7),  # cap 0 -> NaN row; one valid text row
+    (1, 5, 70, [5], [70], 3),
+    (2, 130, 257, [200, 130], [257, 3], 5),      # length beyond T; cap 3
+    (1, 17, 5, [17], [5], 7),                    # A = 5: reflect halo on both sides at once
+    (1, 9, 3, [9], [3], 7),                      # A <= width // 2: unfiltered
+    (1, 33, 1536, [33], [1536], 15),             # the largest audio axis, widest filter
+    (2, 20, 96, [0, 20], [96, 96], 1),           # length 0 -> NaN row; no filter
+])
+def test_attention_prep_fused(cuda, dtype, B, T, A, lens, caps, width):
+    from whisperdrz_amd import dtw_attention_prep
+
+    n_layers, n_heads = 6, 20
+    q_out, k_out = _captures(B, T, A, n_layers, n_heads, dtype, seed=7 * B + T + A + width)
+    head_mask = _mask(n_layers, n_heads, [(1, 0), (1, 17), (3, 5), (4, 19), (5, 2), (5, 11)])
+    what = f"dtw_attention_prep {dtype} B={B} T={T} A={A} width={width}"
+    print(what, flush=True)
+    got = dtw_attention_prep([q.to(cuda) for q in q_out], [k.to(cuda) for k in k_out], head_mask, lens, caps,
+                             width)
+    torch.cuda.synchronize()
+    ref = dtw_prep_ref(_qk_ref(q_out, k_out, head_mask, n_heads), lens, caps, width)
+    _check_fused(got, ref, what)
+
+
+def test_attention_prep_fused_many_heads_and_layouts(cuda):
+    # 32 heads (the most the entry takes), one projection a column slice of a wider tensor
+    from whisperdrz_amd import dtw_attention_prep
+
+    B, T, A, n_layers, n_heads = 2, 48, 1500, 2, 20
+    q_out, k_out = _captures(B, T, A, n_layers, n_heads, torch.bfloat16, seed=91)
+    wide = torch.randn(B, T, 2 * n_heads * 64, generator=torch.Generator().manual_seed(92)).to(torch.bfloat16)
+    q_out[1] = wide[:, :, : n_heads * 64]
+    head_mask = _mask(n_layers, n_heads, [(l, h) for l in range(2) for h in range(16)])
+    lens, caps = [48, 31], [1500, 1100]
+    print("dtw_attention_prep 32 heads, mixed layouts", flush=True)
+    dev_q = [q_out[0].to(cuda), wide.to(cuda)[:, :, : n_heads * 64]]
+    got = dtw_attention_prep(dev_q, [k.to(cuda) for k in k_out], head_mask, lens, caps)
+    torch.cuda.synchronize()
+    ref = dtw_prep_ref(_qk_ref([q.contiguous() for q in q_out], k_out, head_mask, n_heads), lens, caps, 7)
+    _check_fused(got, ref, "dtw_attention_prep 32 heads")
+
+
+def test_attention_prep_fused_bench_shape_matches_chain(cuda):
+    # The bench workload: 16 chunks x 448 text rows x 1500 audio columns, large-v3's 10
+    # alignment heads, against compute_attention + dtw_prep on the same GPU, and repeatable.
+    from whisperdrz_amd import compute_attention, dtw_attention_prep, dtw_prep
+
+    B, T, A, n_layers, n_heads = 16, 448, 1500, 32, 20
+    heads = [(7, 0), (10, 17), (12, 18), (13, 12), (16, 1), (17, 14), (19, 11), (21, 4), (24, 1), (25, 6)]
+    g = torch.Generator(device=cuda).manual_seed(5)
+    used = {l for l, _ in heads}
+    q_out = [torch.randn(B, T, n_heads * 64, generator=g, device=cuda).to(torch.bfloat16) if l in used else None
+             for l in range(n_layers)]
+    k_out = [torch.randn(B, A, n_heads * 64, generator=g, device=cuda).to(torch.bfloat16) if l in used else None
+             for l in range(n_layers)]
+    head_mask = _mask(n_layers, n_heads, heads)
+    rng = np.random.default_rng(5)
+    lens = [int(x) for x in rng.integers(T // 2, T + 1, B)]
+    caps = [int(x) for x in rng.integers(A // 2, A + 1, B)]
+    caps[0] = A
+    print("dtw_attention_prep bench shape vs chain", flush=True)
+    got = dtw_attention_prep(q_out, k_out, head_mask, lens, caps)
+    again = dtw_attention_prep(q_out, k_out, head_mask, lens, caps)
+    chain = dtw_prep(compute_attention(q_out, k_out, head_mask), lens, caps)
+    torch.cuda.synchronize()
+    assert torch.equal(got, again)
+    err = (got - chain).abs().max().item()
+    assert err <= FUSED_TOL_REL * chain.abs().max().item(), err
+
+
+def test_attention_prep_fused_rejects(cuda):
+    from whisperdrz_amd import dtw_attention_prep
+
+    q_out, k_out = _captures(1, 4, 1600, 1, 20, torch.bfloat16, seed=3)
+    mask = _mask(1, 20, [(0, 0)])
+    with pytest.raises(NotImplementedError):  # audio axis beyond 1536
+        dtw_attention_prep([q_out[0].to(cuda)], [k_out[0].to(cuda)], mask, [4], [1600])
+    with pytest.raises(ValueError):
+        dtw_attention_prep([q_out[0].to(cuda)], [k_out[0].to(cuda)], mask, [4, 4], [8, 8])  # B mismatch

@@ -28,6 +28,7 @@ EXPORTED_SYMBOLS = (
     "wdrz_dtw_qk",
     "wdrz_dtw_prep_workspace_size",
     "wdrz_dtw_prep",
+    "wdrz_dtw_attention_prep",
 )
 ABI_VERSION = 1
 
@@ -95,6 +96,13 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.wdrz_dtw_prep.argtypes = [
         _p, _i64p, _i32p, _i32p, _p, _i64p,  # weights, strides, lens, caps, out, out strides
         _i64, _i64, _i64, _i64, _i64, ctypes.c_int,  # B, H, T, A, C, medfilt_width
+        _p, ctypes.c_size_t, _p,  # workspace, bytes, stream
+    ]
+    lib.wdrz_dtw_attention_prep.restype = ctypes.c_int
+    lib.wdrz_dtw_attention_prep.argtypes = [
+        ctypes.c_int, _p, _i64p, _p, _i64p, ctypes.c_float,  # dtype, q_heads, q strides, k_heads, k strides, scale
+        _i32p, _i32p, _p, _i64p,  # lens, caps, out, out strides
+        _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int,  # B, H, T, A, D, C, medfilt_width
         _p, ctypes.c_size_t, _p,  # workspace, bytes, stream
     ]
 

@@ -822,6 +822,293 @@ __global__ __launch_bounds__(NT) void dtw_band_kernel(DtwArgs a) {
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Fused path: the scores S = (Q_h K_h^T) * s^2 of the alignment heads are computed on the matrix
+// cores inside both passes (CrossAttnCapture.compute_attention, dtw_align.py:553-586, then
+// _dtw_prep_batch), so the [B, H, T, A] fp32 tensor is never written or read.
+//
+// One 16 x 16 score tile = two v_mfma_f32_16x16x32 over the 64 head dimensions; both passes
+// call qk_tile with the same operands, so every score is bit-identical between them (the exact
+// zero of a zero-variance column depends on it). Lane l: text row 4*(l/16) + i of the tile
+// (i = 0..3), key l % 16; operands are 16-byte slices of the head rows (dims 8*(l/16) and
+// 32 + 8*(l/16)).
+// ---------------------------------------------------------------------------------------------
+template <typename T> struct QkMfma;
+template <> struct QkMfma<Bf16> {
+  typedef bf16x8 op_t;
+  static __device__ __forceinline__ f32x4 run(op_t a, op_t b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct QkMfma<F16> {
+  typedef f16x8 op_t;
+  static __device__ __forceinline__ f32x4 run(op_t a, op_t b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <typename T>
+__device__ __forceinline__ void qk_row_ops(const DtwQkArgs& q, int h, int b, int t,
+                                           typename QkMfma<T>::op_t (&qa)[2]) {
+  typedef typename QkMfma<T>::op_t op_t;
+  const int kh = 8 * ((threadIdx.x & 63) >> 4);
+  const char* row = static_cast<const char*>(q.q[h]) + (b * q.qs[0] + (int64_t)t * q.qs[1]) * 2;
+  qa[0] = __builtin_bit_cast(op_t, *reinterpret_cast<const u32x4*>(row + kh * 2));
+  qa[1] = __builtin_bit_cast(op_t, *reinterpret_cast<const u32x4*>(row + (32 + kh) * 2));
+}
+
+template <typename T>
+__device__ __forceinline__ f32x4 qk_tile(const DtwQkArgs& q, int h, int b, int key,
+                                         const typename QkMfma<T>::op_t (&qa)[2]) {
+  typedef typename QkMfma<T>::op_t op_t;
+  const int kh = 8 * ((threadIdx.x & 63) >> 4);
+  const char* row = static_cast<const char*>(q.k[h]) + (b * q.ks[0] + (int64_t)key * q.ks[1]) * 2;
+  const op_t k0 = __builtin_bit_cast(op_t, *reinterpret_cast<const u32x4*>(row + kh * 2));
+  const op_t k1 = __builtin_bit_cast(op_t, *reinterpret_cast<const u32x4*>(row + (32 + kh) * 2));
+  f32x4 acc = QkMfma<T>::run(qa[0], k0, f32x4{0.f, 0.f, 0.f, 0.f});
+  acc = QkMfma<T>::run(qa[1], k1, acc);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) acc[i] *= q.scale2;
+  return acc;
+}
+
+// max / sum over the 16 lanes of a lane group (one DPP row), every lane gets the result
+__device__ __forceinline__ float group16_max(float v) {
+  v = fmaxf(v, dpp_xor1(v));
+  v = fmaxf(v, dpp_xor2(v));
+  v = fmaxf(v, dpp_half_mirror(v));
+  return fmaxf(v, dpp_row_mirror(v));
+}
+// sum over lanes l, l^16, l^32, l^48 (the four lane groups), every lane gets the result
+__device__ __forceinline__ float groups4_sum(float v) {
+  const auto r32 = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(r32[0]) + __uint_as_float(r32[1]);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
+}
+
+constexpr int kQkTilesPerWave = 24;  // 4 wavefronts x 24 tiles x 16 keys = 1536 >= A
+
+// Row statistics and column Welford partials of one (row chunk, h, b) from Q / K: 16 text rows
+// at a time, the 4 wavefronts splitting the key tiles (tile j on wavefront j % 4). Row max and
+// sum: within a lane, across its lane group (DPP), across the wavefronts (LDS). Each column's
+// Welford state lives in LDS and is only touched by the wavefront owning its tile; a block of
+// up to 16 valid rows is folded in by its exact block mean / M2 and Chan's merge.
+template <typename T>
+__global__ __launch_bounds__(256) void dtw_qk_rowcol_kernel(DtwArgs a, DtwQkArgs q) {
+  typedef typename QkMfma<T>::op_t op_t;
+  const int chunk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int grp = lane >> 4;
+  const int cap = clamp_cap(a.caps[b], a.A);
+  const int len = a.lens[b];
+  if (cap <= 0 || len <= 0) return;  // the filter writes NaN for this batch row
+  const int rows_valid = len < a.T ? len : a.T;
+  const int64_t bh = (int64_t)b * a.H + h;
+  const int n_tiles = (a.A + 15) >> 4;
+
+  __shared__ float2 colst[kQkTilesPerWave * 4 * 16];  // (mean, M2) per key column
+  __shared__ float red[2][4][16];                     // per-wavefront row max / row sum
+  for (int c = threadIdx.x; c < kQkTilesPerWave * 4 * 16; c += 256) colst[c] = make_float2(0.f, 0.f);
+  __syncthreads();
+
+  const int t_lo = chunk * a.rc_rows;
+  const int t_hi = min(t_lo + a.rc_rows, a.T);
+  float n_done = 0.f;  // valid rows folded in so far (the same in every lane)
+  for (int t0 = t_lo; t0 < t_hi; t0 += 16) {
+    op_t qa[2];
+    qk_row_ops<T>(q, h, b, min(t0 + (lane & 15), a.T - 1), qa);
+    float s[kQkTilesPerWave][4];
+    float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
+#pragma unroll
+    for (int u = 0; u < kQkTilesPerWave; ++u) {
+      const int j = wave + 4 * u;
+      const int key = 16 * j + (lane & 15);
+      const f32x4 acc = qk_tile<T>(q, h, b, min(key, a.A - 1), qa);
+      const bool ok = j < n_tiles && key < cap;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[u][i] = ok ? acc[i] : -INFINITY;
+        mx[i] = fmaxf(mx[i], s[u][i]);
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) mx[i] = group16_max(mx[i]);
+    if ((lane & 15) == 0)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[0][wave][4 * grp + i] = mx[i];
+    __syncthreads();
+    float2 st[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * grp + i;
+      st[i].x = fmaxf(fmaxf(red[0][0][r], red[0][1][r]), fmaxf(red[0][2][r], red[0][3][r])) * kLog2e;
+    }
+    float sm[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int u = 0; u < kQkTilesPerWave; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        s[u][i] = softmax_exp(s[u][i], st[i].x);  // -inf -> 0
+        sm[i] += s[u][i];
+      }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sm[i] = group_sum<16>(sm[i]);
+    if ((lane & 15) == 0)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) red[1][wave][4 * grp + i] = sm[i];
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * grp + i;
+      st[i].y = 1.f / (red[1][0][r] + red[1][1][r] + red[1][2][r] + red[1][3][r]);
+    }
+    if (wave == 0 && (lane & 15) < 4 && t0 + 4 * grp + (lane & 15) < a.T) {
+      // rows 4*grp + (lane & 15): the statistics of lane group grp's rows
+      float2 v = st[0];
+      if ((lane & 15) == 1) v = st[1];
+      if ((lane & 15) == 2) v = st[2];
+      if ((lane & 15) == 3) v = st[3];
+      a.rs[bh * a.T + t0 + 4 * grp + (lane & 15)] = v;
+    }
+    // fold the block's valid rows into the column states
+    const int nb = min(16, max(0, rows_valid - t0));
+    if (nb > 0) {
+      bool rv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) rv[i] = t0 + 4 * grp + i < rows_valid;
+      const float fnb = (float)nb;
+#pragma unroll
+      for (int u = 0; u < kQkTilesPerWave; ++u) {
+        float p[4], sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[i] = softmax_scale_e(s[u][i], st[i].y);
+          sum += rv[i] ? p[i] : 0.f;
+        }
+        const float mean_b = groups4_sum(sum) / fnb;
+        float sq = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float d = p[i] - mean_b;
+          sq += rv[i] ? d * d : 0.f;
+        }
+        const float m2_b = groups4_sum(sq);
+        if (grp == 0) {
+          const int c = 16 * (wave + 4 * u) + (lane & 15);
+          float2 cs = colst[c];
+          chan_merge(n_done, cs.x, cs.y, fnb, mean_b, m2_b);
+          colst[c] = cs;
+        }
+      }
+      n_done += fnb;
+    }
+  }
+  // the chunk's partial (mean, M2) of every valid column, for dtw_col_merge_kernel
+  if (n_done > 0.f && grp == 0) {
+    const int n_chunks = (a.T + a.rc_rows - 1) / a.rc_rows;
+    float2* part = a.part + (bh * n_chunks + chunk) * a.cpitch;
+#pragma unroll
+    for (int u = 0; u < kQkTilesPerWave; ++u) {
+      const int c = 16 * (wave + 4 * u) + (lane & 15);
+      if (c < cap) part[c] = colst[c];
+    }
+  }
+}
+
+// Normalise + median filter + head mean from Q / K: one workgroup per (16 text rows, b),
+// 8 wavefronts splitting the key tiles (tile j on wavefront j % 8). Per head the scores of the
+// 16 rows are recomputed, normalised into an LDS tile [16][8 + A + 8] with the reflected halo,
+// and each thread accumulates the medians of its groups of 4 output columns.
+constexpr int kQbTiles = 12;  // 8 wavefronts x 12 tiles x 16 keys = 1536 >= A
+constexpr int kQbPitch = 1536 + 2 * kHalo;
+constexpr int kQbGroups = 12;  // output groups of 4 columns per thread: 16 * 1536 / 4 / 512
+
+template <typename T, int PAD>
+__global__ __launch_bounds__(512) void dtw_qk_band_kernel(DtwArgs a, DtwQkArgs q) {
+  typedef typename QkMfma<T>::op_t op_t;
+  const int b = blockIdx.y;
+  const int t0 = blockIdx.x * 16;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4;
+  const int cap = clamp_cap(a.caps[b], a.A);
+  const int len = a.lens[b];
+  const int C4 = (a.C + 3) >> 2;
+  const int n_rows = min(16, a.T - t0);
+  if (cap <= 0 || len <= 0) {  // 0/0 in the reference: the whole batch row is NaN
+    for (int r = 0; r < n_rows; ++r)
+      for (int c = tid; c < a.C; c += 512) a.out[b * a.os[0] + (int64_t)(t0 + r) * a.os[1] + c] = __builtin_nanf("");
+    return;
+  }
+  __shared__ float tile[16 * kQbPitch];
+  const int n_tiles = (a.A + 15) >> 4;
+
+  float acc[kQbGroups][4];
+#pragma unroll
+  for (int k = 0; k < kQbGroups; ++k)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[k][i] = 0.f;
+
+  for (int h = 0; h < a.H; ++h) {
+    const int64_t bh = (int64_t)b * a.H + h;
+    op_t qa[2];
+    qk_row_ops<T>(q, h, b, min(t0 + (lane & 15), a.T - 1), qa);
+    float2 st[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) st[i] = a.rs[bh * a.T + min(t0 + 4 * grp + i, a.T - 1)];
+    const float2* cs = a.cs + bh * a.cpitch;
+#pragma unroll
+    for (int u = 0; u < kQbTiles; ++u) {
+      const int j = wave + 8 * u;
+      const int key = 16 * j + (lane & 15);
+      if (j < n_tiles) {
+        const f32x4 sc = qk_tile<T>(q, h, b, min(key, a.A - 1), qa);
+        const bool ok = key < cap;
+        const float2 c = ok ? cs[key] : make_float2(0.f, 0.f);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float z = ok ? (softmax_value(sc[i], st[i]) - c.x) * c.y : 0.f;
+          float* row = tile + (4 * grp + i) * kQbPitch + kHalo;
+          if (key < a.A) {
+            row[key] = z;
+            if (PAD > 0) {
+              if (key >= 1 && key <= PAD) row[-key] = z;
+              if (key >= a.A - 1 - PAD && key <= a.A - 2) row[2 * (a.A - 1) - key] = z;
+            }
+          }
+        }
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kQbGroups; ++k) {
+      const int idx = tid + 512 * k;
+      const int r = idx / C4, g = idx - r * C4;
+      if (r < 16) {
+        float win[4 + 2 * PAD];
+        const float* src = tile + r * kQbPitch + kHalo + 4 * g - PAD;
+#pragma unroll
+        for (int i = 0; i < 4 + 2 * PAD; ++i) win[i] = src[i];
+        float med[4];
+        window_medians<PAD>(win, med);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[k][i] += med[i];
+      }
+    }
+    __syncthreads();  // the tile is rewritten by the next head
+  }
+#pragma unroll
+  for (int k = 0; k < kQbGroups; ++k) {
+    const int idx = tid + 512 * k;
+    const int r = idx / C4, g = idx - r * C4;
+    if (r < n_rows) {
+      float* dst = a.out + b * a.os[0] + (int64_t)(t0 + r) * a.os[1] + 4 * g;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (4 * g + i < a.C) dst[i] = acc[k][i] / (float)a.H;
+    }
+  }
+}
+
 }  // namespace
 
 // Workspace: row statistics [B*H*T], column statistics [B*H, cpitch], chunk partials
@@ -910,6 +1197,37 @@ hipError_t launch_dtw_prep(DtwArgs a, hipStream_t stream) {
     break;
     WDRZ_FILT(0) WDRZ_FILT(1) WDRZ_FILT(2) WDRZ_FILT(3) WDRZ_FILT(4) WDRZ_FILT(5) WDRZ_FILT(6) WDRZ_FILT(7)
 #undef WDRZ_FILT
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// Rows per chunk of the fused statistics pass: the two-pass chunking rounded up to whole 16-row
+// blocks (never more chunks than the workspace holds).
+static int dtw_qk_chunk_rows(int64_t B, int64_t H, int64_t T) {
+  const int r = dtw_chunk_rows(B, H, T);
+  return (r + 15) / 16 * 16;
+}
+
+hipError_t launch_dtw_qk_prep(int dtype, DtwArgs a, const DtwQkArgs& q, hipStream_t stream) {
+  if ((int64_t)a.B * a.H * a.T == 0 || a.C == 0) return hipSuccess;
+  if (a.A > kQkTilesPerWave * 4 * 16) return hipErrorInvalidValue;
+  a.rc_rows = dtw_qk_chunk_rows(a.B, a.H, a.T);
+  const dim3 g1((a.T + a.rc_rows - 1) / a.rc_rows, a.H, a.B);
+  if (dtype == 2) hipLaunchKernelGGL(dtw_qk_rowcol_kernel<Bf16>, g1, dim3(256), 0, stream, a, q);
+  else hipLaunchKernelGGL(dtw_qk_rowcol_kernel<F16>, g1, dim3(256), 0, stream, a, q);
+  const int need = a.C + a.pad < a.A ? a.C + a.pad : a.A;
+  hipLaunchKernelGGL(dtw_col_merge_kernel, dim3((need + 255) / 256, a.H, a.B), dim3(256), 0, stream, a, need);
+  const dim3 g2((a.T + 15) / 16, a.B);
+  switch (a.pad) {
+#define WDRZ_QB(P)                                                                                   \
+  case P:                                                                                            \
+    if (dtype == 2) hipLaunchKernelGGL((dtw_qk_band_kernel<Bf16, P>), g2, dim3(512), 0, stream, a, q); \
+    else hipLaunchKernelGGL((dtw_qk_band_kernel<F16, P>), g2, dim3(512), 0, stream, a, q);             \
+    break;
+    WDRZ_QB(0) WDRZ_QB(1) WDRZ_QB(2) WDRZ_QB(3) WDRZ_QB(4) WDRZ_QB(5) WDRZ_QB(6) WDRZ_QB(7)
+#undef WDRZ_QB
     default:
       return hipErrorInvalidValue;
   }

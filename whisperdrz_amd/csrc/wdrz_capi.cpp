@@ -58,6 +58,78 @@ int check_ptr(const char* name, const void* p) {
   return WDRZ_OK;
 }
 
+// Validates what wdrz_dtw_prep and wdrz_dtw_attention_prep share and fills the DtwArgs (no
+// scores pointer). Returns WDRZ_OK, an error code, or -1 for "nothing to do".
+int dtw_common_args(const int32_t* actual_lens, const int32_t* audio_caps, float* out, const int64_t* out_strides,
+                    int64_t B, int64_t H, int64_t T, int64_t A, int64_t C, int medfilt_width, void* workspace,
+                    size_t workspace_bytes, wdrz::DtwArgs* a) {
+  if (B < 0 || H <= 0 || T < 0 || A <= 0 || C < 0)
+    return fail(WDRZ_EINVAL, "bad sizes B=%lld H=%lld T=%lld A=%lld C=%lld", (long long)B, (long long)H,
+                (long long)T, (long long)A, (long long)C);
+  if (C > A) return fail(WDRZ_EINVAL, "C=%lld exceeds A=%lld", (long long)C, (long long)A);
+  if (T > wdrz::kDtwMaxRows)
+    return fail(WDRZ_EUNSUPPORTED, "T=%lld text rows exceed the supported %d", (long long)T, wdrz::kDtwMaxRows);
+  if (B > 65535 || H > 65535 || A > (1 << 24) || B * H * T > (int64_t(1) << 31))
+    return fail(WDRZ_EUNSUPPORTED, "sizes too large");
+  if (medfilt_width < 1 || (medfilt_width > 1 && medfilt_width % 2 == 0))
+    return fail(WDRZ_EINVAL, "medfilt_width=%d must be 1 or odd", medfilt_width);
+  if (medfilt_width / 2 > wdrz::kDtwMaxPad)
+    return fail(WDRZ_EUNSUPPORTED, "medfilt_width=%d exceeds the supported %d", medfilt_width,
+                2 * wdrz::kDtwMaxPad + 1);
+  if (!out) return fail(WDRZ_EINVAL, "out is NULL");
+  if (!actual_lens || !audio_caps) return fail(WDRZ_EINVAL, "actual_lens / audio_caps is NULL");
+  if (!out_strides) return fail(WDRZ_EINVAL, "strides pointer is NULL");
+  if (out_strides[2] != 1) return fail(WDRZ_EINVAL, "out: last stride must be 1");
+  if (B == 0 || T == 0 || C == 0) return -1;
+  const size_t need = wdrz::dtw_workspace_bytes(B, H, T, A);
+  if (!workspace || workspace_bytes < need)
+    return fail(WDRZ_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace ? workspace_bytes : 0);
+  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
+    return fail(WDRZ_EINVAL, "workspace is not 256-byte aligned");
+  a->lens = actual_lens;
+  a->caps = audio_caps;
+  a->out = out;
+  a->B = (int)B;
+  a->H = (int)H;
+  a->T = (int)T;
+  a->A = (int)A;
+  a->C = (int)C;
+  const int pad = medfilt_width / 2;
+  a->pad = (medfilt_width > 1 && A > pad) ? pad : 0;  // dtw_align.py:68-69: too short -> unfiltered
+  a->os[0] = out_strides[0];
+  a->os[1] = out_strides[1];
+  wdrz::dtw_workspace_layout(workspace, a);
+  return WDRZ_OK;
+}
+
+// q/k head pointer arrays and strides for the alignment heads (shared by the two QK entry points).
+int dtw_qk_heads(int dtype, const void* const* q_heads, const int64_t* q_strides, const void* const* k_heads,
+                 const int64_t* k_strides, int64_t H, int64_t D, wdrz::DtwQkArgs* a) {
+  if (dtype != WDRZ_BF16 && dtype != WDRZ_F16)
+    return fail(dtype == WDRZ_F32 ? WDRZ_EUNSUPPORTED : WDRZ_EINVAL,
+                "dtype %d: only WDRZ_BF16 / WDRZ_F16 projections are supported", dtype);
+  if (D != 64) return fail(WDRZ_EUNSUPPORTED, "head_dim %lld is not supported (only 64)", (long long)D);
+  if (H <= 0) return fail(WDRZ_EINVAL, "bad head count %lld", (long long)H);
+  if (H > wdrz::kDtwMaxHeads)
+    return fail(WDRZ_EUNSUPPORTED, "%lld heads exceed the supported %d", (long long)H, wdrz::kDtwMaxHeads);
+  if (!q_heads || !k_heads) return fail(WDRZ_EINVAL, "q_heads / k_heads is NULL");
+  if (!q_strides || !k_strides) return fail(WDRZ_EINVAL, "strides pointer is NULL");
+  if (q_strides[2] != 1 || k_strides[2] != 1) return fail(WDRZ_EINVAL, "q/k: head_dim stride must be 1");
+  for (int i = 0; i < 2; ++i)
+    if (((q_strides[i] * 2) & 15) || ((k_strides[i] * 2) & 15))
+      return fail(WDRZ_EINVAL, "q/k: stride[%d] is not 16-byte aligned", i);
+  for (int64_t h = 0; h < H; ++h) {
+    int rc;
+    if ((rc = check_ptr("q_heads[h]", q_heads[h])) || (rc = check_ptr("k_heads[h]", k_heads[h]))) return rc;
+    a->q[h] = q_heads[h];
+    a->k[h] = k_heads[h];
+  }
+  a->qs[0] = q_strides[0];
+  a->qs[1] = q_strides[1];
+  a->ks[0] = k_strides[0];
+  a->ks[1] = k_strides[1];
+  return WDRZ_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -228,42 +300,22 @@ int wdrz_dtw_qk(int dtype, const void* const* q_heads, const int64_t* q_strides,
                 const int64_t* k_strides, float* out, const int64_t* out_strides, int64_t B, int64_t H, int64_t T,
                 int64_t A, int64_t D, float scale, void* stream) {
   g_last_error.clear();
-  if (dtype != WDRZ_BF16 && dtype != WDRZ_F16)
-    return fail(dtype == WDRZ_F32 ? WDRZ_EUNSUPPORTED : WDRZ_EINVAL,
-                "dtype %d: only WDRZ_BF16 / WDRZ_F16 projections are supported", dtype);
-  if (D != 64) return fail(WDRZ_EUNSUPPORTED, "head_dim %lld is not supported (only 64)", (long long)D);
-  if (B < 0 || H <= 0 || T < 0 || A < 0)
-    return fail(WDRZ_EINVAL, "bad sizes B=%lld H=%lld T=%lld A=%lld", (long long)B, (long long)H, (long long)T,
-                (long long)A);
-  if (H > wdrz::kDtwMaxHeads)
-    return fail(WDRZ_EUNSUPPORTED, "%lld heads exceed the supported %d", (long long)H, wdrz::kDtwMaxHeads);
+  if (B < 0 || T < 0 || A < 0)
+    return fail(WDRZ_EINVAL, "bad sizes B=%lld T=%lld A=%lld", (long long)B, (long long)T, (long long)A);
+  wdrz::DtwQkArgs a{};
+  int rc = dtw_qk_heads(dtype, q_heads, q_strides, k_heads, k_strides, H, D, &a);
+  if (rc != WDRZ_OK) return rc;
   if (B * H > 65535 || T > (1 << 24) || A > (1 << 24)) return fail(WDRZ_EUNSUPPORTED, "sizes too large");
   if (!(scale > 0.f) || scale != scale) return fail(WDRZ_EINVAL, "scale must be a positive finite number");
-  if (!q_heads || !k_heads) return fail(WDRZ_EINVAL, "q_heads / k_heads is NULL");
-  if (!q_strides || !k_strides || !out_strides) return fail(WDRZ_EINVAL, "strides pointer is NULL");
+  if (!out_strides) return fail(WDRZ_EINVAL, "strides pointer is NULL");
   if (!out) return fail(WDRZ_EINVAL, "out is NULL");
-  if (q_strides[2] != 1 || k_strides[2] != 1) return fail(WDRZ_EINVAL, "q/k: head_dim stride must be 1");
   if (out_strides[3] != 1) return fail(WDRZ_EINVAL, "out: last stride must be 1");
-  for (int i = 0; i < 2; ++i)
-    if (((q_strides[i] * 2) & 15) || ((k_strides[i] * 2) & 15))
-      return fail(WDRZ_EINVAL, "q/k: stride[%d] is not 16-byte aligned", i);
-  wdrz::DtwQkArgs a{};
-  for (int64_t h = 0; h < H; ++h) {
-    int rc;
-    if ((rc = check_ptr("q_heads[h]", q_heads[h])) || (rc = check_ptr("k_heads[h]", k_heads[h]))) return rc;
-    a.q[h] = q_heads[h];
-    a.k[h] = k_heads[h];
-  }
   if (B == 0 || T == 0 || A == 0) return WDRZ_OK;
   a.out = out;
   a.B = (int)B;
   a.H = (int)H;
   a.T = (int)T;
   a.A = (int)A;
-  a.qs[0] = q_strides[0];
-  a.qs[1] = q_strides[1];
-  a.ks[0] = k_strides[0];
-  a.ks[1] = k_strides[1];
   for (int i = 0; i < 3; ++i) a.os[i] = out_strides[i];
   a.scale2 = scale * scale;
   hipError_t err = wdrz::launch_dtw_qk(dtype, a, reinterpret_cast<hipStream_t>(stream));
@@ -384,49 +436,40 @@ int wdrz_dtw_prep(const float* weights, const int64_t* w_strides, const int32_t*
                   int64_t T, int64_t A, int64_t C, int medfilt_width, void* workspace, size_t workspace_bytes,
                   void* stream) {
   g_last_error.clear();
-  if (B < 0 || H <= 0 || T < 0 || A <= 0 || C < 0)
-    return fail(WDRZ_EINVAL, "bad sizes B=%lld H=%lld T=%lld A=%lld C=%lld", (long long)B, (long long)H,
-                (long long)T, (long long)A, (long long)C);
-  if (C > A) return fail(WDRZ_EINVAL, "C=%lld exceeds A=%lld", (long long)C, (long long)A);
-  if (T > wdrz::kDtwMaxRows)
-    return fail(WDRZ_EUNSUPPORTED, "T=%lld text rows exceed the supported %d", (long long)T, wdrz::kDtwMaxRows);
-  if (B > 65535 || H > 65535 || A > (1 << 24) || B * H * T > (int64_t(1) << 31))
-    return fail(WDRZ_EUNSUPPORTED, "sizes too large");
-  if (medfilt_width < 1 || (medfilt_width > 1 && medfilt_width % 2 == 0))
-    return fail(WDRZ_EINVAL, "medfilt_width=%d must be 1 or odd", medfilt_width);
-  if (medfilt_width / 2 > wdrz::kDtwMaxPad)
-    return fail(WDRZ_EUNSUPPORTED, "medfilt_width=%d exceeds the supported %d", medfilt_width,
-                2 * wdrz::kDtwMaxPad + 1);
   if (!weights) return fail(WDRZ_EINVAL, "weights is NULL");
-  if (!out) return fail(WDRZ_EINVAL, "out is NULL");
-  if (!actual_lens || !audio_caps) return fail(WDRZ_EINVAL, "actual_lens / audio_caps is NULL");
-  if (!w_strides || !out_strides) return fail(WDRZ_EINVAL, "strides pointer is NULL");
+  if (!w_strides) return fail(WDRZ_EINVAL, "strides pointer is NULL");
   if (w_strides[3] != 1) return fail(WDRZ_EINVAL, "weights: last stride must be 1");
-  if (out_strides[2] != 1) return fail(WDRZ_EINVAL, "out: last stride must be 1");
-  if (B == 0 || T == 0 || C == 0) return WDRZ_OK;
-  const size_t need = wdrz::dtw_workspace_bytes(B, H, T, A);
-  if (!workspace || workspace_bytes < need)
-    return fail(WDRZ_EWORKSPACE, "workspace of %zu bytes required (got %zu)", need, workspace ? workspace_bytes : 0);
-  if ((reinterpret_cast<uintptr_t>(workspace) & 255u) != 0)
-    return fail(WDRZ_EINVAL, "workspace is not 256-byte aligned");
-
   wdrz::DtwArgs a{};
+  int rc = dtw_common_args(actual_lens, audio_caps, out, out_strides, B, H, T, A, C, medfilt_width, workspace,
+                           workspace_bytes, &a);
+  if (rc == -1) return WDRZ_OK;
+  if (rc != WDRZ_OK) return rc;
   a.w = weights;
-  a.lens = actual_lens;
-  a.caps = audio_caps;
-  a.out = out;
-  a.B = (int)B;
-  a.H = (int)H;
-  a.T = (int)T;
-  a.A = (int)A;
-  a.C = (int)C;
-  const int pad = medfilt_width / 2;
-  a.pad = (medfilt_width > 1 && A > pad) ? pad : 0;  // dtw_align.py:68-69: too short -> unfiltered
   for (int i = 0; i < 3; ++i) a.ws[i] = w_strides[i];
-  a.os[0] = out_strides[0];
-  a.os[1] = out_strides[1];
-  wdrz::dtw_workspace_layout(workspace, &a);
   hipError_t err = wdrz::launch_dtw_prep(a, reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(WDRZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  return WDRZ_OK;
+}
+
+int wdrz_dtw_attention_prep(int dtype, const void* const* q_heads, const int64_t* q_strides,
+                            const void* const* k_heads, const int64_t* k_strides, float scale,
+                            const int32_t* actual_lens, const int32_t* audio_caps, float* out,
+                            const int64_t* out_strides, int64_t B, int64_t H, int64_t T, int64_t A, int64_t D,
+                            int64_t C, int medfilt_width, void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error.clear();
+  if (!(scale > 0.f) || scale != scale) return fail(WDRZ_EINVAL, "scale must be a positive finite number");
+  if (A > wdrz::kDtwQkMaxA)
+    return fail(WDRZ_EUNSUPPORTED, "A=%lld audio rows exceed the supported %d", (long long)A, wdrz::kDtwQkMaxA);
+  wdrz::DtwQkArgs q{};
+  int rc = dtw_qk_heads(dtype, q_heads, q_strides, k_heads, k_strides, H, D, &q);
+  if (rc != WDRZ_OK) return rc;
+  q.scale2 = scale * scale;
+  wdrz::DtwArgs a{};
+  rc = dtw_common_args(actual_lens, audio_caps, out, out_strides, B, H, T, A, C, medfilt_width, workspace,
+                       workspace_bytes, &a);
+  if (rc == -1) return WDRZ_OK;
+  if (rc != WDRZ_OK) return rc;
+  hipError_t err = wdrz::launch_dtw_qk_prep(dtype, a, q, reinterpret_cast<hipStream_t>(stream));
   if (err != hipSuccess) return fail(WDRZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
   return WDRZ_OK;
 }

@@ -126,6 +126,9 @@ size_t logmel_workspace_bytes(int64_t B, int64_t n_mels);
 hipError_t launch_logmel(LogMelArgs a, void* ws, hipStream_t stream);
 
 size_t dtw_workspace_bytes(int64_t B, int64_t H, int64_t T, int64_t A);
+// The prep with the scores computed from the heads' Q / K inside both passes (A <= 1536).
+constexpr int kDtwQkMaxA = 1536;
+hipError_t launch_dtw_qk_prep(int dtype, DtwArgs a, const DtwQkArgs& q, hipStream_t stream);
 void dtw_workspace_layout(void* ws, DtwArgs* a);
 hipError_t launch_dtw_prep(DtwArgs a, hipStream_t stream);
 

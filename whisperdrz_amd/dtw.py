@@ -22,7 +22,7 @@ import torch
 from . import _lib
 from .attention import WorkspaceCache, _check_cuda, _raise, _stream_handle
 
-__all__ = ["compute_attention", "dtw_prep", "dtw_prep_batch", "dtw_prep_workspace_size"]
+__all__ = ["compute_attention", "dtw_attention_prep", "dtw_prep", "dtw_prep_batch", "dtw_prep_workspace_size"]
 
 _QK_DTYPES = {torch.bfloat16: _lib.WDRZ_BF16, torch.float16: _lib.WDRZ_F16}
 
@@ -30,6 +30,49 @@ _QK_DTYPES = {torch.bfloat16: _lib.WDRZ_BF16, torch.float16: _lib.WDRZ_F16}
 # workspace, whose counters must stay zero.
 _DTW_WORKSPACES = WorkspaceCache()
 _PINNED: dict[tuple, torch.Tensor] = {}
+
+
+class _Heads:
+    """The selected heads' query / key slices as one set of per-head pointers with shared strides."""
+
+    def __init__(self, q_out, k_out, head_mask):
+        mask = torch.as_tensor(head_mask)
+        n_heads = int(mask.shape[1])
+        sel = mask.nonzero().tolist()
+        if not sel:
+            raise ValueError("head_mask selects no heads")
+        q_views, k_views = [], []
+        for layer, head in sel:
+            q, k = q_out[layer], k_out[layer]
+            if q is None or k is None:
+                raise ValueError(f"layer {layer} has no captured projection")
+            B, T, width = q.shape
+            D = width // n_heads
+            q_views.append(q.view(B, T, n_heads, D)[:, :, head])
+            k_views.append(k.view(k.shape[0], k.shape[1], n_heads, D)[:, :, head])
+        q0, k0 = q_views[0], k_views[0]
+        self.device = q0.device
+        _check_cuda("q_out", q0, self.device)
+        if q0.dtype not in _QK_DTYPES:
+            raise TypeError(f"q_out: dtype {q0.dtype} is not supported (bfloat16, float16)")
+        self.B, self.T, self.D = (int(x) for x in q0.shape)
+        self.A = int(k0.shape[1])
+        dev = self.device
+        same = all(v.stride() == q0.stride() and v.dtype == q0.dtype and v.device == dev for v in q_views) and all(
+            v.stride() == k0.stride() and v.dtype == q0.dtype and v.device == dev and v.shape[1] == self.A
+            for v in k_views
+        )
+        if not same:  # heads from differently laid-out captures: give them one layout
+            q_views = [v.contiguous() for v in q_views]
+            k_views = [v.to(q0.dtype).contiguous() for v in k_views]
+        self.views = (q_views, k_views)  # keeps the copies alive for the call
+        self.H = len(sel)
+        self.dtype = _QK_DTYPES[q0.dtype]
+        self.qp = (_lib.ctypes.c_void_p * self.H)(*[v.data_ptr() for v in q_views])
+        self.kp = (_lib.ctypes.c_void_p * self.H)(*[v.data_ptr() for v in k_views])
+        self.qs = (_lib.ctypes.c_int64 * 3)(*q_views[0].stride())
+        self.ks = (_lib.ctypes.c_int64 * 3)(*k_views[0].stride())
+        self.scale = float(self.D) ** -0.25  # dtw_align.py:561
 
 
 def compute_attention(q_out, k_out, head_mask) -> torch.Tensor:
@@ -41,47 +84,45 @@ def compute_attention(q_out, k_out, head_mask) -> torch.Tensor:
     Returns fp32 ``[B, n_selected, T_text, T_audio]``, or ``[n_selected, T_text, T_audio]`` when
     B == 1, as the reference does. Each head's slice is read in place; no stacked copies.
     """
-    mask = torch.as_tensor(head_mask)
-    n_heads = int(mask.shape[1])
-    sel = mask.nonzero().tolist()
-    if not sel:
-        raise ValueError("head_mask selects no heads")
-    q_views, k_views = [], []
-    for layer, head in sel:
-        q, k = q_out[layer], k_out[layer]
-        if q is None or k is None:
-            raise ValueError(f"layer {layer} has no captured projection")
-        B, T, width = q.shape
-        D = width // n_heads
-        q_views.append(q.view(B, T, n_heads, D)[:, :, head])
-        k_views.append(k.view(k.shape[0], k.shape[1], n_heads, D)[:, :, head])
-    q0, k0 = q_views[0], k_views[0]
-    device = q0.device
-    _check_cuda("q_out", q0, device)
-    if q0.dtype not in _QK_DTYPES:
-        raise TypeError(f"q_out: dtype {q0.dtype} is not supported (bfloat16, float16)")
-    B, T, D = (int(x) for x in q0.shape)
-    A = int(k0.shape[1])
-    same = all(v.stride() == q0.stride() and v.dtype == q0.dtype and v.device == device for v in q_views) and all(
-        v.stride() == k0.stride() and v.dtype == q0.dtype and v.device == device and v.shape[1] == A
-        for v in k_views
-    )
-    if not same:  # heads from differently laid-out captures: give them one layout
-        q_views = [v.contiguous() for v in q_views]
-        k_views = [v.to(q0.dtype).contiguous() for v in k_views]
-    H = len(sel)
-    out = torch.empty((B, H, T, A), dtype=torch.float32, device=device)
-    qp = (_lib.ctypes.c_void_p * H)(*[v.data_ptr() for v in q_views])
-    kp = (_lib.ctypes.c_void_p * H)(*[v.data_ptr() for v in k_views])
-    qs = (_lib.ctypes.c_int64 * 3)(*q_views[0].stride())
-    ks = (_lib.ctypes.c_int64 * 3)(*k_views[0].stride())
+    hd = _Heads(q_out, k_out, head_mask)
+    B, H, T, A = hd.B, hd.H, hd.T, hd.A
+    out = torch.empty((B, H, T, A), dtype=torch.float32, device=hd.device)
     rc = _lib.load().wdrz_dtw_qk(
-        _QK_DTYPES[q0.dtype], qp, qs, kp, ks, out.data_ptr(), _lib.strides4(out.stride()),
-        B, H, T, A, D, float(D) ** -0.25, _stream_handle(),
+        hd.dtype, hd.qp, hd.qs, hd.kp, hd.ks, out.data_ptr(), _lib.strides4(out.stride()),
+        B, H, T, A, hd.D, hd.scale, _stream_handle(),
     )
     if rc != _lib.WDRZ_OK:
         _raise(rc, "compute_attention")
     return out[0] if B == 1 else out
+
+
+def dtw_attention_prep(q_out, k_out, head_mask, actual_lens: Sequence[int], audio_caps: Sequence[int],
+                       medfilt_width: int = 7) -> torch.Tensor:
+    """``dtw_prep(compute_attention(q_out, k_out, head_mask), actual_lens, audio_caps)`` in one
+    pass over the projections: the scores are recomputed on the matrix cores inside the prep
+    instead of being stored (dtw_align.py:1184-1197). Returns the device tensor
+    ``[B, T_text, max_audio_cap]`` (fp32). T_audio <= 1536."""
+    hd = _Heads(q_out, k_out, head_mask)
+    B, H, T, A = hd.B, hd.H, hd.T, hd.A
+    lens = [int(x) for x in actual_lens]
+    caps = [int(x) for x in audio_caps]
+    if len(lens) != B or len(caps) != B:
+        raise ValueError(f"actual_lens / audio_caps must have {B} entries")
+    C = len(range(A)[: max(caps)])
+    out = torch.empty((B, T, C), dtype=torch.float32, device=hd.device)
+    if T == 0 or C == 0:
+        return out
+    meta = torch.tensor([lens, caps], dtype=torch.int32).pin_memory().to(hd.device, non_blocking=True)
+    nbytes = dtw_prep_workspace_size(B, H, T, A)
+    ws = _DTW_WORKSPACES.get(hd.device, nbytes)
+    rc = _lib.load().wdrz_dtw_attention_prep(
+        hd.dtype, hd.qp, hd.qs, hd.kp, hd.ks, hd.scale, meta[0].data_ptr(), meta[1].data_ptr(),
+        out.data_ptr(), (_lib.ctypes.c_int64 * 3)(*out.stride()), B, H, T, A, hd.D, C, int(medfilt_width),
+        ws.data_ptr() if ws is not None else None, ws.numel() if ws is not None else 0, _stream_handle(),
+    )
+    if rc != _lib.WDRZ_OK:
+        _raise(rc, "dtw_attention_prep")
+    return out
 
 
 def dtw_prep_workspace_size(B: int, H: int, T: int, A: int) -> int:
