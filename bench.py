@@ -595,7 +595,8 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
 def pmc_sample(dev) -> None:
     """A short, fixed kernel sequence for hardware-counter passes (rocprofv3 --pmc):
     a calibration copy of 1 GiB (known HBM bytes), then 3 launches of the encoder kernel, of
-    each decode kernel, of the DTW prep, compute_attention and the log-mel front end at the
+    each decode kernel, of the DTW prep, compute_attention, the fused attention + prep and the
+    log-mel front end at the
     bench shapes (eager)."""
     from whisperdrz_amd import flash_attn_with_kvcache, scaled_dot_product_attention
 
@@ -632,7 +633,7 @@ def pmc_sample(dev) -> None:
         flash_attn_with_kvcache(q5, kv_x[0], kv_x[1], cache_batch_idx=slots, softmax_scale=0.125)
         torch.cuda.synchronize()
         del kv_s, kv_x
-    from whisperdrz_amd import compute_attention, dtw_prep, log_mel_spectrogram
+    from whisperdrz_amd import compute_attention, dtw_attention_prep, dtw_prep, log_mel_spectrogram
 
     for i in range(3):
         w, lens, caps = _dtw_inputs(dev, 5000 + i)
@@ -649,6 +650,11 @@ def pmc_sample(dev) -> None:
         k_out[l] = torch.randn((DTW_B, DTW_A, H * D), generator=g, device=dev).to(torch.bfloat16)
     for _ in range(3):
         compute_attention(q_out, k_out, mask)
+        torch.cuda.synchronize()
+    rng = np.random.default_rng(5000)
+    lens = [int(x) for x in rng.integers(DTW_T // 2, DTW_T + 1, DTW_B)]
+    for _ in range(3):
+        dtw_attention_prep(q_out, k_out, mask, lens, [DTW_A] * DTW_B)
         torch.cuda.synchronize()
     del q_out, k_out
     audio = 0.1 * torch.randn((MEL_B, MEL_N), generator=g, device=dev)

@@ -828,7 +828,7 @@ __global__ __launch_bounds__(NT) void dtw_band_kernel(DtwArgs a) {
 // _dtw_prep_batch), so the [B, H, T, A] fp32 tensor is never written or read.
 //
 // One 16 x 16 score tile = two v_mfma_f32_16x16x32 over the 64 head dimensions; both passes
-// call qk_tile with the same operands, so every score is bit-identical between them (the exact
+// call qk_product with the same operands, so every score is bit-identical between them (the exact
 // zero of a zero-variance column depends on it). Lane l: text row 4*(l/16) + i of the tile
 // (i = 0..3), key l % 16; operands are 16-byte slices of the head rows (dims 8*(l/16) and
 // 32 + 8*(l/16)).
@@ -857,16 +857,28 @@ __device__ __forceinline__ void qk_row_ops(const DtwQkArgs& q, int h, int b, int
   qa[1] = __builtin_bit_cast(op_t, *reinterpret_cast<const u32x4*>(row + (32 + kh) * 2));
 }
 
+template <typename T> struct QkKey {
+  typename QkMfma<T>::op_t k0, k1;
+};
+
 template <typename T>
-__device__ __forceinline__ f32x4 qk_tile(const DtwQkArgs& q, int h, int b, int key,
-                                         const typename QkMfma<T>::op_t (&qa)[2]) {
+__device__ __forceinline__ QkKey<T> qk_key_ops(const DtwQkArgs& q, int h, int b, int key) {
   typedef typename QkMfma<T>::op_t op_t;
   const int kh = 8 * ((threadIdx.x & 63) >> 4);
-  const char* row = static_cast<const char*>(q.k[h]) + (b * q.ks[0] + (int64_t)key * q.ks[1]) * 2;
-  const op_t k0 = __builtin_bit_cast(op_t, *reinterpret_cast<const u32x4*>(row + kh * 2));
-  const op_t k1 = __builtin_bit_cast(op_t, *reinterpret_cast<const u32x4*>(row + (32 + kh) * 2));
-  f32x4 acc = QkMfma<T>::run(qa[0], k0, f32x4{0.f, 0.f, 0.f, 0.f});
-  acc = QkMfma<T>::run(qa[1], k1, acc);
+  // a wave-uniform base and a 32-bit per-lane offset (one batch row of keys is < 4 GiB)
+  const char* base = static_cast<const char*>(q.k[h]) + b * q.ks[0] * 2;
+  const char* row = base + (uint32_t)(key * (uint32_t)q.ks[1] * 2u);
+  QkKey<T> k;
+  k.k0 = __builtin_bit_cast(op_t, *reinterpret_cast<const u32x4*>(row + kh * 2));
+  k.k1 = __builtin_bit_cast(op_t, *reinterpret_cast<const u32x4*>(row + (32 + kh) * 2));
+  return k;
+}
+
+template <typename T>
+__device__ __forceinline__ f32x4 qk_product(const DtwQkArgs& q, const QkKey<T>& k,
+                                            const typename QkMfma<T>::op_t (&qa)[2]) {
+  f32x4 acc = QkMfma<T>::run(qa[0], k.k0, f32x4{0.f, 0.f, 0.f, 0.f});
+  acc = QkMfma<T>::run(qa[1], k.k1, acc);
 #pragma unroll
   for (int i = 0; i < 4; ++i) acc[i] *= q.scale2;
   return acc;
@@ -887,17 +899,41 @@ __device__ __forceinline__ float groups4_sum(float v) {
   return __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
 }
 
-constexpr int kQkTilesPerWave = 24;  // 4 wavefronts x 24 tiles x 16 keys = 1536 >= A
+// Chan's merge of the Welford states (n, mean, M2) held by lanes l and l ^ 32 (X = 32) or by the
+// two 16-lane rows of a pair (X = 16); every lane of the pair gets the same merged state.
+template <int X>
+__device__ __forceinline__ void lane_pair_merge(float& n, float& mean, float& m2) {
+  auto swap = [](float v) {
+    if constexpr (X == 32)
+      return __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    else
+      return __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  };
+  const auto rn = swap(n), rm = swap(mean), rq = swap(m2);
+  float na = __uint_as_float(rn[0]), ma = __uint_as_float(rm[0]), qa = __uint_as_float(rq[0]);
+  chan_merge(na, ma, qa, __uint_as_float(rn[1]), __uint_as_float(rm[1]), __uint_as_float(rq[1]));
+  n = na + __uint_as_float(rn[1]);
+  mean = ma;
+  m2 = qa;
+}
+
+constexpr int kQkWaves = 8;
+constexpr int kQkTilesPerWave = 12;  // 8 wavefronts x 12 tiles x 16 keys = 1536 >= A
 
 // Row statistics and column Welford partials of one (row chunk, h, b) from Q / K: 16 text rows
-// at a time, the 4 wavefronts splitting the key tiles (tile j on wavefront j % 4). Row max and
-// sum: within a lane, across its lane group (DPP), across the wavefronts (LDS). Each column's
-// Welford state lives in LDS and is only touched by the wavefront owning its tile; a block of
-// up to 16 valid rows is folded in by its exact block mean / M2 and Chan's merge.
+// at a time, the 8 wavefronts splitting the key tiles (tile j on wavefront j % 8). Row max and
+// sum: within a lane, across its lane group (DPP), across the wavefronts (LDS). Column states:
+// each lane keeps a running Welford state of its key column over the rows its lane group holds
+// (rows 4*grp .. 4*grp + 3 of every block), folded in 4 rows at a time; the four lane groups'
+// states are merged once, at the end of the chunk.
 template <typename T>
-__global__ __launch_bounds__(256) void dtw_qk_rowcol_kernel(DtwArgs a, DtwQkArgs q) {
+__global__ __launch_bounds__(512) void dtw_qk_rowcol_kernel(DtwArgs a, DtwQkArgs q) {
   typedef typename QkMfma<T>::op_t op_t;
-  const int chunk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  // logical order: chunks fastest, then h, then b; remapped so that the chunks of one head run
+  // on one XCD and read its keys through the same L2
+  const int n_chunks = (a.T + a.rc_rows - 1) / a.rc_rows;
+  const int w = remap_xcd(blockIdx.x, gridDim.x);
+  const int chunk = w % n_chunks, h = (w / n_chunks) % a.H, b = w / (n_chunks * a.H);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int grp = lane >> 4;
   const int cap = clamp_cap(a.caps[b], a.A);
@@ -907,24 +943,32 @@ __global__ __launch_bounds__(256) void dtw_qk_rowcol_kernel(DtwArgs a, DtwQkArgs
   const int64_t bh = (int64_t)b * a.H + h;
   const int n_tiles = (a.A + 15) >> 4;
 
-  __shared__ float2 colst[kQkTilesPerWave * 4 * 16];  // (mean, M2) per key column
-  __shared__ float red[2][4][16];                     // per-wavefront row max / row sum
-  for (int c = threadIdx.x; c < kQkTilesPerWave * 4 * 16; c += 256) colst[c] = make_float2(0.f, 0.f);
-  __syncthreads();
+  // this wavefront's key operands, the same for every row block of the chunk: held in registers
+  QkKey<T> kop[kQkTilesPerWave];
+#pragma unroll
+  for (int u = 0; u < kQkTilesPerWave; ++u)
+    kop[u] = qk_key_ops<T>(q, h, b, min(16 * (wave + kQkWaves * u) + (lane & 15), a.A - 1));
+
+  __shared__ float red[2][kQkWaves][16];  // per-wavefront row max / row sum
+  float mu[kQkTilesPerWave], m2[kQkTilesPerWave];
+#pragma unroll
+  for (int u = 0; u < kQkTilesPerWave; ++u) mu[u] = m2[u] = 0.f;
+  float n_l = 0.f;  // valid rows folded into this lane's states
 
   const int t_lo = chunk * a.rc_rows;
   const int t_hi = min(t_lo + a.rc_rows, a.T);
-  float n_done = 0.f;  // valid rows folded in so far (the same in every lane)
+  op_t qn[2];  // the query rows of the next block, loaded one block ahead
+  qk_row_ops<T>(q, h, b, min(t_lo + (lane & 15), a.T - 1), qn);
   for (int t0 = t_lo; t0 < t_hi; t0 += 16) {
-    op_t qa[2];
-    qk_row_ops<T>(q, h, b, min(t0 + (lane & 15), a.T - 1), qa);
+    op_t qa[2] = {qn[0], qn[1]};
+    if (t0 + 16 < t_hi) qk_row_ops<T>(q, h, b, min(t0 + 16 + (lane & 15), a.T - 1), qn);
     float s[kQkTilesPerWave][4];
     float mx[4] = {-INFINITY, -INFINITY, -INFINITY, -INFINITY};
 #pragma unroll
     for (int u = 0; u < kQkTilesPerWave; ++u) {
-      const int j = wave + 4 * u;
+      const int j = wave + kQkWaves * u;
       const int key = 16 * j + (lane & 15);
-      const f32x4 acc = qk_tile<T>(q, h, b, min(key, a.A - 1), qa);
+      const f32x4 acc = qk_product<T>(q, kop[u], qa);
       const bool ok = j < n_tiles && key < cap;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -942,7 +986,10 @@ __global__ __launch_bounds__(256) void dtw_qk_rowcol_kernel(DtwArgs a, DtwQkArgs
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * grp + i;
-      st[i].x = fmaxf(fmaxf(red[0][0][r], red[0][1][r]), fmaxf(red[0][2][r], red[0][3][r])) * kLog2e;
+      float m = red[0][0][r];
+#pragma unroll
+      for (int w = 1; w < kQkWaves; ++w) m = fmaxf(m, red[0][w][r]);
+      st[i].x = m * kLog2e;
     }
     float sm[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -961,23 +1008,29 @@ __global__ __launch_bounds__(256) void dtw_qk_rowcol_kernel(DtwArgs a, DtwQkArgs
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * grp + i;
-      st[i].y = 1.f / (red[1][0][r] + red[1][1][r] + red[1][2][r] + red[1][3][r]);
-    }
-    if (wave == 0 && (lane & 15) < 4 && t0 + 4 * grp + (lane & 15) < a.T) {
-      // rows 4*grp + (lane & 15): the statistics of lane group grp's rows
-      float2 v = st[0];
-      if ((lane & 15) == 1) v = st[1];
-      if ((lane & 15) == 2) v = st[2];
-      if ((lane & 15) == 3) v = st[3];
-      a.rs[bh * a.T + t0 + 4 * grp + (lane & 15)] = v;
-    }
-    // fold the block's valid rows into the column states
-    const int nb = min(16, max(0, rows_valid - t0));
-    if (nb > 0) {
-      bool rv[4];
+      float t = red[1][0][r];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) rv[i] = t0 + 4 * grp + i < rows_valid;
-      const float fnb = (float)nb;
+      for (int w = 1; w < kQkWaves; ++w) t += red[1][w][r];
+      st[i].y = 1.f / t;
+    }
+    if (wave == 0)  // lane i of lane group grp stores row 4*grp + i
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if ((lane & 15) == i && t0 + 4 * grp + i < a.T) a.rs[bh * a.T + t0 + 4 * grp + i] = st[i];
+    if (t0 < rows_valid) {
+      // fold this lane group's valid rows of the block (0..4 of them) into its column states
+      bool rv[4];
+      float fnb = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        rv[i] = t0 + 4 * grp + i < rows_valid;
+        fnb += rv[i] ? 1.f : 0.f;
+      }
+      const float n_new = n_l + fnb;
+      const bool any = fnb > 0.f;
+      const float inv_nb = any ? 1.f / fnb : 0.f;
+      const float ra = any ? fnb / n_new : 0.f;
+      const float rb = any ? n_l * fnb / n_new : 0.f;
 #pragma unroll
       for (int u = 0; u < kQkTilesPerWave; ++u) {
         float p[4], sum = 0.f;
@@ -986,125 +1039,193 @@ __global__ __launch_bounds__(256) void dtw_qk_rowcol_kernel(DtwArgs a, DtwQkArgs
           p[i] = softmax_scale_e(s[u][i], st[i].y);
           sum += rv[i] ? p[i] : 0.f;
         }
-        const float mean_b = groups4_sum(sum) / fnb;
+        const float mean_b = sum * inv_nb;
         float sq = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const float d = p[i] - mean_b;
           sq += rv[i] ? d * d : 0.f;
         }
-        const float m2_b = groups4_sum(sq);
-        if (grp == 0) {
-          const int c = 16 * (wave + 4 * u) + (lane & 15);
-          float2 cs = colst[c];
-          chan_merge(n_done, cs.x, cs.y, fnb, mean_b, m2_b);
-          colst[c] = cs;
-        }
+        const float d = mean_b - mu[u];
+        mu[u] += d * ra;
+        m2[u] += sq + d * d * rb;
       }
-      n_done += fnb;
+      n_l = n_new;
     }
   }
   // the chunk's partial (mean, M2) of every valid column, for dtw_col_merge_kernel
-  if (n_done > 0.f && grp == 0) {
-    const int n_chunks = (a.T + a.rc_rows - 1) / a.rc_rows;
+  if (t_lo < rows_valid) {
     float2* part = a.part + (bh * n_chunks + chunk) * a.cpitch;
 #pragma unroll
     for (int u = 0; u < kQkTilesPerWave; ++u) {
-      const int c = 16 * (wave + 4 * u) + (lane & 15);
-      if (c < cap) part[c] = colst[c];
+      float n = n_l;
+      lane_pair_merge<32>(n, mu[u], m2[u]);
+      lane_pair_merge<16>(n, mu[u], m2[u]);
+      const int c = 16 * (wave + kQkWaves * u) + (lane & 15);
+      if (grp == 0 && c < cap) part[c] = make_float2(mu[u], m2[u]);
     }
   }
 }
 
-// Normalise + median filter + head mean from Q / K: one workgroup per (16 text rows, b),
-// 8 wavefronts splitting the key tiles (tile j on wavefront j % 8). Per head the scores of the
-// 16 rows are recomputed, normalised into an LDS tile [16][8 + A + 8] with the reflected halo,
-// and each thread accumulates the medians of its groups of 4 output columns.
-constexpr int kQbTiles = 12;  // 8 wavefronts x 12 tiles x 16 keys = 1536 >= A
-constexpr int kQbPitch = 1536 + 2 * kHalo;
-constexpr int kQbGroups = 12;  // output groups of 4 columns per thread: 16 * 1536 / 4 / 512
+// Normalise + median filter + head mean from Q / K. One workgroup per (256 output columns,
+// 32 text rows, b), 4 wavefronts. Per head the scores of the 32 rows over the segment and one
+// 16-key tile of halo on each side are recomputed (key tile j on wavefront j % 4, both 16-row
+// halves from one load of its key operands), normalised into an LDS tile [32][292] (reflected
+// halo at the ends of the audio axis), and each lane accumulates the medians of one group of 4
+// columns in 8 rows. The [B, H, T, A] scores are never stored; each WG reads 18 x 2 KB of K per
+// head.
+constexpr int kQsRows = 32;
+constexpr int kQsSeg = 256;
+constexpr int kQsKeyTiles = kQsSeg / 16 + 2;
+constexpr int kQsPitch = kQsSeg + 32 + 4;  // 16-byte rows; the 4 lane groups' rows on distinct banks
+constexpr int kQsTilesPerWave = (kQsKeyTiles + 3) / 4;
 
 template <typename T, int PAD>
-__global__ __launch_bounds__(512) void dtw_qk_band_kernel(DtwArgs a, DtwQkArgs q) {
+__global__ __launch_bounds__(256, 2) void dtw_qk_band_kernel(DtwArgs a, DtwQkArgs q) {
   typedef typename QkMfma<T>::op_t op_t;
-  const int b = blockIdx.y;
-  const int t0 = blockIdx.x * 16;
+  const int n_seg = (a.C + kQsSeg - 1) / kQsSeg, n_tb = (a.T + kQsRows - 1) / kQsRows;
+  // logical order: row blocks fastest, then segments, then b; remapped so that the work items
+  // reading one batch row's keys run on one XCD
+  const int w = remap_xcd(blockIdx.x, gridDim.x);
+  const int tb = w % n_tb, sg = (w / n_tb) % n_seg, b = w / (n_tb * n_seg);
+  const int c0 = sg * kQsSeg, t0 = tb * kQsRows;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, grp = lane >> 4;
   const int cap = clamp_cap(a.caps[b], a.A);
   const int len = a.lens[b];
-  const int C4 = (a.C + 3) >> 2;
-  const int n_rows = min(16, a.T - t0);
+  const int n_rows = min(kQsRows, a.T - t0);
+  float* out = a.out + b * a.os[0];
   if (cap <= 0 || len <= 0) {  // 0/0 in the reference: the whole batch row is NaN
-    for (int r = 0; r < n_rows; ++r)
-      for (int c = tid; c < a.C; c += 512) a.out[b * a.os[0] + (int64_t)(t0 + r) * a.os[1] + c] = __builtin_nanf("");
+    for (int r = wave; r < n_rows; r += 4)
+      for (int c = c0 + lane; c < min(c0 + kQsSeg, a.C); c += 64) out[(int64_t)(t0 + r) * a.os[1] + c] = __builtin_nanf("");
     return;
   }
-  __shared__ float tile[16 * kQbPitch];
-  const int n_tiles = (a.A + 15) >> 4;
+  // double-buffered: head h is normalised into buffer h % 2, so the writes of head h + 1 never
+  // meet the median reads of head h and one barrier per head suffices
+  __shared__ __align__(16) float tiles[2][kQsRows * kQsPitch];
+  const int key_base = c0 - 16;  // key of tile column 0
 
-  float acc[kQbGroups][4];
+  float acc[kQsRows / 4][4];
 #pragma unroll
-  for (int k = 0; k < kQbGroups; ++k)
+  for (int k = 0; k < kQsRows / 4; ++k)
 #pragma unroll
     for (int i = 0; i < 4; ++i) acc[k][i] = 0.f;
 
-  for (int h = 0; h < a.H; ++h) {
+  // Operands of one head (query rows and row statistics of both halves, key operands and
+  // column statistics of this wavefront's key tiles), loaded one head ahead: the loads of head
+  // h + 1 are in flight during the median phase of head h.
+  struct HeadOps {
+    op_t qa[2][2];
+    float2 st[2][4];
+    QkKey<T> k[kQsTilesPerWave];
+    float2 c[kQsTilesPerWave];
+  };
+  auto load = [&](int h, HeadOps& o) __attribute__((always_inline)) {
     const int64_t bh = (int64_t)b * a.H + h;
-    op_t qa[2];
-    qk_row_ops<T>(q, h, b, min(t0 + (lane & 15), a.T - 1), qa);
-    float2 st[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) st[i] = a.rs[bh * a.T + min(t0 + 4 * grp + i, a.T - 1)];
+    for (int hf = 0; hf < 2; ++hf) {
+      qk_row_ops<T>(q, h, b, min(t0 + 16 * hf + (lane & 15), a.T - 1), o.qa[hf]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o.st[hf][i] = a.rs[bh * a.T + min(t0 + 16 * hf + 4 * grp + i, a.T - 1)];
+    }
     const float2* cs = a.cs + bh * a.cpitch;
 #pragma unroll
-    for (int u = 0; u < kQbTiles; ++u) {
-      const int j = wave + 8 * u;
-      const int key = 16 * j + (lane & 15);
-      if (j < n_tiles) {
-        const f32x4 sc = qk_tile<T>(q, h, b, min(key, a.A - 1), qa);
-        const bool ok = key < cap;
-        const float2 c = ok ? cs[key] : make_float2(0.f, 0.f);
+    for (int i = 0; i < kQsTilesPerWave; ++i) {
+      const int key = key_base + 16 * (wave + 4 * i) + (lane & 15);
+      const int kc = key < 0 ? 0 : (key > a.A - 1 ? a.A - 1 : key);  // a valid address; unused if clamped
+      if (wave + 4 * i < kQsKeyTiles) {
+        o.k[i] = qk_key_ops<T>(q, h, b, kc);
+        o.c[i] = cs[kc];
+      }
+    }
+  };
+  HeadOps cur;
+  load(0, cur);
+  for (int h = 0; h < a.H; ++h) {
+    float* tile = tiles[h & 1];
+    const f32x4* tile4 = reinterpret_cast<const f32x4*>(tile);
+    f32x4 sc_all[kQsTilesPerWave][2];  // every tile's products first: the matrix-core latency overlaps
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float z = ok ? (softmax_value(sc[i], st[i]) - c.x) * c.y : 0.f;
-          float* row = tile + (4 * grp + i) * kQbPitch + kHalo;
-          if (key < a.A) {
-            row[key] = z;
-            if (PAD > 0) {
-              if (key >= 1 && key <= PAD) row[-key] = z;
-              if (key >= a.A - 1 - PAD && key <= a.A - 2) row[2 * (a.A - 1) - key] = z;
+    for (int i = 0; i < kQsTilesPerWave; ++i)
+      if (wave + 4 * i < kQsKeyTiles)
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf) sc_all[i][hf] = qk_product<T>(q, cur.k[i], cur.qa[hf]);
+#pragma unroll
+    for (int i = 0; i < kQsTilesPerWave; ++i) {
+      const int j = wave + 4 * i;  // key tile
+      if (j >= kQsKeyTiles) continue;
+      const int key = key_base + 16 * j + (lane & 15);
+      const bool ok = key >= 0 && key < cap;
+      const float2 c = cur.c[i];
+#pragma unroll
+      for (int hf = 0; hf < 2; ++hf) {
+        float z[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          // computed for every lane (a clamped key has a finite score), then selected: no branch
+          const float v = (softmax_value(sc_all[i][hf][r], cur.st[hf][r]) - c.x) * c.y;
+          z[r] = ok ? v : 0.f;
+        }
+        float* row0 = tile + (16 * hf + 4 * grp) * kQsPitch;
+        if (key >= 0 && key < a.A) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) row0[r * kQsPitch + key - key_base] = z[r];
+        }
+        if constexpr (PAD > 0) {
+          // mirrored copies about column 0 and column A-1; only the tiles at the two ends of
+          // the audio axis hold such keys (a wave-uniform test)
+          const int k0 = key_base + 16 * j;
+          if ((c0 == 0 && k0 <= PAD) || (k0 + 15 >= a.A - 1 - PAD && k0 <= a.A - 2)) {
+            // on a short axis (A <= 2 * PAD + 1) one key can have both mirror images
+            if (c0 == 0 && key >= 1 && key <= PAD) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) row0[r * kQsPitch + 16 - key] = z[r];
+            }
+            const int xr = 2 * (a.A - 1) - key - key_base;
+            if (key >= a.A - 1 - PAD && key <= a.A - 2 && xr < kQsSeg + 32) {
+#pragma unroll
+              for (int r = 0; r < 4; ++r) row0[r * kQsPitch + xr] = z[r];
             }
           }
         }
       }
     }
     __syncthreads();
+    if (h + 1 < a.H) load(h + 1, cur);  // cur is consumed: refill it for the next head
+    {
+      constexpr int kJ0 = (16 - PAD) / 4, kJ1 = (16 + 3 + PAD) / 4;
+      constexpr int kOff = 16 - PAD - 4 * kJ0;
+      constexpr int NJ = kJ1 - kJ0 + 1;
+      // rows 4k + wave; the next row's reads are issued before this row's medians
+      f32x4 segv[2][NJ];
 #pragma unroll
-    for (int k = 0; k < kQbGroups; ++k) {
-      const int idx = tid + 512 * k;
-      const int r = idx / C4, g = idx - r * C4;
-      if (r < 16) {
+      for (int j = 0; j < NJ; ++j) segv[0][j] = tile4[(wave * kQsPitch) / 4 + lane + kJ0 + j];
+#pragma unroll
+      for (int k = 0; k < kQsRows / 4; ++k) {
+        if (k + 1 < kQsRows / 4) {
+          const int rn = 4 * (k + 1) + wave;
+#pragma unroll
+          for (int j = 0; j < NJ; ++j) segv[(k + 1) & 1][j] = tile4[(rn * kQsPitch) / 4 + lane + kJ0 + j];
+        }
         float win[4 + 2 * PAD];
-        const float* src = tile + r * kQbPitch + kHalo + 4 * g - PAD;
 #pragma unroll
-        for (int i = 0; i < 4 + 2 * PAD; ++i) win[i] = src[i];
+        for (int i = 0; i < 4 + 2 * PAD; ++i) win[i] = segv[k & 1][(kOff + i) / 4][(kOff + i) % 4];
         float med[4];
         window_medians<PAD>(win, med);
 #pragma unroll
         for (int i = 0; i < 4; ++i) acc[k][i] += med[i];
       }
     }
-    __syncthreads();  // the tile is rewritten by the next head
   }
 #pragma unroll
-  for (int k = 0; k < kQbGroups; ++k) {
-    const int idx = tid + 512 * k;
-    const int r = idx / C4, g = idx - r * C4;
+  for (int k = 0; k < kQsRows / 4; ++k) {
+    const int r = 4 * k + wave;
     if (r < n_rows) {
-      float* dst = a.out + b * a.os[0] + (int64_t)(t0 + r) * a.os[1] + 4 * g;
+      float* dst = out + (int64_t)(t0 + r) * a.os[1];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (4 * g + i < a.C) dst[i] = acc[k][i] / (float)a.H;
+      for (int i = 0; i < 4; ++i) {
+        const int c = c0 + 4 * lane + i;
+        if (c < a.C) dst[c] = acc[k][i] / (float)a.H;
+      }
     }
   }
 }
@@ -1212,19 +1333,20 @@ static int dtw_qk_chunk_rows(int64_t B, int64_t H, int64_t T) {
 
 hipError_t launch_dtw_qk_prep(int dtype, DtwArgs a, const DtwQkArgs& q, hipStream_t stream) {
   if ((int64_t)a.B * a.H * a.T == 0 || a.C == 0) return hipSuccess;
-  if (a.A > kQkTilesPerWave * 4 * 16) return hipErrorInvalidValue;
+  if (a.A > kQkTilesPerWave * kQkWaves * 16) return hipErrorInvalidValue;
   a.rc_rows = dtw_qk_chunk_rows(a.B, a.H, a.T);
-  const dim3 g1((a.T + a.rc_rows - 1) / a.rc_rows, a.H, a.B);
-  if (dtype == 2) hipLaunchKernelGGL(dtw_qk_rowcol_kernel<Bf16>, g1, dim3(256), 0, stream, a, q);
-  else hipLaunchKernelGGL(dtw_qk_rowcol_kernel<F16>, g1, dim3(256), 0, stream, a, q);
+  const dim3 g1((unsigned)((a.T + a.rc_rows - 1) / a.rc_rows * a.H * a.B));
+  if (dtype == 2) hipLaunchKernelGGL(dtw_qk_rowcol_kernel<Bf16>, g1, dim3(512), 0, stream, a, q);
+  else hipLaunchKernelGGL(dtw_qk_rowcol_kernel<F16>, g1, dim3(512), 0, stream, a, q);
   const int need = a.C + a.pad < a.A ? a.C + a.pad : a.A;
   hipLaunchKernelGGL(dtw_col_merge_kernel, dim3((need + 255) / 256, a.H, a.B), dim3(256), 0, stream, a, need);
-  const dim3 g2((a.T + 15) / 16, a.B);
+  const int64_t n2 = (int64_t)((a.C + kQsSeg - 1) / kQsSeg) * ((a.T + kQsRows - 1) / kQsRows) * a.B;
+  const dim3 g2((unsigned)n2);
   switch (a.pad) {
 #define WDRZ_QB(P)                                                                                   \
   case P:                                                                                            \
-    if (dtype == 2) hipLaunchKernelGGL((dtw_qk_band_kernel<Bf16, P>), g2, dim3(512), 0, stream, a, q); \
-    else hipLaunchKernelGGL((dtw_qk_band_kernel<F16, P>), g2, dim3(512), 0, stream, a, q);             \
+    if (dtype == 2) hipLaunchKernelGGL((dtw_qk_band_kernel<Bf16, P>), g2, dim3(256), 0, stream, a, q); \
+    else hipLaunchKernelGGL((dtw_qk_band_kernel<F16, P>), g2, dim3(256), 0, stream, a, q);             \
     break;
     WDRZ_QB(0) WDRZ_QB(1) WDRZ_QB(2) WDRZ_QB(3) WDRZ_QB(4) WDRZ_QB(5) WDRZ_QB(6) WDRZ_QB(7)
 #undef WDRZ_QB

@@ -464,6 +464,8 @@ int wdrz_dtw_attention_prep(int dtype, const void* const* q_heads, const int64_t
   int rc = dtw_qk_heads(dtype, q_heads, q_strides, k_heads, k_strides, H, D, &q);
   if (rc != WDRZ_OK) return rc;
   q.scale2 = scale * scale;
+  if (A > 0 && ((A - 1) * k_strides[1] + D) * 2 >= (int64_t(1) << 32))
+    return fail(WDRZ_EUNSUPPORTED, "one batch row of keys spans more than 4 GiB");
   wdrz::DtwArgs a{};
   rc = dtw_common_args(actual_lens, audio_caps, out, out_strides, B, H, T, A, C, medfilt_width, workspace,
                        workspace_bytes, &a);
