@@ -257,6 +257,26 @@ def test_attention_prep_fused(cuda, dtype, B, T, A, lens, caps, width):
     _check_fused(got, ref, what)
 
 
+@pytest.mark.parametrize("heads,B,T,A,lens,caps,width", [
+    ([(0, 4)], 1, 1, 1500, [1], [1500], 7),              # one head, one text row (n = 1: zero variance)
+    ([(0, 1), (2, 9), (3, 3)], 2, 33, 1500, [33, 2], [900, 1500], 7),  # odd head count, tiny length
+    ([(1, 0), (1, 1)], 3, 64, 17, [64, 64, 10], [17, 1, 16], 3),       # A = 17 (one key past a tile)
+])
+def test_attention_prep_fused_heads_and_edges(cuda, heads, B, T, A, lens, caps, width):
+    from whisperdrz_amd import dtw_attention_prep
+
+    n_layers, n_heads = 4, 20
+    q_out, k_out = _captures(B, T, A, n_layers, n_heads, torch.float16, seed=1000 + T + A)
+    head_mask = _mask(n_layers, n_heads, heads)
+    what = f"dtw_attention_prep H={len(heads)} B={B} T={T} A={A} width={width}"
+    print(what, flush=True)
+    got = dtw_attention_prep([q.to(cuda) for q in q_out], [k.to(cuda) for k in k_out], head_mask, lens, caps,
+                             width)
+    torch.cuda.synchronize()
+    ref = dtw_prep_ref(_qk_ref(q_out, k_out, head_mask, n_heads), lens, caps, width)
+    _check_fused(got, ref, what)
+
+
 def test_attention_prep_fused_many_heads_and_layouts(cuda):
     # 32 heads (the most the entry takes), one projection a column slice of a wider tensor
     from whisperdrz_amd import dtw_attention_prep
