@@ -13,7 +13,9 @@ cached attention, so the HIP kernels can be exercised exactly as WhisperDRZ driv
   ``seq_lens`` bump after all layers, final LN and tied-embedding logits (model.py:570-617,
   824-869).
 * ``TextDecoderStack._fused_blocks`` — the same blocks with each residual add fused into the
-  next LayerNorm (``decode_ops.add_layernorm_``), the default for 16-bit GPU activations.
+  next LayerNorm (``decode_ops.add_layernorm_``), the step's metadata (int32 slot map, every
+  layer's gathered lengths) computed once per step and the self-attention query / key / value
+  projections as one GEMM; the default for 16-bit GPU activations.
 * ``BucketedDecodeGraphs`` — one captured decode step per batch bucket, replayed with static
   token / position / slot buffers (reference ``transcriber.py:18-173``); on ROCm
   ``torch.cuda.CUDAGraph`` is a hipGraph.
@@ -47,6 +49,18 @@ def bucket_for(batch: int, buckets: list[int]) -> int:
     return batch
 
 
+def lengths_matrix(self_kv: list[FlashKVCache]) -> Optional[Tensor]:
+    """The ``[n_layers, n_slots]`` tensor whose row ``l`` is ``self_kv[l].seq_lens`` (as
+    ``KVSlotPool`` lays them out), or None when the layers' lengths are separate tensors."""
+    base = self_kv[0].seq_lens._base if self_kv else None
+    if base is None or base.dim() != 2 or base.shape[0] != len(self_kv) or not base.is_contiguous():
+        return None
+    for l, s in enumerate(self_kv):
+        if s.seq_lens._base is not base or s.seq_lens.data_ptr() != base[l].data_ptr() or s.seq_lens.shape != base[l].shape:
+            return None
+    return base
+
+
 class MultiHeadAttention(nn.Module):
     def __init__(self, n_state: int, n_head: int, causal: bool = False,
                  attn_kvcache: Callable = flash_attn_with_kvcache, attn_dense: Callable = scaled_dot_product_attention):
@@ -69,6 +83,39 @@ class MultiHeadAttention(nn.Module):
         scale = d ** -0.25
         o = self.attn_dense(heads(q), heads(k), heads(v), is_causal=self.causal and T > 1, scale=scale * scale)
         return self.out(o.permute(0, 2, 1, 3).reshape(B, T, self.n_state))
+
+    def qkv_weight(self) -> tuple[Tensor, Tensor]:
+        """``[query; key; value]`` weights ``[3*n_state, n_state]`` and bias (the key's part zero)
+        as one projection, rebuilt whenever a parameter is replaced or modified in place."""
+        ps = (self.query.weight, self.key.weight, self.value.weight, self.query.bias, self.value.bias)
+        key = tuple((p.data_ptr(), p._version, p.dtype) for p in ps)
+        cached = getattr(self, "_qkv_cache", None)
+        if cached is None or cached[0] != key:
+            with torch.no_grad():
+                w = torch.cat([self.query.weight, self.key.weight, self.value.weight])
+                b = torch.cat([self.query.bias, torch.zeros_like(self.query.bias), self.value.bias])
+            cached = (key, w, b)
+            self._qkv_cache = cached
+        return cached[1], cached[2]
+
+    def forward_flash_step(self, x: Tensor, kv_cache: FlashKVCache, is_cross_attn: bool,
+                           cache_seqlens: Optional[Tensor], batch_idx: Optional[Tensor]) -> Tensor:
+        """``forward_flash`` with the step's metadata computed once by the caller (the gathered
+        ``cache_seqlens`` and the int32 slot map) and, for self-attention, the query / key /
+        value projections as one GEMM. Same arithmetic per output element."""
+        B, seq_len, _ = x.shape
+        d = self.n_state // self.n_head
+        if is_cross_attn:
+            q = self.query(x).view(B, seq_len, self.n_head, d)
+            o = self.attn_kvcache(q, kv_cache.k_cache, kv_cache.v_cache, cache_batch_idx=batch_idx,
+                                  softmax_scale=d ** -0.5, causal=False)
+        else:
+            w, b = self.qkv_weight()
+            qkv = F.linear(x, w, b).view(B, seq_len, 3, self.n_head, d)
+            o = self.attn_kvcache(qkv[:, :, 0], kv_cache.k_cache, kv_cache.v_cache, k=qkv[:, :, 1], v=qkv[:, :, 2],
+                                  cache_seqlens=cache_seqlens, cache_batch_idx=batch_idx, softmax_scale=d ** -0.5,
+                                  causal=self.causal)
+        return self.out(o.reshape(B, seq_len, self.n_state))
 
     def forward_flash(self, x: Tensor, kv_cache: FlashKVCache, is_cross_attn: bool = False,
                       slot_indices: Optional[Tensor] = None) -> Tensor:
@@ -145,11 +192,18 @@ class TextDecoderStack(nn.Module):
                 x = block.forward_flash(x, s_kv, c_kv, slot_indices=slot_indices)
             h = self.ln(x)
         # the attention never bumps lengths; the caller does, after all layers
-        for s_kv in self_kv:
+        lens = lengths_matrix(self_kv)
+        if lens is not None:  # every layer's row at once, same indexing as per layer
             if slot_indices is not None:
-                s_kv.seq_lens[slot_indices] += seq_len
+                lens[:, slot_indices] += seq_len
             else:
-                s_kv.seq_lens[:B] += seq_len
+                lens[:, :B] += seq_len
+        else:
+            for s_kv in self_kv:
+                if slot_indices is not None:
+                    s_kv.seq_lens[slot_indices] += seq_len
+                else:
+                    s_kv.seq_lens[:B] += seq_len
         return h @ self.token_embedding.weight.to(h.dtype).T
 
     def _fused_blocks(self, x: Tensor, self_kv: list[FlashKVCache], cross_kv: list[FlashKVCache],
@@ -157,11 +211,22 @@ class TextDecoderStack(nn.Module):
         """The blocks of ``forward_flash`` with each residual add fused into the next LayerNorm
         (model.py:420-433): x is the residual stream, updated in place; returns ln(x)."""
         blocks = list(self.blocks)
+        # the step's metadata once, not per layer: the int32 slot map and every layer's gathered
+        # self lengths (one gather from the [n_layers, n_slots] lengths when the layers' lengths
+        # are its rows)
+        B = x.shape[0]
+        batch_idx = None if slot_indices is None else slot_indices.to(torch.int32)
+        lens = lengths_matrix(self_kv)
+        if lens is not None:
+            seqlens = (lens[:, slot_indices] if slot_indices is not None else lens[:, :B]).contiguous()
+            layer_lens = [seqlens[i] for i in range(len(blocks))]
+        else:
+            layer_lens = [s.seq_lens if slot_indices is None else s.seq_lens[slot_indices] for s in self_kv]
         h = layer_norm(x, blocks[0].attn_ln)
         for i, (block, s_kv, c_kv) in enumerate(zip(blocks, self_kv, cross_kv, strict=True)):
-            d = block.attn.forward_flash(h, s_kv, is_cross_attn=False, slot_indices=slot_indices)
+            d = block.attn.forward_flash_step(h, s_kv, False, layer_lens[i], batch_idx)
             h = add_layernorm_(x, d, block.cross_attn_ln)
-            d = block.cross_attn.forward_flash(h, c_kv, is_cross_attn=True, slot_indices=slot_indices)
+            d = block.cross_attn.forward_flash_step(h, c_kv, True, None, batch_idx)
             h = add_layernorm_(x, d, block.mlp_ln)
             d = block.mlp(h)
             h = add_layernorm_(x, d, blocks[i + 1].attn_ln if i + 1 < len(blocks) else self.ln)

@@ -147,7 +147,9 @@ class KVSlotPool:
 
     ``self_kv[l]`` / ``cross_kv[l]`` are ``FlashKVCache`` objects whose storage are slices of
     the arena. Self caches of all layers share nothing but the arena; each layer keeps its
-    own ``seq_lens`` as in the reference.
+    own ``seq_lens`` as in the reference, stored as row ``l`` of one ``[n_layers, n_slots]``
+    int32 tensor (``self_seq_lens``) so that a decode step can gather and bump every layer's
+    lengths with one operation each.
     """
 
     def __init__(self, n_layers: int, n_slots: int, n_heads: int = 20, head_dim: int = 64,
@@ -171,9 +173,11 @@ class KVSlotPool:
 
         self.self_kv: list[FlashKVCache] = []
         self.cross_kv: list[FlashKVCache] = []
-        for _ in range(n_layers):
+        self.self_seq_lens = torch.zeros((n_layers, n_slots), dtype=torch.int32, device=self.arena.device)
+        for l in range(n_layers):
             ks, vs = take(self_len), take(self_len)
-            self.self_kv.append(FlashKVCache(n_slots, self_len, n_heads, head_dim, k_storage=ks, v_storage=vs))
+            self.self_kv.append(FlashKVCache(n_slots, self_len, n_heads, head_dim, k_storage=ks, v_storage=vs,
+                                             seq_lens=self.self_seq_lens[l]))
             kx, vx = take(cross_len), take(cross_len)
             self.cross_kv.append(FlashKVCache(n_slots, cross_len, n_heads, head_dim, k_storage=kx, v_storage=vx))
 
