@@ -54,10 +54,10 @@ __device__ __forceinline__ float wave_sum64(float v) {
   return __uint_as_float(r16[0]) + __uint_as_float(r16[1]);
 }
 
-// ---- residual add + LayerNorm (16-bit rows of n <= 64*8*kLnChunks elements) ------------------
-constexpr int kLnChunks = 8;  // 16-byte chunks per lane: n <= 4096
-
-template <typename T>
+// ---- residual add + LayerNorm (16-bit rows of n <= 64*8*NC elements) -------------------------
+// NC = 16-byte chunks per lane (n <= 512 * NC). The LayerNorm weight and bias are loaded with the
+// row, so the only dependent round trip is the row itself.
+template <typename T, int NC>
 __global__ __launch_bounds__(256) void add_layernorm_kernel(AddLnArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -65,24 +65,33 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(AddLnArgs a) {
   const int nc = a.n >> 3;  // 8-element chunks
   char* xrow = static_cast<char*>(a.x) + row * a.x_stride * 2;
   const char* drow = a.delta ? static_cast<const char*>(a.delta) + row * a.d_stride * 2 : nullptr;
-  float v[kLnChunks][8];
+  u32x4 xw[NC], dw[NC], ww[NC], bw[NC];
+#pragma unroll
+  for (int c = 0; c < NC; ++c) {
+    const int ci = lane + 64 * c;
+    xw[c] = dw[c] = ww[c] = bw[c] = u32x4{0, 0, 0, 0};
+    if (ci < nc) {
+      xw[c] = *reinterpret_cast<const u32x4*>(xrow + ci * 16);
+      if (drow) dw[c] = *reinterpret_cast<const u32x4*>(drow + ci * 16);
+      ww[c] = *reinterpret_cast<const u32x4*>(static_cast<const char*>(a.weight) + ci * 16);
+      bw[c] = *reinterpret_cast<const u32x4*>(static_cast<const char*>(a.bias) + ci * 16);
+    }
+  }
+  float v[NC][8];
   float sum = 0.f;
 #pragma unroll
-  for (int c = 0; c < kLnChunks; ++c) {
+  for (int c = 0; c < NC; ++c) {
     const int ci = lane + 64 * c;
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[c][i] = 0.f;
     if (ci < nc) {
-      const u32x4 xw = *reinterpret_cast<const u32x4*>(xrow + ci * 16);
-      u32x4 dw = u32x4{0, 0, 0, 0};
-      if (drow) dw = *reinterpret_cast<const u32x4*>(drow + ci * 16);
       u32x4 sw;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        float s0 = Elem<T>::lo(xw[j]), s1 = Elem<T>::hi(xw[j]);
+        float s0 = Elem<T>::lo(xw[c][j]), s1 = Elem<T>::hi(xw[c][j]);
         if (drow) {
-          s0 = Elem<T>::round(s0 + Elem<T>::lo(dw[j]));
-          s1 = Elem<T>::round(s1 + Elem<T>::hi(dw[j]));
+          s0 = Elem<T>::round(s0 + Elem<T>::lo(dw[c][j]));
+          s1 = Elem<T>::round(s1 + Elem<T>::hi(dw[c][j]));
           sw[j] = Elem<T>::pack(s0, s1);
         }
         v[c][2 * j] = s0;
@@ -96,7 +105,7 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(AddLnArgs a) {
   const float mean = wave_sum64(sum) * inv_n;
   float sq = 0.f;
 #pragma unroll
-  for (int c = 0; c < kLnChunks; ++c)
+  for (int c = 0; c < NC; ++c)
     if (lane + 64 * c < nc)
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
@@ -106,16 +115,14 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(AddLnArgs a) {
   const float rstd = 1.f / sqrtf(wave_sum64(sq) * inv_n + a.eps);
   char* yrow = static_cast<char*>(a.y) + row * a.y_stride * 2;
 #pragma unroll
-  for (int c = 0; c < kLnChunks; ++c) {
+  for (int c = 0; c < NC; ++c) {
     const int ci = lane + 64 * c;
     if (ci < nc) {
-      const u32x4 ww = *reinterpret_cast<const u32x4*>(static_cast<const char*>(a.weight) + ci * 16);
-      const u32x4 bw = *reinterpret_cast<const u32x4*>(static_cast<const char*>(a.bias) + ci * 16);
       u32x4 yw;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const float y0 = (v[c][2 * j] - mean) * rstd * Elem<T>::lo(ww[j]) + Elem<T>::lo(bw[j]);
-        const float y1 = (v[c][2 * j + 1] - mean) * rstd * Elem<T>::hi(ww[j]) + Elem<T>::hi(bw[j]);
+        const float y0 = (v[c][2 * j] - mean) * rstd * Elem<T>::lo(ww[c][j]) + Elem<T>::lo(bw[c][j]);
+        const float y1 = (v[c][2 * j + 1] - mean) * rstd * Elem<T>::hi(ww[c][j]) + Elem<T>::hi(bw[c][j]);
         yw[j] = Elem<T>::pack(y0, y1);
       }
       *reinterpret_cast<u32x4*>(yrow + ci * 16) = yw;
@@ -176,8 +183,18 @@ __global__ __launch_bounds__(256) void masked_argmax_kernel(ArgmaxArgs a) {
 hipError_t launch_add_layernorm(int dtype, const AddLnArgs& a, hipStream_t stream) {
   if (a.rows == 0) return hipSuccess;
   const dim3 grid((unsigned)((a.rows + 3) / 4));
-  if (dtype == 2) hipLaunchKernelGGL(add_layernorm_kernel<Bf16>, grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL(add_layernorm_kernel<F16>, grid, dim3(256), 0, stream, a);
+  const int nc = (a.n + 511) / 512;
+  switch (nc) {
+#define WDRZ_LN(NC)                                                                                  \
+  case NC:                                                                                           \
+    if (dtype == 2) hipLaunchKernelGGL((add_layernorm_kernel<Bf16, NC>), grid, dim3(256), 0, stream, a); \
+    else hipLaunchKernelGGL((add_layernorm_kernel<F16, NC>), grid, dim3(256), 0, stream, a);         \
+    break;
+    WDRZ_LN(1) WDRZ_LN(2) WDRZ_LN(3) WDRZ_LN(4) WDRZ_LN(5) WDRZ_LN(6) WDRZ_LN(7) WDRZ_LN(8)
+#undef WDRZ_LN
+    default:
+      return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 
