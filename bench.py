@@ -562,6 +562,68 @@ def dtw_cpu_baseline(budget_s: float = 12.0) -> dict:
     }
 
 
+def decode_cpu_baseline(budget_s: float = 15.0) -> dict:
+    """The reference's CPU path for decode configs 3, 4 and 5 (``_sdpa_attn_with_kvcache``,
+    model.py:20-76, as the oracle restates it) in torch fp32 on the host cores: one layer of
+    each config at full size (64 streams, the same seeded lengths). Reported in the GPU line's
+    unit: that config's algorithmic bytes per layer (counted in bf16, as the GPU line counts
+    them) per second of CPU time."""
+    from oracle.attention_oracle import kvcache_torch
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    Bs, Lself, Lcross = 64, 448, 1500
+    g = torch.Generator().manual_seed(2)
+    idx = torch.arange(Bs, dtype=torch.int32)
+    L3 = _lengths(3, Bs, 1, Lself)
+    L5 = _lengths(5, Bs, 5, Lself)
+    kself, vself = (torch.randn((Bs, Lself, H, D), generator=g) for _ in range(2))
+    kx, vx = (torch.randn((Bs, Lcross, H, D), generator=g) for _ in range(2))
+
+    def new(sq):
+        return tuple(torch.randn((Bs, sq, H, D), generator=g) for _ in range(3))
+
+    q1, k1, v1 = new(1)
+    q5, k5, v5 = new(5)
+    qx5 = new(5)[0]
+    cs3 = torch.from_numpy((L3 - 1).astype(np.int32))
+    cs5 = torch.from_numpy((L5 - 5).astype(np.int32))
+    cases = {
+        "config3_self_decode": (lambda: kvcache_torch(q1, kself, vself, k1, v1, cs3, idx, 0.125),
+                                2 * H * D * E * int(L3.sum()) + 4 * H * D * E * Bs + 8 * Bs),
+        "config4_cross_decode": (lambda: kvcache_torch(q1, kx, vx, None, None, None, idx, 0.125),
+                                 2 * Bs * Lcross * H * D * E + 2 * H * D * E * Bs + 4 * Bs),
+        "config5_verify_self_plus_cross": (
+            lambda: (kvcache_torch(q5, kself, vself, k5, v5, cs5, idx, 0.125),
+                     kvcache_torch(qx5, kx, vx, None, None, None, idx, 0.125)),
+            2 * H * D * E * int(L5.sum()) + 4 * H * D * E * Bs * 5 + 8 * Bs + 2 * Bs * Lcross * H * D * E
+            + 2 * H * D * E * Bs * 5 + 4 * Bs),
+    }
+    out = {}
+    per_case = budget_s / len(cases)
+    for name, (fn, nbytes) in cases.items():
+        fn()  # warm-up
+        times = []
+        t_end = time.perf_counter() + per_case
+        while len(times) < 3 or (time.perf_counter() < t_end and len(times) < 50):
+            t0 = time.perf_counter()
+            fn()
+            times.append(time.perf_counter() - t0)
+        med = float(np.median(times))
+        log(f"[bench] {name} cpu baseline: {med * 1e3:.1f} ms per layer on {cores} threads -> "
+            f"{nbytes / med / 1e9:.2f} GB/s")
+        out[name] = {
+            "value": round(nbytes / med / 1e9, 3),
+            "unit": "GB/s",
+            "cores": cores,
+            "kind": "port",
+            "sample": f"torch CPU fp32 restatement of _sdpa_attn_with_kvcache (model.py:20-76: append, gather, "
+            f"bottom-right mask, SDPA) on one full layer of the config (64 streams), median of {len(times)} runs "
+            f"({med * 1e3:.1f} ms each); bytes = the GPU line's bf16 algorithmic bytes per layer",
+        }
+    return out
+
+
 def cpu_baseline(budget_s: float = 12.0) -> dict:
     from oracle.attention_oracle import sdpa_torch
 
@@ -703,6 +765,9 @@ def main() -> int:
         dtw["cpu_baseline"] = dtw_cpu_baseline()
     if mel is not None and not args.no_cpu:
         mel["cpu_baseline"] = logmel_cpu_baseline()
+    if dec is not None and not args.no_cpu:
+        for name, base in decode_cpu_baseline().items():
+            dec[name]["cpu_baseline"] = base
 
     line = {
         "metric": METRIC,
