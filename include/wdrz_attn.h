@@ -257,6 +257,28 @@ int wdrz_dtw_attention_prep(int dtype, const void* const* q_heads, const int64_t
                             int64_t A, int64_t D, int64_t C, int medfilt_width, void* workspace,
                             size_t workspace_bytes, void* stream);
 
+/*
+ * Projected K/V rows into the slot caches:
+ *   k_cache[slot_indices[b], start_pos + t, h, :] = k_src[b, t, h, :]   (and v), t < T.
+ *
+ * Replaces: FlashKVCache.prefill(k, v, start_pos, slot_indices) and
+ *           FlashKVCache.set_cross_attention(k, v, slot_indices) (src/whisperdrz/model.py:150-183),
+ *           the cache writes of prefill_flash's cross fill (model.py:851-862); the callers keep
+ *           the seq_lens / cross_attn_len bookkeeping.
+ *
+ * k_src / v_src: [B, T, H, 64] 16-bit, element strides src_strides[3] of b, t, h (head_dim
+ *                contiguous; e.g. the key / value halves of one fused projection output).
+ * k_cache / v_cache: [n_slots, Lmax, H, 64], strides cache_strides[3] of slot, position, head
+ *                (any order: head-major storage viewed slot-major works).
+ * slot_indices:  device int64 [B], or NULL for slot b. Ids outside [0, n_slots) are skipped.
+ * Rows 16-byte aligned; start_pos + T <= Lmax. Each element is written once (duplicate slot ids
+ * race, as the reference's index_put does).
+ */
+int wdrz_kv_fill(int dtype, const void* k_src, const void* v_src, const int64_t* src_strides,
+                 void* k_cache, void* v_cache, const int64_t* cache_strides,
+                 const int64_t* slot_indices, int64_t B, int64_t T, int64_t H, int64_t D,
+                 int64_t n_slots, int64_t Lmax, int64_t start_pos, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

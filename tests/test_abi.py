@@ -243,3 +243,32 @@ def test_log_mel_rejects_bad_arguments(lib, over, code, msg):
                           args["frames"], None, 0, None)
     assert rc == code
     assert msg in lib.wdrz_last_error().decode()
+
+
+def call_fill(lib, **over):
+    args = dict(dtype=2, k=FAKE, v=FAKE, ss=(ctypes.c_int64 * 3)(1500 * 2560, 2560, 64), kc=FAKE, vc=FAKE,
+                cs=(ctypes.c_int64 * 3)(20 * 1500 * 64, 64, 1500 * 64), slots=None, B=16, T=1500, H=20, D=64,
+                n_slots=64, Lmax=1500, start=0)
+    args.update(over)
+    return lib.wdrz_kv_fill(args["dtype"], args["k"], args["v"], args["ss"], args["kc"], args["vc"], args["cs"],
+                            args["slots"], args["B"], args["T"], args["H"], args["D"], args["n_slots"],
+                            args["Lmax"], args["start"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(dtype=0), 2, "only WDRZ_BF16 / WDRZ_F16"),
+    (dict(D=128), 2, "head_dim"),
+    (dict(start=1), 1, "exceed the cache length"),
+    (dict(k=None), 1, "is NULL"),
+    (dict(kc=FAKE + 8), 1, "16-byte aligned"),
+    (dict(ss=(ctypes.c_int64 * 3)(1500 * 2560, 2561, 64)), 1, "16-byte aligned"),
+    (dict(T=-1), 1, "bad sizes"),
+])
+def test_kv_fill_rejects_bad_arguments(lib, over, code, msg):
+    assert call_fill(lib, **over) == code
+    assert msg in lib.wdrz_last_error().decode()
+
+
+def test_kv_fill_empty_is_a_no_op(lib):
+    assert call_fill(lib, B=0) == 0
+    assert call_fill(lib, T=0) == 0

@@ -29,6 +29,7 @@ EXPORTED_SYMBOLS = (
     "wdrz_dtw_prep_workspace_size",
     "wdrz_dtw_prep",
     "wdrz_dtw_attention_prep",
+    "wdrz_kv_fill",
 )
 ABI_VERSION = 1
 
@@ -104,6 +105,12 @@ def _declare(lib: ctypes.CDLL) -> None:
         _i32p, _i32p, _p, _i64p,  # lens, caps, out, out strides
         _i64, _i64, _i64, _i64, _i64, _i64, ctypes.c_int,  # B, H, T, A, D, C, medfilt_width
         _p, ctypes.c_size_t, _p,  # workspace, bytes, stream
+    ]
+
+    lib.wdrz_kv_fill.restype = ctypes.c_int
+    lib.wdrz_kv_fill.argtypes = [
+        ctypes.c_int, _p, _p, _i64p, _p, _p, _i64p, _p,  # dtype, k/v src, src strides, k/v cache, cache strides, slots
+        _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p,  # B, T, H, D, n_slots, Lmax, start_pos, stream
     ]
 
 

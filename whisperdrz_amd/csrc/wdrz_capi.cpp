@@ -383,6 +383,48 @@ int wdrz_masked_argmax(int dtype, const void* logits, int64_t logits_stride, con
   return WDRZ_OK;
 }
 
+int wdrz_kv_fill(int dtype, const void* k_src, const void* v_src, const int64_t* src_strides, void* k_cache,
+                 void* v_cache, const int64_t* cache_strides, const int64_t* slot_indices, int64_t B, int64_t T,
+                 int64_t H, int64_t D, int64_t n_slots, int64_t Lmax, int64_t start_pos, void* stream) {
+  g_last_error.clear();
+  if (dtype != WDRZ_BF16 && dtype != WDRZ_F16)
+    return fail(dtype == WDRZ_F32 ? WDRZ_EUNSUPPORTED : WDRZ_EINVAL, "dtype %d: only WDRZ_BF16 / WDRZ_F16", dtype);
+  if (D != 64) return fail(WDRZ_EUNSUPPORTED, "head_dim %lld: only 64", (long long)D);
+  if (B < 0 || T < 0 || H < 0 || n_slots < 0 || Lmax < 0 || start_pos < 0)
+    return fail(WDRZ_EINVAL, "bad sizes B=%lld T=%lld H=%lld", (long long)B, (long long)T, (long long)H);
+  if (start_pos + T > Lmax)
+    return fail(WDRZ_EINVAL, "rows [%lld, %lld) exceed the cache length %lld", (long long)start_pos,
+                (long long)(start_pos + T), (long long)Lmax);
+  if (B > 65535 || H > 65535 || T > (1 << 24) || n_slots > (1 << 30)) return fail(WDRZ_EUNSUPPORTED, "sizes too large");
+  if (B == 0 || T == 0 || H == 0) return WDRZ_OK;
+  if (!k_src || !v_src || !k_cache || !v_cache) return fail(WDRZ_EINVAL, "a K/V pointer is NULL");
+  if (!src_strides || !cache_strides) return fail(WDRZ_EINVAL, "strides pointer is NULL");
+  const void* ptrs[4] = {k_src, v_src, k_cache, v_cache};
+  for (const void* p : ptrs)
+    if (reinterpret_cast<uintptr_t>(p) & 15) return fail(WDRZ_EINVAL, "K/V rows are not 16-byte aligned");
+  for (int i = 0; i < 3; ++i)
+    if (((src_strides[i] * 2) & 15) || ((cache_strides[i] * 2) & 15))
+      return fail(WDRZ_EINVAL, "K/V rows are not 16-byte aligned (strides)");
+  wdrz::KvFillArgs a{};
+  a.k_src = k_src;
+  a.v_src = v_src;
+  a.k_cache = k_cache;
+  a.v_cache = v_cache;
+  for (int i = 0; i < 3; ++i) {
+    a.ss[i] = src_strides[i];
+    a.cs[i] = cache_strides[i];
+  }
+  a.slots = slot_indices;
+  a.B = (int)B;
+  a.T = (int)T;
+  a.H = (int)H;
+  a.n_slots = (int)n_slots;
+  a.start = (int)start_pos;
+  hipError_t err = wdrz::launch_kv_fill(a, reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(WDRZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  return WDRZ_OK;
+}
+
 size_t wdrz_log_mel_workspace_size(int64_t B, int64_t n_mels) {
   if (B <= 0 || n_mels <= 0) return 0;
   return wdrz::logmel_workspace_bytes(B, n_mels);

@@ -99,6 +99,21 @@ struct AddLnArgs {
 hipError_t launch_add_layernorm(int dtype, const AddLnArgs& a, hipStream_t stream);
 
 // Masked greedy sampling over logits rows (strides in elements / bytes for the masks).
+// Rows of projected K/V into the slot caches (kv_fill.hip): cache[slot[b], start + t, h, :] =
+// src[b, t, h, :] for K and V; 16-bit elements, head_dim 64, strides in elements.
+struct KvFillArgs {
+  const void* k_src;
+  const void* v_src;
+  int64_t ss[3];  // source strides of b, t, h (the head_dim is contiguous)
+  void* k_cache;
+  void* v_cache;
+  int64_t cs[3];  // cache strides of slot, position, head
+  const int64_t* slots;  // [B] slot of each batch row, or null for slot b
+  int B, T, H;
+  int n_slots, start;
+};
+hipError_t launch_kv_fill(const KvFillArgs& a, hipStream_t stream);
+
 struct ArgmaxArgs {
   const void* logits;
   int64_t l_stride;

@@ -98,6 +98,20 @@ class MultiHeadAttention(nn.Module):
             self._qkv_cache = cached
         return cached[1], cached[2]
 
+    def kv_weight(self) -> tuple[Tensor, Tensor]:
+        """``[key; value]`` weights ``[2*n_state, n_state]`` and bias (the key's part zero): the
+        cross-attention fill's two projections of the encoder output as one GEMM."""
+        ps = (self.key.weight, self.value.weight, self.value.bias)
+        key = tuple((p.data_ptr(), p._version, p.dtype) for p in ps)
+        cached = getattr(self, "_kv_cache", None)
+        if cached is None or cached[0] != key:
+            with torch.no_grad():
+                w = torch.cat([self.key.weight, self.value.weight])
+                b = torch.cat([torch.zeros_like(self.value.bias), self.value.bias])
+            cached = (key, w, b)
+            self._kv_cache = cached
+        return cached[1], cached[2]
+
     def forward_flash_step(self, x: Tensor, kv_cache: FlashKVCache, is_cross_attn: bool,
                            cache_seqlens: Optional[Tensor], batch_idx: Optional[Tensor]) -> Tensor:
         """``forward_flash`` with the step's metadata computed once by the caller (the gathered
@@ -238,9 +252,15 @@ class TextDecoderStack(nn.Module):
         run the prompt as one multi-token causal step (model.py:824-869)."""
         B, seq_len = tokens.shape
         d = self.n_state // self.n_head
+        fused = self.fused_small_ops and xa.is_cuda and xa.dtype in (torch.bfloat16, torch.float16)
         for block, c_kv in zip(self.blocks, cross_kv, strict=True):
-            k = block.cross_attn.key(xa).view(B, -1, self.n_head, d)
-            v = block.cross_attn.value(xa).view(B, -1, self.n_head, d)
+            if fused:  # key and value projections as one [B*T, n_state] x [n_state, 2*n_state] GEMM
+                w, b = block.cross_attn.kv_weight()
+                kv = F.linear(xa, w, b).view(B, -1, 2, self.n_head, d)
+                k, v = kv[:, :, 0], kv[:, :, 1]
+            else:
+                k = block.cross_attn.key(xa).view(B, -1, self.n_head, d)
+                v = block.cross_attn.value(xa).view(B, -1, self.n_head, d)
             c_kv.set_cross_attention(k, v, slot_indices)
         for s_kv in self_kv:
             if slot_indices is not None:

@@ -13,6 +13,10 @@ methods ``prefill``, ``set_cross_attention`` and ``reset``. What changes is the 
   allocation whose size is known up front, and ``plan_slots`` sizes the slot count for the
   HBM that is left after weights and activations.
 
+* cache writes on the GPU go through ``wdrz_kv_fill`` (one kernel for K and V, contiguous 4 KB
+  runs per (slot, head)) instead of torch's index_put over the permuted view, which is ~3x
+  slower on the cross fill.
+
 Sizes at Whisper large-v3 (32 layers, 20 heads, head_dim 64, bf16): 448-position self caches
 take 73.4 MB per slot, 1500-position cross caches 245.8 MB per slot, 319 MB per slot in all;
 about 850 slots fit in 272 GB.
@@ -25,7 +29,44 @@ from typing import Optional
 import torch
 from torch import Tensor
 
+from . import _lib
+
 _ALIGN = 2 << 20  # slice alignment inside the arena (bytes)
+_FILL_DTYPES = {torch.bfloat16: _lib.WDRZ_BF16, torch.float16: _lib.WDRZ_F16}
+
+
+def _hip_fill(k_cache: Tensor, v_cache: Tensor, k: Tensor, v: Tensor, slot_indices: Optional[Tensor],
+              start_pos: int) -> bool:
+    """``k_cache[slot_indices, start_pos:start_pos + T] = k`` (and v) with ``wdrz_kv_fill``.
+    Returns False (nothing written) for what the kernel does not take: CPU tensors, a dtype
+    other than the caches' bf16 / fp16, head_dim != 64; the caller then uses torch indexing,
+    which also casts."""
+    if not (k.is_cuda and k_cache.is_cuda and k.dtype == v.dtype == k_cache.dtype == v_cache.dtype
+            and k.dtype in _FILL_DTYPES and k.shape[-1] == 64 and k.dim() == 4):
+        return False
+    from .attention import _raise, _stream_handle
+
+    B, T, H, D = (int(x) for x in k.shape)
+    if tuple(v.shape) != (B, T, H, D) or k_cache.shape[2] != H:
+        raise ValueError(f"k/v {tuple(k.shape)} / {tuple(v.shape)} do not match the cache {tuple(k_cache.shape)}")
+    if k.stride(-1) != 1 or v.stride() != k.stride():  # one set of source strides for both
+        k, v = k.contiguous(), v.contiguous()
+    slots = None
+    if slot_indices is not None:
+        slots = slot_indices.to(device=k.device, dtype=torch.int64)
+        if slots.dim() != 1 or slots.shape[0] != B:
+            raise ValueError(f"slot_indices must be [{B}]")
+        slots = slots.contiguous()
+    n_slots, Lmax = int(k_cache.shape[0]), int(k_cache.shape[1])
+    rc = _lib.load().wdrz_kv_fill(
+        _FILL_DTYPES[k.dtype], k.data_ptr(), v.data_ptr(), (_lib.ctypes.c_int64 * 3)(*k.stride()[:3]),
+        k_cache.data_ptr(), v_cache.data_ptr(), (_lib.ctypes.c_int64 * 3)(*k_cache.stride()[:3]),
+        slots.data_ptr() if slots is not None else None, B, T, H, D, n_slots, Lmax, int(start_pos),
+        _stream_handle(),
+    )
+    if rc != _lib.WDRZ_OK:
+        _raise(rc, "kv_fill")
+    return True
 
 
 class FlashKVCache:
@@ -82,26 +123,30 @@ class FlashKVCache:
         to the end position (model.py:150-168)."""
         seq_len = k.shape[1]
         end_pos = start_pos + seq_len
+        written = _hip_fill(self.k_cache, self.v_cache, k, v, slot_indices, start_pos)
         if slot_indices is not None:
-            self.k_cache[slot_indices, start_pos:end_pos] = k
-            self.v_cache[slot_indices, start_pos:end_pos] = v
+            if not written:
+                self.k_cache[slot_indices, start_pos:end_pos] = k
+                self.v_cache[slot_indices, start_pos:end_pos] = v
             self.seq_lens[slot_indices] = end_pos
         else:
             B = k.shape[0]
-            self.k_cache[:B, start_pos:end_pos] = k
-            self.v_cache[:B, start_pos:end_pos] = v
+            if not written:
+                self.k_cache[:B, start_pos:end_pos] = k
+                self.v_cache[:B, start_pos:end_pos] = v
             self.seq_lens[:B] = end_pos
 
     def set_cross_attention(self, k: Tensor, v: Tensor, slot_indices: Optional[Tensor] = None):
         """Write the encoder-side ``k, v`` ``[B, seq, heads, head_dim]`` (model.py:170-183)."""
         seq_len = k.shape[1]
-        if slot_indices is not None:
-            self.k_cache[slot_indices, :seq_len] = k
-            self.v_cache[slot_indices, :seq_len] = v
-        else:
-            B = k.shape[0]
-            self.k_cache[:B, :seq_len] = k
-            self.v_cache[:B, :seq_len] = v
+        if not _hip_fill(self.k_cache, self.v_cache, k, v, slot_indices, 0):
+            if slot_indices is not None:
+                self.k_cache[slot_indices, :seq_len] = k
+                self.v_cache[slot_indices, :seq_len] = v
+            else:
+                B = k.shape[0]
+                self.k_cache[:B, :seq_len] = k
+                self.v_cache[:B, :seq_len] = v
         self.cross_attn_len = seq_len
         self.done = True
 
