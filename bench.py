@@ -13,10 +13,12 @@ carries the DTW alignment inputs (compute_attention and _dtw_prep_batch) in GB/s
 HBM bytes, and under ``log_mel`` the GPU log-mel front end in TFLOP/s of fp32 matrix work, each
 with its own roofline and CPU baseline.
 
+Under ``cross_fill`` it times the encoder output's projection into every layer's cross cache (the
+key/value GEMM and ``wdrz_kv_fill``, with its own HBM roofline).
 Under ``decode_step`` it times a whole captured large-v3 decode step (64 streams) with and without
 the fused add + LayerNorm.
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only enc|dec|dtw|mel|step]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--only enc|dec|dtw|mel|step|fill]
 """
 from __future__ import annotations
 
@@ -457,6 +459,80 @@ def bench_decode_step(dev, steps: int, warmup: int) -> dict:
 
 
 # --------------------------------------------------------------------------------------------
+# cross-attention fill after the encoder (prefill_flash, model.py:851-862)
+# --------------------------------------------------------------------------------------------
+
+FILL_B, FILL_L = 16, 1500
+
+
+def bench_cross_fill(dev, steps: int, warmup: int) -> dict:
+    """The encoder output of 16 windows projected into every layer's cross cache: per layer one
+    key / value GEMM ([16*1500, 1280] x [1280, 2560], hipBLASLt) and one wdrz_kv_fill into the
+    head-major slots. The fill alone is HBM-bound: it reads and writes 2 x 16 x 1500 x 1280 bf16."""
+    import torch.nn.functional as F
+
+    from whisperdrz_amd.decoder import TextDecoderStack
+    from whisperdrz_amd.kv_cache import KVSlotPool
+
+    torch.manual_seed(0)
+    with torch.device(dev):
+        dec = TextDecoderStack(51866, 448, H * D, H, N_LAYERS).to(torch.bfloat16).eval()
+    pool = KVSlotPool(N_LAYERS, FILL_B, H, D, self_len=448, cross_len=FILL_L, dtype=torch.bfloat16, device=dev)
+    g = torch.Generator(device=dev).manual_seed(9000)
+    xa = torch.randn((FILL_B, FILL_L, H * D), generator=g, device=dev).to(torch.bfloat16)
+    slots = torch.arange(FILL_B, device=dev)
+    stream = torch.cuda.current_stream()
+    kvs = [torch.randn((FILL_B, FILL_L, 2, H, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(4)]
+
+    def fill_only():
+        for i, c in enumerate(pool.cross_kv[:4]):
+            c.set_cross_attention(kvs[i][:, :, 0], kvs[i][:, :, 1], slots)
+
+    def fill_torch():  # the reference's index_put on the same views
+        for i, c in enumerate(pool.cross_kv[:4]):
+            c.k_cache[slots, :FILL_L] = kvs[i][:, :, 0]
+            c.v_cache[slots, :FILL_L] = kvs[i][:, :, 1]
+
+    def full():
+        for blk, c in zip(dec.blocks, pool.cross_kv):
+            w, b = blk.cross_attn.kv_weight()
+            kv = F.linear(xa, w, b).view(FILL_B, FILL_L, 2, H, D)
+            c.set_cross_attention(kv[:, :, 0], kv[:, :, 1], slots)
+
+    with torch.no_grad():
+        for _ in range(warmup):
+            fill_only()
+            full()
+        us = timed_events(fill_only, steps, stream) * 1e3 / 4
+        fill_torch()
+        us_torch = timed_events(fill_torch, 3, stream) * 1e3 / 4
+        ms_full = timed_events(full, max(3, steps // 4), stream)
+    nbytes = 2 * 2 * FILL_B * FILL_L * H * D * E  # K and V, read once and written once
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"[bench] cross fill: wdrz_kv_fill {us:.1f} us per layer, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}% of "
+        f"HBM); torch index_put {us_torch:.1f} us; GEMM + fill for 32 layers {ms_full:.2f} ms")
+    del dec, pool, kvs
+    torch.cuda.empty_cache()
+    return {
+        "workload": f"prefill_flash cross fill: {FILL_B} windows x {FILL_L} encoder rows, 32 layers, per layer one "
+        "[24000, 1280] x [1280, 2560] key/value GEMM (hipBLASLt) and one wdrz_kv_fill into head-major slots",
+        "fill_us_per_layer": round(us, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(gbs, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4),
+            "traffic": measured_traffic("kv_fill_kernel"),
+            "bytes_per_layer": nbytes,
+            "kernel": "kv_fill_kernel",
+        },
+        "torch_index_put_us_per_layer": round(us_torch, 1),
+        "ms_32_layers_gemm_plus_fill": round(ms_full, 3),
+    }
+
+
+# --------------------------------------------------------------------------------------------
 # log-mel front end (LogMelSpectrogram, audio.py:81-156)
 # --------------------------------------------------------------------------------------------
 
@@ -657,8 +733,8 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
 def pmc_sample(dev) -> None:
     """A short, fixed kernel sequence for hardware-counter passes (rocprofv3 --pmc):
     a calibration copy of 1 GiB (known HBM bytes), then 3 launches of the encoder kernel, of
-    each decode kernel, of the DTW prep, compute_attention, the fused attention + prep and the
-    log-mel front end at the
+    each decode kernel, of the DTW prep, compute_attention, the fused attention + prep, the
+    cross-cache fill and the log-mel front end at the
     bench shapes (eager)."""
     from whisperdrz_amd import flash_attn_with_kvcache, scaled_dot_product_attention
 
@@ -719,6 +795,14 @@ def pmc_sample(dev) -> None:
         dtw_attention_prep(q_out, k_out, mask, lens, [DTW_A] * DTW_B)
         torch.cuda.synchronize()
     del q_out, k_out
+    from whisperdrz_amd.kv_cache import FlashKVCache
+
+    fc = FlashKVCache(FILL_B, FILL_L, H, D, dtype=torch.bfloat16, device=dev)
+    kv = torch.randn((FILL_B, FILL_L, 2, H, D), generator=g, device=dev).to(torch.bfloat16)
+    for _ in range(3):
+        fc.set_cross_attention(kv[:, :, 0], kv[:, :, 1], torch.arange(FILL_B, device=dev))
+        torch.cuda.synchronize()
+    del fc, kv
     audio = 0.1 * torch.randn((MEL_B, MEL_N), generator=g, device=dev)
     for _ in range(3):
         log_mel_spectrogram(audio, MEL_MELS, 3000)
@@ -732,7 +816,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--only", choices=["enc", "dec", "dtw", "mel", "step"], default=None)
+    ap.add_argument("--only", choices=["enc", "dec", "dtw", "mel", "step", "fill"], default=None)
     ap.add_argument("--pmc-sample", action="store_true",
                     help="run the short fixed kernel sequence used for rocprofv3 --pmc passes and exit")
     args = ap.parse_args()
@@ -760,6 +844,7 @@ def main() -> int:
     dtw = bench_dtw(dev, args.steps, args.warmup) if args.only in (None, "dtw") else None
     mel = bench_logmel(dev, args.steps, args.warmup) if args.only in (None, "mel") else None
     step = bench_decode_step(dev, args.steps, args.warmup) if args.only in (None, "step") else None
+    fill = bench_cross_fill(dev, args.steps, args.warmup) if args.only in (None, "fill") else None
     cpu = None if args.no_cpu else cpu_baseline()
     if dtw is not None and not args.no_cpu:
         dtw["cpu_baseline"] = dtw_cpu_baseline()
@@ -798,6 +883,7 @@ def main() -> int:
         "dtw_prep": dtw,
         "log_mel": mel,
         "decode_step": step,
+        "cross_fill": fill,
     }
     print(json.dumps(line), flush=True)
     return 0
