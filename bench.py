@@ -319,6 +319,7 @@ def bench_dtw(dev, steps: int, warmup: int) -> dict:
     del inputs, outs
     torch.cuda.empty_cache()
     qk = bench_dtw_qk(dev, steps, warmup)
+    dec_attn = bench_dtw_decoder_attention(dev, steps, warmup)
     return {
         "workload": f"_dtw_prep_batch: B={DTW_B} chunks x H={DTW_H} alignment heads x T_text={DTW_T} x "
         f"T_audio={DTW_A} fp32 scores, caps={DTW_A}, lens ~ U[{DTW_T // 2},{DTW_T}], median width 7; "
@@ -338,6 +339,58 @@ def bench_dtw(dev, steps: int, warmup: int) -> dict:
         },
         "torch_ops_gpu_us": round(ms_torch * 1e3, 1),
         "compute_attention": qk,
+        "decoder_attention": dec_attn,
+    }
+
+
+def bench_dtw_decoder_attention(dev, steps: int, warmup: int) -> dict:
+    """The uncached decoder forward that feeds the alignment (dtw_align.py:1183, model.py:288):
+    per layer a causal self-attention over the padded text [16, 20, 448, 64] and a cross-attention
+    of those 448 rows over the 1500 encoder rows, bf16, 8 distinct layers in rotation. Algorithmic
+    FLOP: 4*B*H*T*T*D/2 for the causal half (keys at or before each query) + 4*B*H*T*A*D."""
+    from whisperdrz_amd import scaled_dot_product_attention
+
+    B, T, A, n_l = DTW_B, DTW_T, DTW_A, 8
+    g = torch.Generator(device=dev).manual_seed(6500)
+    layers = []
+    for _ in range(n_l):
+        q, k, v = (torch.randn((B, H, T, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+        kx, vx = (torch.randn((B, H, A, D), generator=g, device=dev).to(torch.bfloat16) for _ in range(2))
+        layers.append((q, k, v, kx, vx))
+    stream = torch.cuda.current_stream()
+
+    def self_attn():
+        for q, k, v, _, _ in layers:
+            scaled_dot_product_attention(q, k, v, is_causal=True, scale=0.125)
+
+    def cross_attn():
+        for q, _, _, kx, vx in layers:
+            scaled_dot_product_attention(q, kx, vx, is_causal=False, scale=0.125)
+
+    for _ in range(warmup):
+        self_attn()
+        cross_attn()
+    us_self = timed_events(self_attn, steps, stream) * 1e3 / n_l
+    us_cross = timed_events(cross_attn, steps, stream) * 1e3 / n_l
+    f_self = 4.0 * B * H * T * T * D / 2
+    f_cross = 4.0 * B * H * T * A * D
+    t_self = f_self / (us_self * 1e-6) / 1e12
+    t_cross = f_cross / (us_cross * 1e-6) / 1e12
+    log(f"[bench] dtw decoder attention: causal self {us_self:.1f} us/layer ({t_self:.0f} TFLOP/s), "
+        f"cross {us_cross:.1f} us/layer ({t_cross:.0f} TFLOP/s)")
+    del layers
+    torch.cuda.empty_cache()
+
+    def roof(t, kernel):
+        return {"bound": "mfma", "achieved": round(t, 1), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                "frac": round(t / PEAK_BF16_TFLOPS, 4), "traffic": None, "kernel": kernel}
+
+    return {
+        "workload": f"uncached decoder attention for DTW: B={B} chunks, H={H}, T_text={T}, T_audio={A}, bf16",
+        "causal_self_us_per_layer": round(us_self, 2),
+        "causal_self_roofline": roof(t_self, "dense_mfma_kernel<Bf16, true>"),
+        "cross_us_per_layer": round(us_cross, 2),
+        "cross_roofline": roof(t_cross, "dense_fwd_kernel<Bf16>"),
     }
 
 
