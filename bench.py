@@ -320,6 +320,7 @@ def bench_dtw(dev, steps: int, warmup: int) -> dict:
     torch.cuda.empty_cache()
     qk = bench_dtw_qk(dev, steps, warmup)
     dec_attn = bench_dtw_decoder_attention(dev, steps, warmup)
+    mf = bench_median_filter(dev, steps, warmup)
     return {
         "workload": f"_dtw_prep_batch: B={DTW_B} chunks x H={DTW_H} alignment heads x T_text={DTW_T} x "
         f"T_audio={DTW_A} fp32 scores, caps={DTW_A}, lens ~ U[{DTW_T // 2},{DTW_T}], median width 7; "
@@ -340,6 +341,36 @@ def bench_dtw(dev, steps: int, warmup: int) -> dict:
         "torch_ops_gpu_us": round(ms_torch * 1e3, 1),
         "compute_attention": qk,
         "decoder_attention": dec_attn,
+        "median_filter": mf,
+    }
+
+
+def bench_median_filter(dev, steps: int, warmup: int) -> dict:
+    """median_filter (dtw_align.py:156-167), width 7, on the prep's [16, 10, 448, 1500] fp32 scores:
+    HBM-bound, the scores read once and the result written once."""
+    from oracle.dtw_oracle import median_filter_torch
+    from whisperdrz_amd import median_filter
+
+    g = torch.Generator(device=dev).manual_seed(6600)
+    x = torch.randn((DTW_B, DTW_H, DTW_T, DTW_A), generator=g, device=dev)
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        median_filter(x, 7)
+    us = timed_events(lambda: median_filter(x, 7), steps, stream) * 1e3
+    median_filter_torch(x, 7)
+    us_torch = timed_events(lambda: median_filter_torch(x, 7), 3, stream) * 1e3
+    nbytes = 2 * x.numel() * 4
+    gbs = nbytes / (us * 1e-6) / 1e9
+    log(f"[bench] median_filter width 7: {us:.1f} us, {gbs:.0f} GB/s ({100 * gbs / PEAK_HBM_GBS:.1f}% of HBM); "
+        f"torch sort-based form {us_torch:.0f} us")
+    del x
+    torch.cuda.empty_cache()
+    return {
+        "us": round(us, 2),
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                     "frac": round(gbs / PEAK_HBM_GBS, 4), "traffic": measured_traffic("median_filter_kernel<3>"),
+                     "bytes_per_call": nbytes, "kernel": "median_filter_kernel<3>"},
+        "torch_sort_gpu_us": round(us_torch, 1),
     }
 
 
@@ -847,6 +878,13 @@ def pmc_sample(dev) -> None:
     for _ in range(3):
         dtw_attention_prep(q_out, k_out, mask, lens, [DTW_A] * DTW_B)
         torch.cuda.synchronize()
+    from whisperdrz_amd import median_filter
+
+    xm = torch.randn((DTW_B, DTW_H, DTW_T, DTW_A), generator=g, device=dev)
+    for _ in range(3):
+        median_filter(xm, 7)
+        torch.cuda.synchronize()
+    del xm
     del q_out, k_out
     from whisperdrz_amd.kv_cache import FlashKVCache
 

@@ -279,6 +279,19 @@ int wdrz_kv_fill(int dtype, const void* k_src, const void* v_src, const int64_t*
                  const int64_t* slot_indices, int64_t B, int64_t T, int64_t H, int64_t D,
                  int64_t n_slots, int64_t Lmax, int64_t start_pos, void* stream);
 
+/*
+ * Median filter along the last axis, reflect padding.
+ *
+ * Replaces: median_filter(x, width) (src/whisperdrz/dtw_align.py:156-167: the Triton kernel of
+ *           dtw_align.py:87-155 on GPU, the sort-based _median_filter_sort of dtw_align.py:65-78
+ *           elsewhere), for fp32 rows: y[r, c] = median(x[r, c - width/2 .. c + width/2]).
+ * x, y:   fp32 [rows, N], row strides in elements (last stride 1); y may not alias x.
+ * width:  1 or odd <= 15. A row with N <= width/2 is copied unchanged (dtw_align.py:66-67).
+ * Inputs must be finite (NaN ordering is not torch.sort's).
+ */
+int wdrz_median_filter(const float* x, int64_t x_stride, float* y, int64_t y_stride, int64_t rows,
+                       int64_t N, int width, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -113,8 +113,17 @@ def dtw_prep_torch(full_weights, actual_lens, audio_caps, medfilt_width: int = 7
     var = (((w - mean) ** 2) * text_mask).sum(dim=-2, keepdim=True) / n
     w = (w - mean) / var.clamp_min(1e-12).sqrt()
     if medfilt_width > 1:
-        pad = medfilt_width // 2
-        if w.shape[-1] > pad:
-            flat = torch.nn.functional.pad(w.reshape(-1, 1, A), (pad, pad), mode="reflect")
-            w = flat.unfold(-1, medfilt_width, 1).sort(dim=-1).values[..., pad].reshape(w.shape)
+        w = median_filter_torch(w, medfilt_width)
     return w.mean(dim=1)[:, :, :max_cap].contiguous()
+
+
+def median_filter_torch(x, width: int):
+    """The reference's sort-based median filter (_median_filter_sort, dtw_align.py:63-78) in
+    torch ops on whatever device ``x`` is on: reflect pad, unfold, sort, middle element."""
+    import torch
+
+    pad = width // 2
+    if x.shape[-1] <= pad:
+        return x
+    flat = torch.nn.functional.pad(x.reshape(-1, 1, x.shape[-1]), (pad, pad), mode="reflect")
+    return flat.unfold(-1, width, 1).sort(dim=-1).values[..., pad].reshape(x.shape)

@@ -272,3 +272,16 @@ def test_kv_fill_rejects_bad_arguments(lib, over, code, msg):
 def test_kv_fill_empty_is_a_no_op(lib):
     assert call_fill(lib, B=0) == 0
     assert call_fill(lib, T=0) == 0
+
+
+@pytest.mark.parametrize("width,code,msg", [(4, 1, "must be 1 or odd"), (0, 1, "must be 1 or odd"),
+                                            (17, 2, "exceeds the supported 15")])
+def test_median_filter_rejects_bad_widths(lib, width, code, msg):
+    assert lib.wdrz_median_filter(FAKE, 100, FAKE, 100, 4, 100, width, None) == code
+    assert msg in lib.wdrz_last_error().decode()
+
+
+def test_median_filter_rejects_short_strides_and_empty_is_a_no_op(lib):
+    assert lib.wdrz_median_filter(FAKE, 50, FAKE, 100, 4, 100, 7, None) == 1
+    assert "row strides" in lib.wdrz_last_error().decode()
+    assert lib.wdrz_median_filter(FAKE, 100, FAKE, 100, 0, 100, 7, None) == 0

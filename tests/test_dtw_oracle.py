@@ -126,3 +126,17 @@ def test_compute_attention_matches_per_head_loop():
         for b in range(B):
             want = (q[i, b] @ k[i, b].T) / np.sqrt(D)  # (D^-0.25)^2 = D^-0.5
             np.testing.assert_allclose(got[b, i], want, rtol=1e-12)
+
+
+@pytest.mark.parametrize("width", [1, 3, 7, 15])
+def test_median_filter_torch_equals_numpy_restatement(width):
+    # the timed torch form and the numpy restatement agree exactly (both select the middle element)
+    import torch
+
+    from oracle.dtw_oracle import median_filter_ref, median_filter_torch
+
+    x = np.random.default_rng(width).standard_normal((3, 2, 40)).astype(np.float32)
+    got = median_filter_torch(torch.from_numpy(x), width).numpy()
+    np.testing.assert_array_equal(got, median_filter_ref(x, width))
+    short = x[..., : width // 2]  # no longer than the half width: returned unchanged
+    np.testing.assert_array_equal(median_filter_torch(torch.from_numpy(short), width).numpy(), short)

@@ -332,3 +332,38 @@ def test_attention_prep_fused_rejects(cuda):
         dtw_attention_prep([q_out[0].to(cuda)], [k_out[0].to(cuda)], mask, [4], [1600])
     with pytest.raises(ValueError):
         dtw_attention_prep([q_out[0].to(cuda)], [k_out[0].to(cuda)], mask, [4, 4], [8, 8])  # B mismatch
+
+
+# ---- median_filter (dtw_align.py:156-167), standalone ----------------------------------------
+
+
+@pytest.mark.parametrize("width", [1, 3, 5, 7, 9, 11, 13, 15])
+@pytest.mark.parametrize("shape", [(3, 4, 1500), (2, 2049), (7, 8), (1, 5)])
+def test_median_filter_matches_oracle(cuda, width, shape):
+    from oracle.dtw_oracle import median_filter_ref
+    from whisperdrz_amd import median_filter
+
+    x = _scores(shape, seed=width * 100 + shape[-1])
+    print(f"median_filter width={width} shape={shape}", flush=True)
+    got = median_filter(x.to(cuda), width)
+    torch.cuda.synchronize()
+    assert got.shape == x.shape and got.dtype == x.dtype
+    np.testing.assert_array_equal(got.cpu().numpy(), median_filter_ref(x.numpy(), width))  # a selection: exact
+
+
+def test_median_filter_strided_bf16_and_rejects(cuda):
+    from oracle.dtw_oracle import median_filter_ref
+    from whisperdrz_amd import median_filter
+
+    wide = _scores((6, 2 * 300), seed=5).to(cuda)
+    x = wide[:, ::2]  # last stride 2
+    print("median_filter strided / bf16 / rejects", flush=True)
+    np.testing.assert_array_equal(median_filter(x, 7).cpu().numpy(), median_filter_ref(x.cpu().numpy(), 7))
+    xb = _scores((4, 100), seed=6).to(torch.bfloat16)
+    got = median_filter(xb.to(cuda), 5)
+    assert got.dtype == torch.bfloat16
+    np.testing.assert_array_equal(got.float().cpu().numpy(), median_filter_ref(xb.float().numpy(), 5))
+    with pytest.raises(ValueError):
+        median_filter(x, 4)  # even width: the reference's own reshape fails
+    with pytest.raises(NotImplementedError):
+        median_filter(x, 17)

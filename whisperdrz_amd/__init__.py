@@ -15,7 +15,8 @@ from .attention import (
 )
 from .audio import LogMelSpectrogram, log_mel_spectrogram
 from .decode_ops import add_layernorm_, layer_norm, masked_argmax
-from .dtw import compute_attention, dtw_attention_prep, dtw_prep, dtw_prep_batch, dtw_prep_workspace_size
+from .dtw import (compute_attention, dtw_attention_prep, dtw_prep, dtw_prep_batch, dtw_prep_workspace_size,
+                  median_filter)
 
 HAS_WDRZ = _lib.available()
 
@@ -28,6 +29,7 @@ __all__ = [
     "log_mel_spectrogram",
     "compute_attention",
     "dtw_attention_prep",
+    "median_filter",
     "dtw_prep",
     "dtw_prep_batch",
     "dtw_prep_workspace_size",

@@ -30,6 +30,7 @@ EXPORTED_SYMBOLS = (
     "wdrz_dtw_prep",
     "wdrz_dtw_attention_prep",
     "wdrz_kv_fill",
+    "wdrz_median_filter",
 )
 ABI_VERSION = 1
 
@@ -112,6 +113,9 @@ def _declare(lib: ctypes.CDLL) -> None:
         ctypes.c_int, _p, _p, _i64p, _p, _p, _i64p, _p,  # dtype, k/v src, src strides, k/v cache, cache strides, slots
         _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p,  # B, T, H, D, n_slots, Lmax, start_pos, stream
     ]
+
+    lib.wdrz_median_filter.restype = ctypes.c_int
+    lib.wdrz_median_filter.argtypes = [_p, _i64, _p, _i64, _i64, _i64, ctypes.c_int, _p]
 
 
 def load() -> ctypes.CDLL:

@@ -1230,6 +1230,72 @@ __global__ __launch_bounds__(256, 2) void dtw_qk_band_kernel(DtwArgs a, DtwQkArg
   }
 }
 
+// ---------------------------------------------------------------------------------------------
+// Standalone median filter along the last axis (median_filter, dtw_align.py:156-167, and its
+// sort-based form at dtw_align.py:65-78): width 2*PAD+1, reflect padding. One workgroup per
+// row (per 2048-column piece of longer rows), 4 columns per lane: the columns and an 8-wide
+// reflected halo go to LDS (16-byte loads when rows are 16-byte aligned), each lane takes the
+// medians of 4 adjacent windows with the networks the prep's filter pass uses.
+// ---------------------------------------------------------------------------------------------
+constexpr int kMfMaxThreads = 512;  // 4 columns per lane: up to 2048 columns per workgroup
+
+template <int PAD>
+__global__ __launch_bounds__(kMfMaxThreads) void median_filter_kernel(MedianArgs a) {
+  __shared__ __align__(16) float row[4 * kMfMaxThreads + 2 * kHalo];
+  const int cols = 4 * blockDim.x;
+  const int c0 = blockIdx.x * cols;
+  const int64_t r = blockIdx.y;
+  const float* src = a.x + r * a.xs;
+  if (a.vec) {
+    // interior as 16-byte loads (c0 and the row start are multiples of 4 floats), halo scalar
+    for (int i = threadIdx.x; i < cols / 4; i += blockDim.x) {
+      const int c = c0 + 4 * i;
+      f32x4 v;
+      if (c + 4 <= a.N) {
+        v = *reinterpret_cast<const f32x4*>(src + c);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          int cc = c + j;
+          cc = cc >= a.N ? 2 * (a.N - 1) - cc : cc;
+          v[j] = src[cc < 0 ? 0 : cc];
+        }
+      }
+      *reinterpret_cast<f32x4*>(&row[kHalo + 4 * i]) = v;
+    }
+    for (int i = threadIdx.x; i < 2 * kHalo; i += blockDim.x) {
+      const int li = i < kHalo ? i : cols + i;  // left halo, then right halo
+      int c = c0 - kHalo + li;
+      c = c < 0 ? -c : (c >= a.N ? 2 * (a.N - 1) - c : c);
+      c = c < 0 ? 0 : (c >= a.N ? a.N - 1 : c);
+      row[li] = src[c];
+    }
+  } else {
+    for (int i = threadIdx.x; i < cols + 2 * kHalo; i += blockDim.x) {
+      int c = c0 - kHalo + i;
+      c = c < 0 ? -c : (c >= a.N ? 2 * (a.N - 1) - c : c);  // reflect (N > PAD: in range for the halo used)
+      c = c < 0 ? 0 : (c >= a.N ? a.N - 1 : c);               // columns no output reads: any valid address
+      row[i] = src[c];
+    }
+  }
+  __syncthreads();
+  const int col = c0 + 4 * threadIdx.x;
+  if (col >= a.N) return;
+  float win[4 + 2 * PAD];
+#pragma unroll
+  for (int i = 0; i < 4 + 2 * PAD; ++i) win[i] = row[kHalo + 4 * threadIdx.x - PAD + i];
+  float med[4];
+  window_medians<PAD>(win, med);
+  float* dst = a.y + r * a.ys;
+  if (a.vec && col + 4 <= a.N) {
+    __builtin_nontemporal_store(f32x4{med[0], med[1], med[2], med[3]}, reinterpret_cast<f32x4*>(dst + col));
+  } else {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (col + i < a.N) dst[col + i] = med[i];
+  }
+}
+
 }  // namespace
 
 // Workspace: row statistics [B*H*T], column statistics [B*H, cpitch], chunk partials
@@ -1354,6 +1420,35 @@ hipError_t launch_dtw_qk_prep(int dtype, DtwArgs a, const DtwQkArgs& q, hipStrea
       return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+hipError_t launch_median_filter(const MedianArgs& a, hipStream_t stream) {
+  if (a.pad < 0 || a.pad > kDtwMaxPad) return hipErrorInvalidValue;
+  MedianArgs v = a;
+  v.vec = (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 &&
+          a.xs % 4 == 0 && a.ys % 4 == 0;
+  for (int64_t r0 = 0; r0 < a.rows; r0 += 65535) {  // grid.y holds at most 65535 rows per launch
+    MedianArgs c = v;
+    c.x = a.x + r0 * a.xs;
+    c.y = a.y + r0 * a.ys;
+    c.rows = a.rows - r0 < 65535 ? a.rows - r0 : 65535;
+    // one workgroup per row when it fits 2048 columns (64-lane steps), else 2048-column pieces
+    int threads = (int)(((a.N + 3) / 4 + 63) / 64 * 64);
+    threads = threads > kMfMaxThreads ? kMfMaxThreads : threads;
+    const int cols = 4 * threads;
+    const dim3 grid((unsigned)((a.N + cols - 1) / cols), (unsigned)c.rows);
+    switch (a.pad) {
+#define WDRZ_MF(P) \
+  case P:          \
+    hipLaunchKernelGGL(median_filter_kernel<P>, grid, dim3(threads), 0, stream, c); \
+    break;
+      WDRZ_MF(0) WDRZ_MF(1) WDRZ_MF(2) WDRZ_MF(3) WDRZ_MF(4) WDRZ_MF(5) WDRZ_MF(6) WDRZ_MF(7)
+#undef WDRZ_MF
+    }
+    const hipError_t err = hipGetLastError();
+    if (err != hipSuccess) return err;
+  }
+  return hipSuccess;
 }
 
 }  // namespace wdrz

@@ -425,6 +425,31 @@ int wdrz_kv_fill(int dtype, const void* k_src, const void* v_src, const int64_t*
   return WDRZ_OK;
 }
 
+int wdrz_median_filter(const float* x, int64_t x_stride, float* y, int64_t y_stride, int64_t rows, int64_t N,
+                       int width, void* stream) {
+  g_last_error.clear();
+  if (width < 1 || (width > 1 && width % 2 == 0))
+    return fail(WDRZ_EINVAL, "width %d must be 1 or odd (an even width makes the reference's reshape fail)", width);
+  if (width / 2 > wdrz::kDtwMaxPad) return fail(WDRZ_EUNSUPPORTED, "width %d exceeds the supported 15", width);
+  if (rows < 0 || N < 0) return fail(WDRZ_EINVAL, "bad sizes rows=%lld N=%lld", (long long)rows, (long long)N);
+  if (N > (1 << 30)) return fail(WDRZ_EUNSUPPORTED, "sizes too large");
+  if (rows == 0 || N == 0) return WDRZ_OK;
+  if (!x || !y) return fail(WDRZ_EINVAL, "x / y is NULL");
+  if (x_stride < N || y_stride < N) return fail(WDRZ_EINVAL, "row strides shorter than the rows");
+  wdrz::MedianArgs a{};
+  a.x = x;
+  a.xs = x_stride;
+  a.y = y;
+  a.ys = y_stride;
+  a.rows = rows;
+  a.N = (int)N;
+  // a row no longer than the half width is returned as it is (dtw_align.py:66-67)
+  a.pad = N <= width / 2 ? 0 : width / 2;
+  hipError_t err = wdrz::launch_median_filter(a, reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(WDRZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  return WDRZ_OK;
+}
+
 size_t wdrz_log_mel_workspace_size(int64_t B, int64_t n_mels) {
   if (B <= 0 || n_mels <= 0) return 0;
   return wdrz::logmel_workspace_bytes(B, n_mels);

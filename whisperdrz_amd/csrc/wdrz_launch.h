@@ -114,6 +114,18 @@ struct KvFillArgs {
 };
 hipError_t launch_kv_fill(const KvFillArgs& a, hipStream_t stream);
 
+// Median filter along rows (dtw_prep.hip): y[r, c] = median of x[r, c-pad .. c+pad], reflected.
+struct MedianArgs {
+  const float* x;
+  int64_t xs;
+  float* y;
+  int64_t ys;
+  int64_t rows;
+  int N, pad;
+  int vec;  // rows 16-byte aligned: vector loads / stores
+};
+hipError_t launch_median_filter(const MedianArgs& a, hipStream_t stream);
+
 struct ArgmaxArgs {
   const void* logits;
   int64_t l_stride;

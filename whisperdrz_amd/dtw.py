@@ -22,7 +22,7 @@ import torch
 from . import _lib
 from .attention import WorkspaceCache, _check_cuda, _raise, _stream_handle
 
-__all__ = ["compute_attention", "dtw_attention_prep", "dtw_prep", "dtw_prep_batch", "dtw_prep_workspace_size"]
+__all__ = ["compute_attention", "dtw_attention_prep", "dtw_prep", "median_filter", "dtw_prep_batch", "dtw_prep_workspace_size"]
 
 _QK_DTYPES = {torch.bfloat16: _lib.WDRZ_BF16, torch.float16: _lib.WDRZ_F16}
 
@@ -123,6 +123,33 @@ def dtw_attention_prep(q_out, k_out, head_mask, actual_lens: Sequence[int], audi
     if rc != _lib.WDRZ_OK:
         _raise(rc, "dtw_attention_prep")
     return out
+
+
+def median_filter(x: torch.Tensor, width: int) -> torch.Tensor:
+    """Drop-in for ``median_filter(x, width)`` (dtw_align.py:156-167): the median of each
+    ``width``-wide window along the last axis, reflect padding, same shape and dtype as ``x``.
+    ``width`` is 1 or odd <= 15; a last axis no longer than ``width // 2`` is returned as it is.
+    Other float dtypes are filtered in fp32 (a median selects one input, so the conversion back
+    is exact)."""
+    if not isinstance(x, torch.Tensor):
+        raise TypeError("x must be a torch.Tensor")
+    _check_cuda("x", x, x.device)
+    if not x.is_floating_point():
+        raise TypeError(f"x: dtype {x.dtype} is not a floating-point type")
+    if x.dim() == 0:
+        raise ValueError("x must have at least one axis")
+    N = int(x.shape[-1])
+    rows = x.numel() // N if N else 0
+    src = x.reshape(rows, N) if N else x.reshape(0, 0)
+    src = src.to(torch.float32)
+    if src.stride(-1) != 1:
+        src = src.contiguous()
+    out = torch.empty((rows, N), dtype=torch.float32, device=x.device)
+    rc = _lib.load().wdrz_median_filter(src.data_ptr(), src.stride(0) if rows else N, out.data_ptr(), N, rows, N,
+                                        int(width), _stream_handle())
+    if rc != _lib.WDRZ_OK:
+        _raise(rc, "median_filter")
+    return out.view(x.shape).to(x.dtype)
 
 
 def dtw_prep_workspace_size(B: int, H: int, T: int, A: int) -> int:
