@@ -1243,8 +1243,9 @@ template <int PAD>
 __global__ __launch_bounds__(kMfMaxThreads) void median_filter_kernel(MedianArgs a) {
   __shared__ __align__(16) float row[4 * kMfMaxThreads + 2 * kHalo];
   const int cols = 4 * blockDim.x;
-  const int c0 = blockIdx.x * cols;
-  const int64_t r = blockIdx.y;
+  const int n_pieces = (a.N + cols - 1) / cols;
+  const int c0 = (int)(blockIdx.x % n_pieces) * cols;
+  const int64_t r = blockIdx.x / n_pieces;
   const float* src = a.x + r * a.xs;
   if (a.vec) {
     // interior as 16-byte loads (c0 and the row start are multiples of 4 floats), halo scalar
@@ -1423,32 +1424,26 @@ hipError_t launch_dtw_qk_prep(int dtype, DtwArgs a, const DtwQkArgs& q, hipStrea
 }
 
 hipError_t launch_median_filter(const MedianArgs& a, hipStream_t stream) {
+  if (a.rows == 0 || a.N == 0) return hipSuccess;
   if (a.pad < 0 || a.pad > kDtwMaxPad) return hipErrorInvalidValue;
   MedianArgs v = a;
   v.vec = (reinterpret_cast<uintptr_t>(a.x) & 15) == 0 && (reinterpret_cast<uintptr_t>(a.y) & 15) == 0 &&
           a.xs % 4 == 0 && a.ys % 4 == 0;
-  for (int64_t r0 = 0; r0 < a.rows; r0 += 65535) {  // grid.y holds at most 65535 rows per launch
-    MedianArgs c = v;
-    c.x = a.x + r0 * a.xs;
-    c.y = a.y + r0 * a.ys;
-    c.rows = a.rows - r0 < 65535 ? a.rows - r0 : 65535;
-    // one workgroup per row when it fits 2048 columns (64-lane steps), else 2048-column pieces
-    int threads = (int)(((a.N + 3) / 4 + 63) / 64 * 64);
-    threads = threads > kMfMaxThreads ? kMfMaxThreads : threads;
-    const int cols = 4 * threads;
-    const dim3 grid((unsigned)((a.N + cols - 1) / cols), (unsigned)c.rows);
-    switch (a.pad) {
+  // one workgroup per row when it fits 2048 columns (64-lane steps), else 2048-column pieces
+  int threads = (int)(((a.N + 3) / 4 + 63) / 64 * 64);
+  threads = threads > kMfMaxThreads ? kMfMaxThreads : threads;
+  const int64_t cols = 4 * threads;
+  const int64_t n = (a.N + cols - 1) / cols * a.rows;
+  if (n > 0x7fffffff) return hipErrorInvalidValue;
+  switch (a.pad) {
 #define WDRZ_MF(P) \
   case P:          \
-    hipLaunchKernelGGL(median_filter_kernel<P>, grid, dim3(threads), 0, stream, c); \
+    hipLaunchKernelGGL(median_filter_kernel<P>, dim3((unsigned)n), dim3(threads), 0, stream, v); \
     break;
-      WDRZ_MF(0) WDRZ_MF(1) WDRZ_MF(2) WDRZ_MF(3) WDRZ_MF(4) WDRZ_MF(5) WDRZ_MF(6) WDRZ_MF(7)
+    WDRZ_MF(0) WDRZ_MF(1) WDRZ_MF(2) WDRZ_MF(3) WDRZ_MF(4) WDRZ_MF(5) WDRZ_MF(6) WDRZ_MF(7)
 #undef WDRZ_MF
-    }
-    const hipError_t err = hipGetLastError();
-    if (err != hipSuccess) return err;
   }
-  return hipSuccess;
+  return hipGetLastError();
 }
 
 }  // namespace wdrz

@@ -432,7 +432,7 @@ int wdrz_median_filter(const float* x, int64_t x_stride, float* y, int64_t y_str
     return fail(WDRZ_EINVAL, "width %d must be 1 or odd (an even width makes the reference's reshape fail)", width);
   if (width / 2 > wdrz::kDtwMaxPad) return fail(WDRZ_EUNSUPPORTED, "width %d exceeds the supported 15", width);
   if (rows < 0 || N < 0) return fail(WDRZ_EINVAL, "bad sizes rows=%lld N=%lld", (long long)rows, (long long)N);
-  if (N > (1 << 30)) return fail(WDRZ_EUNSUPPORTED, "sizes too large");
+  if (N > (1 << 30) || rows * ((N + 2047) / 2048) > 0x7fffffff) return fail(WDRZ_EUNSUPPORTED, "sizes too large");
   if (rows == 0 || N == 0) return WDRZ_OK;
   if (!x || !y) return fail(WDRZ_EINVAL, "x / y is NULL");
   if (x_stride < N || y_stride < N) return fail(WDRZ_EINVAL, "row strides shorter than the rows");
