@@ -4,7 +4,7 @@ same decoder run with the reference's torch arithmetic (the oracle's restatement
 _sdpa_attn_with_kvcache and SDPA), through prefill, eager decode steps and hipGraph replay.
 
 Tolerance: fp32 logits within 1e-4 * max|ref| (two layers of LayerNorm/MLP amplify the
-attention's ~1e-6 relative differences); bf16 logits within 2e-2 max-abs relative scale.
+attention's ~1e-6 relative differences); bf16 and fp16 logits within 2e-2 max-abs relative scale.
 """
 import copy
 
@@ -60,7 +60,7 @@ def _close(a, b, dtype, what):
     assert err <= tol, f"{what}: max|diff|={err:.3e} > {tol:.3e}"
 
 
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16, torch.float16])
 def test_prefill_and_decode_match_reference(cuda, dtype):
     hip, ref = _make(cuda, dtype)
     B, n_slots = 3, 5
