@@ -108,3 +108,53 @@ def test_graph_bucket_choice():
     from whisperdrz_amd.decoder import GRAPH_BUCKETS, bucket_for
 
     assert [bucket_for(b, GRAPH_BUCKETS) for b in (1, 3, 9, 33, 53, 54, 60)] == [1, 4, 16, 42, 54, 54, 60]
+
+
+def test_lengths_matrix_detects_the_pool_layout():
+    from whisperdrz_amd.decoder import lengths_matrix
+    from whisperdrz_amd.kv_cache import FlashKVCache, KVSlotPool
+
+    pool = KVSlotPool(3, 4, 2, 64, self_len=16, cross_len=8, dtype=torch.float32)
+    m = lengths_matrix(pool.self_kv)
+    assert m is pool.self_seq_lens and m.shape == (3, 4)
+    pool.self_kv[1].seq_lens[2] = 7  # each layer's lengths are its own row
+    assert int(m[1, 2]) == 7 and int(m[0, 2]) == 0
+    pool.self_kv[0].reset()
+    assert int(m[1, 2]) == 7
+    separate = [FlashKVCache(4, 16, 2, 64, dtype=torch.float32) for _ in range(3)]
+    assert lengths_matrix(separate) is None
+    assert lengths_matrix([pool.self_kv[0], pool.self_kv[2]]) is None  # not the rows in order
+
+
+def test_fused_projection_weights_track_the_parameters():
+    from whisperdrz_amd.decoder import MultiHeadAttention
+
+    torch.manual_seed(0)
+    m = MultiHeadAttention(64, 2)
+    w, b = m.qkv_weight()
+    assert torch.equal(w, torch.cat([m.query.weight, m.key.weight, m.value.weight]))
+    assert torch.equal(b[64:128], torch.zeros(64)) and torch.equal(b[128:], m.value.bias)
+    assert m.qkv_weight()[0] is w  # cached
+    with torch.no_grad():
+        m.value.weight.mul_(2)  # an in-place change rebuilds it
+    w2, _ = m.qkv_weight()
+    assert w2 is not w and torch.equal(w2[128:], m.value.weight)
+    kw, kb = m.kv_weight()
+    assert torch.equal(kw, torch.cat([m.key.weight, m.value.weight])) and torch.equal(kb[:64], torch.zeros(64))
+    x = torch.randn(3, 5, 64)
+    qkv = torch.nn.functional.linear(x, *m.qkv_weight())
+    torch.testing.assert_close(qkv[..., 64:128], m.key(x))
+    torch.testing.assert_close(qkv[..., 128:], m.value(x))
+
+
+def test_cpu_cache_writes_keep_torch_indexing():
+    # the HIP fill takes GPU tensors only; CPU caches are written by torch indexing as before
+    from whisperdrz_amd.kv_cache import FlashKVCache
+
+    c = FlashKVCache(4, 10, 2, 64, dtype=torch.float32)
+    k, v = torch.randn(2, 3, 2, 64), torch.randn(2, 3, 2, 64)
+    c.prefill(k, v, 5, torch.tensor([3, 1]))
+    assert torch.equal(c.k_cache[3, 5:8], k[0]) and torch.equal(c.v_cache[1, 5:8], v[1])
+    assert c.seq_lens.tolist() == [0, 8, 0, 8]
+    c.set_cross_attention(k, v, torch.tensor([0, 2]))
+    assert torch.equal(c.k_cache[2, :3], k[1]) and c.cross_attn_len == 3
