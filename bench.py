@@ -784,6 +784,80 @@ def decode_cpu_baseline(budget_s: float = 15.0) -> dict:
     return out
 
 
+def _cpu_time(fn, budget_s: float, min_runs: int = 3):
+    fn()  # warm-up
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_runs or (time.perf_counter() < t_end and len(times) < 50):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return float(np.median(times)), len(times)
+
+
+def extra_cpu_baselines(budget_s: float = 6.0) -> dict:
+    """The reference's CPU paths beside the remaining rows, bounded samples in fp32 on the host
+    cores: the decode step (one layer of the large-v3 decoder for 64 streams through the oracle's
+    _sdpa_attn_with_kvcache restatement, scaled to 32 layers), the cross fill (one layer's key /
+    value projection of one window and its index_put, scaled to 16 windows x 32 layers) and
+    median_filter (the sort-based form of dtw_align.py:65-78 on one chunk's 10 heads)."""
+    import torch.nn.functional as F
+
+    from oracle.attention_oracle import kvcache_torch
+    from oracle.dtw_oracle import median_filter_torch
+    from whisperdrz_amd.decoder import ResidualAttentionBlock
+    from whisperdrz_amd.kv_cache import FlashKVCache
+
+    cores = min(len(os.sched_getaffinity(0)), 16)
+    torch.set_num_threads(cores)
+    out = {}
+    torch.manual_seed(0)
+    Bs = 64
+    def ref_kv(q, kc, vc, k=None, v=None, cache_seqlens=None, cache_batch_idx=None, softmax_scale=None,
+               causal=False):  # the restatement takes no causal flag (bottom-right is implied by the append)
+        return kvcache_torch(q, kc, vc, k, v, cache_seqlens, cache_batch_idx, softmax_scale)
+
+    blk = ResidualAttentionBlock(H * D, H, attn_kvcache=ref_kv).eval()
+    sk, ck = FlashKVCache(Bs, 448, H, D, dtype=torch.float32), FlashKVCache(Bs, 1500, H, D, dtype=torch.float32)
+    g = torch.Generator().manual_seed(3)
+    ck.k_storage.normal_(generator=g)
+    ck.v_storage.normal_(generator=g)
+    sk.seq_lens.copy_(torch.from_numpy(_lengths(8, Bs, 1, 400).astype(np.int32)) - 1)
+    x = torch.randn((Bs, 1, H * D), generator=g)
+    slots = torch.arange(Bs)
+    with torch.no_grad():
+        med, n = _cpu_time(lambda: blk.forward_flash(x, sk, ck, slot_indices=slots), budget_s)
+    out["decode_step"] = {"value": round(32 * med * 1e3, 1), "unit": "ms/step", "cores": cores, "kind": "port",
+                          "sample": f"one decoder layer (self + cross attention through the torch restatement of "
+                          f"_sdpa_attn_with_kvcache, MLP, LayerNorms) for 64 streams in fp32, median of {n} runs "
+                          f"({med * 1e3:.1f} ms) x 32 layers; logits GEMM not included"}
+    xa = torch.randn((1, FILL_L, H * D), generator=g)
+    wk, wv, bv = torch.randn(H * D, H * D) / 36, torch.randn(H * D, H * D) / 36, torch.randn(H * D)
+    fc = FlashKVCache(1, FILL_L, H, D, dtype=torch.float32)
+    sl = torch.zeros(1, dtype=torch.long)
+
+    def fill():
+        k = F.linear(xa, wk).view(1, FILL_L, H, D)
+        v = F.linear(xa, wv, bv).view(1, FILL_L, H, D)
+        fc.k_cache[sl, :FILL_L] = k
+        fc.v_cache[sl, :FILL_L] = v
+
+    med, n = _cpu_time(fill, budget_s)
+    out["cross_fill"] = {"value": round(med * FILL_B * 32 * 1e3, 1), "unit": "ms per 16 windows x 32 layers",
+                         "cores": cores, "kind": "port",
+                         "sample": f"one window's key/value projection + index_put into a head-major cache, fp32, "
+                         f"median of {n} runs ({med * 1e3:.1f} ms) x 16 windows x 32 layers"}
+    w = torch.randn((1, DTW_H, DTW_T, DTW_A), generator=g)
+    med, n = _cpu_time(lambda: median_filter_torch(w, 7), budget_s)
+    nbytes = 2 * w.numel() * 4
+    out["median_filter"] = {"value": round(nbytes / med / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
+                            "sample": f"sort-based median_filter (dtw_align.py:65-78) width 7 on one chunk "
+                            f"[1, 10, 448, 1500] fp32, median of {n} runs ({med * 1e3:.1f} ms)"}
+    for k, v in out.items():
+        log(f"[bench] {k} cpu baseline: {v['value']} {v['unit']}")
+    return out
+
+
 def cpu_baseline(budget_s: float = 12.0) -> dict:
     from oracle.attention_oracle import sdpa_torch
 
@@ -944,6 +1018,14 @@ def main() -> int:
     if dec is not None and not args.no_cpu:
         for name, base in decode_cpu_baseline().items():
             dec[name]["cpu_baseline"] = base
+    if not args.no_cpu and (step is not None or fill is not None or dtw is not None):
+        extra = extra_cpu_baselines()
+        if step is not None:
+            step["cpu_baseline"] = extra["decode_step"]
+        if fill is not None:
+            fill["cpu_baseline"] = extra["cross_fill"]
+        if dtw is not None:
+            dtw["median_filter"]["cpu_baseline"] = extra["median_filter"]
 
     line = {
         "metric": METRIC,
