@@ -78,6 +78,12 @@ __device__ __forceinline__ float softmax_exp(float x, float m) { return fast_exp
 __device__ __forceinline__ float softmax_value(float x, float2 st) {
   return softmax_scale_e(softmax_exp(x, st.x), st.y);
 }
+// The same for an unscaled score x whose softmax argument is x * c (c = scale^2 * log2e for the
+// fused path's raw Q.K products): the scale rides in the FMA instead of a multiply per score.
+__device__ __forceinline__ float softmax_exp_c(float x, float c, float m) { return fast_exp2(__builtin_fmaf(x, c, -m)); }
+__device__ __forceinline__ float softmax_value_c(float x, float c, float2 st) {
+  return softmax_scale_e(softmax_exp_c(x, c, st.x), st.y);
+}
 
 // f(0), f(1), ..., f(N-1) as straight-line code.
 template <int N, typename F>
@@ -829,7 +835,8 @@ __global__ __launch_bounds__(NT) void dtw_band_kernel(DtwArgs a) {
 //
 // One 16 x 16 score tile = two v_mfma_f32_16x16x32 over the 64 head dimensions; both passes
 // call qk_product with the same operands, so every score is bit-identical between them (the exact
-// zero of a zero-variance column depends on it). Lane l: text row 4*(l/16) + i of the tile
+// zero of a zero-variance column depends on it). The products stay unscaled: s^2 is folded,
+// with log2e, into the softmax's FMA (softmax_exp_c). Lane l: text row 4*(l/16) + i of the tile
 // (i = 0..3), key l % 16; operands are 16-byte slices of the head rows (dims 8*(l/16) and
 // 32 + 8*(l/16)).
 // ---------------------------------------------------------------------------------------------
@@ -877,11 +884,9 @@ __device__ __forceinline__ QkKey<T> qk_key_ops(const DtwQkArgs& q, int h, int b,
 template <typename T>
 __device__ __forceinline__ f32x4 qk_product(const DtwQkArgs& q, const QkKey<T>& k,
                                             const typename QkMfma<T>::op_t (&qa)[2]) {
+  (void)q;
   f32x4 acc = QkMfma<T>::run(qa[0], k.k0, f32x4{0.f, 0.f, 0.f, 0.f});
-  acc = QkMfma<T>::run(qa[1], k.k1, acc);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) acc[i] *= q.scale2;
-  return acc;
+  return QkMfma<T>::run(qa[1], k.k1, acc);  // unscaled: the softmax applies scale^2 * log2e
 }
 
 // max / sum over the 16 lanes of a lane group (one DPP row), every lane gets the result
@@ -942,6 +947,7 @@ __global__ __launch_bounds__(512) void dtw_qk_rowcol_kernel(DtwArgs a, DtwQkArgs
   const int rows_valid = len < a.T ? len : a.T;
   const int64_t bh = (int64_t)b * a.H + h;
   const int n_tiles = (a.A + 15) >> 4;
+  const float csc = q.scale2 * kLog2e;  // the same value in the filter pass
 
   // this wavefront's key operands, the same for every row block of the chunk: held in registers
   QkKey<T> kop[kQkTilesPerWave];
@@ -989,14 +995,14 @@ __global__ __launch_bounds__(512) void dtw_qk_rowcol_kernel(DtwArgs a, DtwQkArgs
       float m = red[0][0][r];
 #pragma unroll
       for (int w = 1; w < kQkWaves; ++w) m = fmaxf(m, red[0][w][r]);
-      st[i].x = m * kLog2e;
+      st[i].x = m * csc;  // max(x) * c is max(x * c) exactly: c > 0 and rounding is monotone
     }
     float sm[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int u = 0; u < kQkTilesPerWave; ++u)
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        s[u][i] = softmax_exp(s[u][i], st[i].x);  // -inf -> 0
+        s[u][i] = softmax_exp_c(s[u][i], csc, st[i].x);  // -inf -> 0
         sm[i] += s[u][i];
       }
 #pragma unroll
@@ -1102,6 +1108,7 @@ __global__ __launch_bounds__(256, 2) void dtw_qk_band_kernel(DtwArgs a, DtwQkArg
   // double-buffered: head h is normalised into buffer h % 2, so the writes of head h + 1 never
   // meet the median reads of head h and one barrier per head suffices
   __shared__ __align__(16) float tiles[2][kQsRows * kQsPitch];
+  const float csc = q.scale2 * kLog2e;  // the same value in the statistics pass
   const int key_base = c0 - 16;  // key of tile column 0
 
   float acc[kQsRows / 4][4];
@@ -1162,7 +1169,7 @@ __global__ __launch_bounds__(256, 2) void dtw_qk_band_kernel(DtwArgs a, DtwQkArg
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           // computed for every lane (a clamped key has a finite score), then selected: no branch
-          const float v = (softmax_value(sc_all[i][hf][r], cur.st[hf][r]) - c.x) * c.y;
+          const float v = (softmax_value_c(sc_all[i][hf][r], csc, cur.st[hf][r]) - c.x) * c.y;
           z[r] = ok ? v : 0.f;
         }
         float* row0 = tile + (16 * hf + 4 * grp) * kQsPitch;
