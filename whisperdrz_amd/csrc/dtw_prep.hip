@@ -28,6 +28,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <type_traits>
+
 #include "wdrz_common.h"
 #include "wdrz_launch.h"
 
@@ -1037,25 +1039,32 @@ __global__ __launch_bounds__(512) void dtw_qk_rowcol_kernel(DtwArgs a, DtwQkArgs
       const float inv_nb = any ? 1.f / fnb : 0.f;
       const float ra = any ? fnb / n_new : 0.f;
       const float rb = any ? n_l * fnb / n_new : 0.f;
+      // FULL: every row of the block is valid (all but the last block of a row range), so the
+      // per-row selects drop out; the arithmetic is the same either way.
+      auto fold = [&](auto full) __attribute__((always_inline)) {
+        constexpr bool FULL = decltype(full)::value;
 #pragma unroll
-      for (int u = 0; u < kQkTilesPerWave; ++u) {
-        float p[4], sum = 0.f;
+        for (int u = 0; u < kQkTilesPerWave; ++u) {
+          float p[4], sum = 0.f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[i] = softmax_scale_e(s[u][i], st[i].y);
-          sum += rv[i] ? p[i] : 0.f;
+          for (int i = 0; i < 4; ++i) {
+            p[i] = softmax_scale_e(s[u][i], st[i].y);
+            sum += (FULL || rv[i]) ? p[i] : 0.f;
+          }
+          const float mean_b = sum * inv_nb;
+          float sq = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float d = p[i] - mean_b;
+            sq += (FULL || rv[i]) ? d * d : 0.f;
+          }
+          const float d = mean_b - mu[u];
+          mu[u] += d * ra;
+          m2[u] += sq + d * d * rb;
         }
-        const float mean_b = sum * inv_nb;
-        float sq = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float d = p[i] - mean_b;
-          sq += rv[i] ? d * d : 0.f;
-        }
-        const float d = mean_b - mu[u];
-        mu[u] += d * ra;
-        m2[u] += sq + d * d * rb;
-      }
+      };
+      if (t0 + 16 <= rows_valid) fold(std::true_type{});
+      else fold(std::false_type{});
       n_l = n_new;
     }
   }
