@@ -27,9 +27,11 @@
 // largely serialise):
 //   * Q is pre-scaled by scale*log2(e) once; fmax runs without NaN canonicalisation (the file
 //     is built with -fno-honor-nans; masked scores are -inf, never NaN).
-//   * Lazy rescaling: the running max only moves when a score exceeds it by more than 2^kTau
-//     (P values up to 2^8 are exact enough in bf16 and harmless in fp32 sums); in steady state
-//     the output accumulator is never rescaled.
+//   * Lazy rescaling: the running max only moves when a score exceeds it by more than kTau
+//     (causal kernel: checked against the step's max) or when a step's row sum exceeds
+//     kSumLimit (non-causal kernel: the sum is needed anyway, the max is not); P values up to
+//     2^8 / 2^10 are exact enough in bf16 and harmless in fp32 sums, and in steady state the
+//     output accumulator is never rescaled.
 //   * Row sums are plain fp32 adds of the unrounded P into four independent partial sums.
 //     (v_dot2 of the packed P against (1, 1) issues half as many instructions, but measured on
 //     gfx950 it costs 1.6x an add and overlaps the other wavefront's MFMAs far less: 23% vs
@@ -51,7 +53,8 @@ constexpr int kBN = 64;               // key rows per LDS tile
 constexpr int kBS = 32;               // key rows per sub-step
 constexpr int kPitchK = kHeadDim + 8; // K tile row pitch in elements (16-byte pad)
 constexpr int kNumBuf = 3;            // LDS tile buffers
-constexpr float kTau = 8.0f;          // lazy-rescale threshold (log2 units)
+constexpr float kTau = 8.0f;          // lazy-rescale threshold (log2 units), causal kernel
+constexpr float kSumLimit = 1024.0f;  // per-step row-sum limit of the non-causal kernel
 
 template <typename T> struct Mfma;
 template <> struct Mfma<Bf16> {
@@ -378,9 +381,11 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const uint16_t* p) {
 //
 // Per step s a wavefront issues PV(s-1) and S(s) (16 MFMAs at raised wave priority), reads the
 // next step's K and V^T operands from LDS, then runs the softmax of S(s). On gfx950 the softmax
-// VALU work and the MFMAs of the wavefronts sharing a SIMD largely serialise, so the step time
-// is their sum: the VALU side is cut to 32 exp2, 16 packs, 16 dot2 row sums and the max check
-// per step, and the subtraction of the running max is folded into the S accumulation, which
+// VALU work and the MFMAs of the wavefronts sharing a SIMD largely serialise (a softmax waits
+// for the score MFMAs issued just before it, queued in the matrix pipe behind the other
+// wavefront's), so the step time is close to their sum: the VALU side is cut to 32 exp2,
+// 16 packs, 32 adds (the row sums, which double as the rescale check) and one compare per
+// step, and the subtraction of the running max is folded into the S accumulation, which
 // starts from -m_run (cinit) instead of zero.
 //
 // K/V tiles of 64 keys are staged through registers into four LDS buffers (tile t+2 loaded
@@ -518,10 +523,32 @@ __global__ __launch_bounds__(kFThreads, 1) void dense_fwd_kernel(DenseArgs a) {
       acc_o[1][i][x] = 0.f;
     }
   float m_run[2] = {0.f, 0.f};
-  float l_part[2][4] = {{0.f, 0.f, 0.f, 0.f}, {0.f, 0.f, 0.f, 0.f}};  // 4 partial row sums
+  float l_run[2] = {0.f, 0.f};
   op_t pcur[2][2];  // [qb][16-key chunk] P of the last softmax
 
-  // Online softmax of step s for query block qb (on sacc[qb]).
+  // Online softmax of step s for query block qb (on sacc[qb], scores relative to m_run).
+  // Fast path: exponentiate against the current max and keep the step's row sum. Each lane's
+  // sum covers 16 scores, so a sum above kSumLimit = 1024 means some score exceeded the max by
+  // more than log2(1024/16) = 6 (or overflowed): only then is the true max taken, the state
+  // rescaled and the step redone. P therefore stays below 1024, which bf16 P and the fp32
+  // accumulators take exactly as well as P <= 1. The first step always takes the true max.
+  // (This replaces a per-step max over the 16 scores: ~10 fewer VALU instructions per block.)
+  auto exp_sum = [&](int qb) __attribute__((always_inline)) {
+    float t[4];
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      u32x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p0 = fast_exp2(sacc[qb][ch * 8 + 2 * e]);
+        const float p1 = fast_exp2(sacc[qb][ch * 8 + 2 * e + 1]);
+        w[e] = Mfma<T>::pack(p0, p1);
+        t[e] = ch == 0 ? p0 + p1 : t[e] + p0 + p1;
+      }
+      pcur[qb][ch] = __builtin_bit_cast(op_t, w);
+    }
+    return (t[0] + t[1]) + (t[2] + t[3]);
+  };
   auto softmax = [&](int qb, int s) __attribute__((always_inline)) {
     const int k0 = s * kBS;
     if (k0 + kBS > a.Lk) {
@@ -529,21 +556,20 @@ __global__ __launch_bounds__(kFThreads, 1) void dense_fwd_kernel(DenseArgs a) {
       for (int x = 0; x < 16; ++x)
         if (k0 + 16 * (x >> 3) + 8 * hl + (x & 7) >= a.Lk) sacc[qb][x] = -INFINITY;
     }
-    // a tree of 3-input maxima (depth 3, not a chain of 8), then across the lane halves
-    const f32x16& v = sacc[qb];
-    const float t0 = fmaxf(fmaxf(v[0], v[1]), v[2]), t1 = fmaxf(fmaxf(v[3], v[4]), v[5]);
-    const float t2 = fmaxf(fmaxf(v[6], v[7]), v[8]), t3 = fmaxf(fmaxf(v[9], v[10]), v[11]);
-    const float t4 = fmaxf(fmaxf(v[12], v[13]), v[14]);
-    const float mx = half_swap_max(fmaxf(fmaxf(fmaxf(t0, t1), t2), fmaxf(fmaxf(t3, t4), v[15])));  // relative to m_run
-    // First step: adopt the max. Later: move the max only when it grew by more than kTau.
-    if (__any(s == 0 || mx > kTau)) {
+    float st = s == 0 ? INFINITY : exp_sum(qb);
+    if (__any(!(st <= kSumLimit))) {
       asm volatile("" ::: "memory");  // keep this rare path a branch
+      // a tree of 3-input maxima (depth 3, not a chain of 8), then across the lane halves
+      const f32x16& v = sacc[qb];
+      const float t0 = fmaxf(fmaxf(v[0], v[1]), v[2]), t1 = fmaxf(fmaxf(v[3], v[4]), v[5]);
+      const float t2 = fmaxf(fmaxf(v[6], v[7]), v[8]), t3 = fmaxf(fmaxf(v[9], v[10]), v[11]);
+      const float t4 = fmaxf(fmaxf(v[12], v[13]), v[14]);
+      const float mx = half_swap_max(fmaxf(fmaxf(fmaxf(t0, t1), t2), fmaxf(fmaxf(t3, t4), v[15])));
       const float delta = s == 0 ? mx : fmaxf(mx, 0.f);
       m_run[qb] += delta;
       if (s != 0) {
         const float alpha = fast_exp2(-delta);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) l_part[qb][j] *= alpha;
+        l_run[qb] *= alpha;
 #pragma unroll
         for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -554,19 +580,9 @@ __global__ __launch_bounds__(kFThreads, 1) void dense_fwd_kernel(DenseArgs a) {
         sacc[qb][x] -= delta;
         cinit[qb][x] = -m_run[qb];
       }
+      st = exp_sum(qb);
     }
-#pragma unroll
-    for (int ch = 0; ch < 2; ++ch) {
-      u32x4 w;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float p0 = fast_exp2(sacc[qb][ch * 8 + 2 * e]);
-        const float p1 = fast_exp2(sacc[qb][ch * 8 + 2 * e + 1]);
-        w[e] = Mfma<T>::pack(p0, p1);
-        l_part[qb][e] = l_part[qb][e] + p0 + p1;
-      }
-      pcur[qb][ch] = __builtin_bit_cast(op_t, w);
-    }
+    l_run[qb] += st;
   };
   auto mfma_s = [&](int qb) __attribute__((always_inline)) {
 #pragma unroll
@@ -625,8 +641,7 @@ __global__ __launch_bounds__(kFThreads, 1) void dense_fwd_kernel(DenseArgs a) {
   // ---- normalise, stage O^T through LDS as [query][dim] rows, store whole rows ----
 #pragma unroll
   for (int qb = 0; qb < 2; ++qb) {
-    const float l_run = (l_part[qb][0] + l_part[qb][1]) + (l_part[qb][2] + l_part[qb][3]);
-    const float inv = 1.f / (l_run + __shfl_xor(l_run, 32));
+    const float inv = 1.f / (l_run[qb] + __shfl_xor(l_run[qb], 32));
     e_t* orow = &smem[(wave * 64 + qb * 32 + l32) * kPitchK];
 #pragma unroll
     for (int db = 0; db < 2; ++db)
