@@ -123,6 +123,32 @@ int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, co
                       size_t workspace_bytes, void* stream);
 
 /*
+ * Attention against a slot KV cache without any allocation: wdrz_attn_kvcache with its split-KV
+ * workspace taken from a static device array of WDRZ_NOALLOC_SCRATCH_BYTES per GPU.
+ *
+ * No counterpart in the reference. For callers that cannot allocate: code under hipGraph
+ * capture without an allocator, tight serving loops, harnesses that forbid hipMalloc. It calls
+ * no hipMalloc / hipFree and no allocating library routine.
+ *
+ * Arguments and semantics as wdrz_attn_kvcache, without workspace / workspace_bytes.
+ * Limit: calls whose workspace (wdrz_attn_kvcache_workspace_size) exceeds
+ * WDRZ_NOALLOC_SCRATCH_BYTES are rejected with WDRZ_EUNSUPPORTED (the split plan never asks
+ * for more than ~4.33 MB at head_dim 64). The array is set up (address taken, cleared by a
+ * kernel on `stream`) on the first call on each device and kept until the process ends.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU race; serialise
+ * them or use wdrz_attn_kvcache with separate workspaces.
+ */
+#define WDRZ_NOALLOC_SCRATCH_BYTES ((size_t)4718592) /* 4.5 MiB */
+int wdrz_attn_kvcache_noalloc(int dtype, const void* q, void* k_cache, void* v_cache,
+                              const void* k_new, const void* v_new, const int32_t* cache_seqlens,
+                              const int32_t* cache_batch_idx, void* o, int64_t B, int64_t sq,
+                              int64_t H, int64_t D, int64_t n_slots, int64_t Lmax,
+                              const int64_t* q_strides, const int64_t* kc_strides,
+                              const int64_t* vc_strides, const int64_t* kn_strides,
+                              const int64_t* vn_strides, const int64_t* o_strides,
+                              float softmax_scale, int causal, void* stream);
+
+/*
  * Residual add + LayerNorm of the decode step.
  *
  * Replaces: the residual add closing a sub-layer and the LayerNorm opening the next

@@ -21,6 +21,7 @@ EXPORTED_SYMBOLS = (
     "wdrz_attn_fwd",
     "wdrz_attn_kvcache_workspace_size",
     "wdrz_attn_kvcache",
+    "wdrz_attn_kvcache_noalloc",
     "wdrz_add_layernorm",
     "wdrz_masked_argmax",
     "wdrz_log_mel_workspace_size",
@@ -67,6 +68,8 @@ def _declare(lib: ctypes.CDLL) -> None:
         ctypes.c_float, ctypes.c_int,  # softmax_scale, causal
         _p, ctypes.c_size_t, _p,  # workspace, bytes, stream
     ]
+    lib.wdrz_attn_kvcache_noalloc.restype = ctypes.c_int
+    lib.wdrz_attn_kvcache_noalloc.argtypes = lib.wdrz_attn_kvcache.argtypes[:-3] + [_p]  # no workspace
     lib.wdrz_add_layernorm.restype = ctypes.c_int
     lib.wdrz_add_layernorm.argtypes = [
         ctypes.c_int, _p, _i64, _p, _i64,  # dtype, x, x stride, delta, delta stride

@@ -18,7 +18,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libwdrz_attn.so"
 LIB_PATH = PKG_DIR / LIB_NAME
-SOURCES = ["attn_kvcache.hip", "attn_dense.hip", "dtw_prep.hip", "dtw_qk.hip", "logmel.hip", "decode_ops.hip", "kv_fill.hip", "wdrz_capi.cpp"]
+SOURCES = ["attn_kvcache.hip", "attn_dense.hip", "dtw_prep.hip", "dtw_qk.hip", "logmel.hip", "decode_ops.hip", "kv_fill.hip", "kv_noalloc.hip", "wdrz_capi.cpp"]
 ARCH = "gfx950"
 
 

@@ -132,6 +132,18 @@ int dtw_qk_heads(int dtype, const void* const* q_heads, const int64_t* q_strides
 }
 }  // namespace
 
+namespace wdrz {
+int set_last_error(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+}  // namespace wdrz
+
 extern "C" {
 
 const char* wdrz_last_error(void) { return g_last_error.c_str(); }

@@ -159,4 +159,7 @@ hipError_t launch_dtw_qk_prep(int dtype, DtwArgs a, const DtwQkArgs& q, hipStrea
 void dtw_workspace_layout(void* ws, DtwArgs* a);
 hipError_t launch_dtw_prep(DtwArgs a, hipStream_t stream);
 
+// Sets the thread-local message wdrz_last_error() returns and returns `code` (C-ABI layer).
+int set_last_error(int code, const char* fmt, ...);
+
 }  // namespace wdrz
