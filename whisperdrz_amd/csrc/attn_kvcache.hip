@@ -295,8 +295,8 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
   const char* kn_row = HAS_NEW ? a.kn + b * a.kns[0] + h * a.kns[2] + r * 16 : nullptr;
   const char* vn_row = HAS_NEW ? a.vn + b * a.vns[0] + h * a.vns[2] + r * 16 : nullptr;
 
-  for (int base = k_begin + g; base < k_end; base += G * kUnroll) {
-    u32x4 kr[kUnroll], vr[kUnroll];
+  // Batches of kUnroll keys per lane group. Loads past the row's end re-read its last key.
+  auto load_batch = [&](int base, u32x4 (&kr)[kUnroll], u32x4 (&vr)[kUnroll]) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
       const int kk = min(base + u * G, k_end - 1);
@@ -312,6 +312,8 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
       kr[u] = load16_stream(kp);
       vr[u] = load16_stream(vp);
     }
+  };
+  auto compute_batch = [&](int base, const u32x4 (&kr)[kUnroll], const u32x4 (&vr)[kUnroll]) __attribute__((always_inline)) {
     // ---- scores (log2 units), masked to -inf outside each query's key range ----
     float sc[SQ][kUnroll];
 #pragma unroll
@@ -396,6 +398,28 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
           for (int e = 0; e < EPL; ++e) acc[t][e] = __builtin_fmaf(p, vs.v[e], acc[t][e]);
         }
       }
+    }
+  };
+  constexpr int kStride = G * kUnroll;
+  if constexpr (SQ == 1) {
+    // Decode rows: software-pipelined, the next batch's loads in flight while the current one
+    // is computed (one workgroup streams a long row ~15% faster; +32 registers).
+    u32x4 kA[kUnroll], vA[kUnroll], kB[kUnroll], vB[kUnroll];
+    int base = k_begin + g;
+    if (base < k_end) load_batch(base, kA, vA);
+    for (; base < k_end; base += 2 * kStride) {
+      const bool more = base + kStride < k_end;
+      if (more) load_batch(base + kStride, kB, vB);
+      compute_batch(base, kA, vA);
+      if (!more) break;
+      if (base + 2 * kStride < k_end) load_batch(base + 2 * kStride, kA, vA);
+      compute_batch(base + kStride, kB, vB);
+    }
+  } else {
+    for (int base = k_begin + g; base < k_end; base += kStride) {
+      u32x4 kr[kUnroll], vr[kUnroll];
+      load_batch(base, kr, vr);
+      compute_batch(base, kr, vr);
     }
   }
 
