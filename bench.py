@@ -132,9 +132,26 @@ def bench_encoder(dev, steps: int, warmup: int) -> dict:
 
 
 def _lengths(seed, n, lo, hi):
-    from oracle.attention_oracle import decode_lengths  # seeded draw only; not timed
+    """Attended lengths L_i ~ U{lo..hi} (inclusive) from the seed: the draw the parity tests use."""
+    return np.random.default_rng(seed).integers(lo, hi + 1, size=n, dtype=np.int64)
 
-    return decode_lengths(seed, n, lo, hi)
+
+def host_cores() -> int:
+    """Threads for the CPU baselines: every core this process may run on (no cap)."""
+    return len(os.sched_getaffinity(0))
+
+
+def _projected_cross_cache(xa, dev, seed):
+    """Cross K/V of one layer as config 4 states them: the simulated encoder output xa
+    [B, L, 1280] projected with this layer's seeded W_k, W_v ~ N(0, 1/1280) (unit-variance K/V),
+    stored head-major [B, H, L, D] and viewed as [B, L, H, D]."""
+    Bn, Ln, n_state = xa.shape
+    g = torch.Generator(device=dev).manual_seed(seed)
+    w = (torch.randn((2, n_state, n_state), generator=g, device=dev) * n_state ** -0.5).to(torch.bfloat16)
+    kv = torch.empty((2, Bn, H, Ln, D), dtype=torch.bfloat16, device=dev)
+    for j in range(2):
+        kv[j].copy_((xa @ w[j]).view(Bn, Ln, H, D).permute(0, 2, 1, 3))
+    return kv[0].permute(0, 2, 1, 3), kv[1].permute(0, 2, 1, 3)
 
 
 def _head_major_cache(n_slots, Lmax, dev, seed):
@@ -196,9 +213,13 @@ def bench_decode(dev, steps: int, warmup: int) -> dict:
         return out
 
     # shared per-layer caches: 32 distinct self caches (capacity 448) and cross caches (1500)
-    log("[bench] decode: generating 32 self caches (64 x 448) and 32 cross caches (64 x 1500), head-major bf16")
+    log("[bench] decode: generating 32 self caches (64 x 448, K/V ~ N(0,1)) and 32 cross caches "
+        "(64 x 1500, projected per layer from one N(0,1) encoder output), head-major bf16")
     self_kv = [_head_major_cache(Bs, Lself, dev, 3000 + i) for i in range(N_LAYERS)]
-    cross_kv = [_head_major_cache(Bs, Lcross, dev, 4000 + i) for i in range(N_LAYERS)]
+    gx = torch.Generator(device=dev).manual_seed(3999)
+    xa = torch.randn((Bs, Lcross, H * D), generator=gx, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    cross_kv = [_projected_cross_cache(xa, dev, 4000 + i) for i in range(N_LAYERS)]
+    del xa
     for sq in (1, 5):
         _WORKSPACES.reserve(dev, max(kvcache_workspace_size(Bs, sq, H, D, Lself),
                                      kvcache_workspace_size(Bs, sq, H, D, Lcross)))
@@ -230,8 +251,11 @@ def bench_decode(dev, steps: int, warmup: int) -> dict:
                                     softmax_scale=0.125, causal=False, out=o4[i])
 
     bytes4 = 2 * Bs * Lcross * H * D * E + 2 * H * D * E * Bs + 4 * Bs
-    res["config4_cross_decode"] = run_graph("config4 cross sq=1", body4, bytes4,
-                                            kernels=("kv_attn_kernel<wdrz::Bf16, 1, false>",))
+    res["config4_cross_decode"] = run_graph(
+        "config4 cross sq=1", body4, bytes4,
+        {"inputs": "per layer K = xa W_k, V = xa W_v with xa ~ N(0,1) [64, 1500, 1280] bf16 (one simulated "
+                   "encoder output) and seeded W_k, W_v ~ N(0, 1/1280) [1280, 1280] per layer; queries ~ N(0,1)"},
+        kernels=("kv_attn_kernel<wdrz::Bf16, 1, false>",))
 
     # ---- config 5: 5-token draft verify (self, causal within the draft) + cross ----
     sq = 5
@@ -666,7 +690,7 @@ def logmel_cpu_baseline(budget_s: float = 8.0) -> dict:
     """The reference's op sequence (torch.stft + filterbank + log) on the host cores, one window."""
     from oracle.mel_oracle import log_mel_torch, mel_filterbank
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = host_cores()
     torch.set_num_threads(cores)
     fb = mel_filterbank(MEL_MELS)
     x = 0.1 * torch.randn(MEL_N, generator=torch.Generator().manual_seed(1))
@@ -696,7 +720,7 @@ def dtw_cpu_baseline(budget_s: float = 12.0) -> dict:
     """The reference's op sequence in torch fp32 on the host cores, on one chunk."""
     from oracle.dtw_oracle import dtw_prep_torch
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = host_cores()
     torch.set_num_threads(cores)
     g = torch.Generator().manual_seed(1)
     w = 2.5 * torch.randn((1, DTW_H, DTW_T, DTW_A), generator=g)
@@ -730,7 +754,7 @@ def decode_cpu_baseline(budget_s: float = 15.0) -> dict:
     them) per second of CPU time."""
     from oracle.attention_oracle import kvcache_torch
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = host_cores()
     torch.set_num_threads(cores)
     Bs, Lself, Lcross = 64, 448, 1500
     g = torch.Generator().manual_seed(2)
@@ -808,7 +832,7 @@ def extra_cpu_baselines(budget_s: float = 6.0) -> dict:
     from whisperdrz_amd.decoder import ResidualAttentionBlock
     from whisperdrz_amd.kv_cache import FlashKVCache
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = host_cores()
     torch.set_num_threads(cores)
     out = {}
     torch.manual_seed(0)
@@ -861,7 +885,7 @@ def extra_cpu_baselines(budget_s: float = 6.0) -> dict:
 def cpu_baseline(budget_s: float = 12.0) -> dict:
     from oracle.attention_oracle import sdpa_torch
 
-    cores = min(len(os.sched_getaffinity(0)), 16)
+    cores = host_cores()
     torch.set_num_threads(cores)
     B, L = 1, 1500
     g = torch.Generator().manual_seed(1)
@@ -1039,7 +1063,7 @@ def main() -> int:
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded N(0,1) Q/K/V and K/V caches generated on the GPU)",
+        "data": "synthetic, generated on the GPU: seeded N(0,1) Q/K/V and self K/V caches; cross K/V caches projected per layer from one seeded N(0,1) encoder output",
         "config": {
             "workload": "config2: encoder self-attention B=16 H=20 L=1500 D=64 bf16, non-causal, scale 1/8, "
             "32 sequential layers with distinct inputs; one step = 32 layers",
