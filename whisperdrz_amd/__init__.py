@@ -18,10 +18,17 @@ from .decode_ops import add_layernorm_, layer_norm, masked_argmax
 from .dtw import (compute_attention, dtw_attention_prep, dtw_prep, dtw_prep_batch, dtw_prep_workspace_size,
                   median_filter)
 
-HAS_WDRZ = _lib.available()
+from .debug import check_kvcache_metadata, force_torch, probe
+
+# Import-time probe, the counterpart of the reference's HAS_FLASH_ATTN (model.py:79-84): true when
+# the HIP library loads and WDRZ_FORCE_TORCH is not set.
+HAS_WDRZ = probe()
 
 __all__ = [
     "HAS_WDRZ",
+    "check_kvcache_metadata",
+    "force_torch",
+    "probe",
     "LogMelSpectrogram",
     "add_layernorm_",
     "layer_norm",

@@ -6,10 +6,21 @@ missing or fails to load, every compute entry point raises ``RuntimeError``.
 from __future__ import annotations
 
 import ctypes
+import os
 import threading
 from pathlib import Path
 
-LIB_PATH = Path(__file__).resolve().parent / "libwdrz_attn.so"
+RELEASE_LIB_PATH = Path(__file__).resolve().parent / "libwdrz_attn.so"
+DEBUG_LIB_PATH = Path(__file__).resolve().parent / "libwdrz_attn_debug.so"
+
+
+def debug_mode() -> bool:
+    """WDRZ_DEBUG=1: host-side checks of device metadata before every cached-attention call
+    (the debug library and the Python checks; synchronous, so not for graph capture)."""
+    return os.environ.get("WDRZ_DEBUG", "0") not in ("", "0")
+
+
+LIB_PATH = DEBUG_LIB_PATH if debug_mode() else RELEASE_LIB_PATH
 
 WDRZ_F32, WDRZ_F16, WDRZ_BF16 = 0, 1, 2
 WDRZ_OK, WDRZ_EINVAL, WDRZ_EUNSUPPORTED, WDRZ_ELAUNCH, WDRZ_EWORKSPACE = 0, 1, 2, 3, 4

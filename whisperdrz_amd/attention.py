@@ -184,6 +184,11 @@ def flash_attn_with_kvcache(
     else:
         seqlens = None
     bidx = None if cache_batch_idx is None else _as_int32("cache_batch_idx", cache_batch_idx, B, device)
+    if _lib.debug_mode():  # host copies of the metadata: debugging runs only, not graph capture
+        from .debug import check_kvcache_metadata
+
+        check_kvcache_metadata(seqlens.cpu().numpy() if seqlens is not None else None,
+                               bidx.cpu().numpy() if bidx is not None else None, sq, S, Lmax, has_new)
     if softmax_scale is None:
         softmax_scale = D ** -0.5
     if out is None:

@@ -3,8 +3,11 @@
 Usage: python -m whisperdrz_amd.build [--debug]
 
 The library is a plain shared object (no torch / pybind dependency); the Python side loads it
-with ctypes. ``--debug`` builds with -O1 -g and device-side bounds assertions off, for host
-debugging only.
+with ctypes. Every build also links libwdrz_attn_debug.so: the same kernel objects with the C-ABI
+layer compiled with WDRZ_DEBUG_CHECKS, which copies the device metadata of a call (slot ids,
+cache lengths) to the host and rejects out-of-range rows before launching (synchronous, so not
+for graph capture; selected with WDRZ_DEBUG=1). ``--debug`` compiles everything with -O1 -g, for
+host-side debugging.
 """
 from __future__ import annotations
 
@@ -18,6 +21,7 @@ PKG_DIR = Path(__file__).resolve().parent
 CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libwdrz_attn.so"
 LIB_PATH = PKG_DIR / LIB_NAME
+DEBUG_LIB_PATH = PKG_DIR / "libwdrz_attn_debug.so"
 SOURCES = ["attn_kvcache.hip", "attn_dense.hip", "dtw_prep.hip", "dtw_qk.hip", "logmel.hip", "decode_ops.hip", "kv_fill.hip", "kv_noalloc.hip", "wdrz_capi.cpp"]
 ARCH = "gfx950"
 
@@ -66,12 +70,20 @@ def build_library(debug: bool = False, verbose: bool = False) -> Path:
         if proc.returncode != 0:
             raise RuntimeError(f"hipcc failed for {src}:\n{proc.stderr}")
         objs.append(str(obj))
-    tmp = out_dir / (LIB_NAME + ".tmp")
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", str(tmp)]
+    # the host-checked twin: the C-ABI layer again, with WDRZ_DEBUG_CHECKS
+    capi_dbg = out_dir / "wdrz_capi.debug.o"
+    cmd = [hipcc(), *common, "-DWDRZ_DEBUG_CHECKS", "-c", str(CSRC / "wdrz_capi.cpp"), "-o", str(capi_dbg)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
-        raise RuntimeError(f"link failed:\n{proc.stderr}")
-    os.replace(tmp, LIB_PATH)
+        raise RuntimeError(f"hipcc failed for wdrz_capi.cpp (debug checks):\n{proc.stderr}")
+    objs_dbg = [str(capi_dbg) if o.endswith("wdrz_capi.cpp.o") else o for o in objs]
+    for target, parts in ((LIB_PATH, objs), (DEBUG_LIB_PATH, objs_dbg)):
+        tmp = out_dir / (target.name + ".tmp")
+        cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *parts, "-o", str(tmp)]
+        proc = subprocess.run(cmd, capture_output=True, text=True)
+        if proc.returncode != 0:
+            raise RuntimeError(f"link failed:\n{proc.stderr}")
+        os.replace(tmp, target)
     return LIB_PATH
 
 

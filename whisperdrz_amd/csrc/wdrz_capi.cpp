@@ -9,6 +9,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <string>
+#include <vector>
 
 #include "../../include/wdrz_attn.h"
 #include "wdrz_launch.h"
@@ -130,6 +131,44 @@ int dtw_qk_heads(int dtype, const void* const* q_heads, const int64_t* q_strides
   a->ks[1] = k_strides[1];
   return WDRZ_OK;
 }
+#ifdef WDRZ_DEBUG_CHECKS
+// Copies the slot ids and pre-append lengths of a cached-attention call to the host
+// (synchronously) and checks every row: slot in [0, n_slots), length >= 0, and with an append
+// length + sq <= Lmax. Append regions [cs, cs + sq) of rows naming the same slot must not
+// overlap; duplicate slot ids with identical regions (the padded rows of a bucketed decode
+// graph) are reported once on stderr but allowed, as the reference tolerates them.
+int debug_check_kv_metadata(const int32_t* seqlens, const int32_t* bidx, bool has_new, int64_t B, int64_t sq,
+                            int64_t n_slots, int64_t Lmax) {
+  std::vector<int32_t> hs(B, 0), hb(B);
+  for (int64_t i = 0; i < B; ++i) hb[i] = (int32_t)i;
+  if (bidx && hipMemcpy(hb.data(), bidx, B * sizeof(int32_t), hipMemcpyDeviceToHost) != hipSuccess)
+    return fail(WDRZ_ELAUNCH, "debug check: reading cache_batch_idx failed");
+  if (has_new && hipMemcpy(hs.data(), seqlens, B * sizeof(int32_t), hipMemcpyDeviceToHost) != hipSuccess)
+    return fail(WDRZ_ELAUNCH, "debug check: reading cache_seqlens failed");
+  for (int64_t i = 0; i < B; ++i) {
+    if (hb[i] < 0 || hb[i] >= n_slots)
+      return fail(WDRZ_EINVAL, "debug check: row %lld names slot %d outside [0, %lld)", (long long)i, hb[i],
+                  (long long)n_slots);
+    if (has_new && (hs[i] < 0 || hs[i] + sq > Lmax))
+      return fail(WDRZ_EINVAL, "debug check: row %lld appends [%d, %lld) outside the cache [0, %lld)", (long long)i,
+                  hs[i], (long long)(hs[i] + sq), (long long)Lmax);
+  }
+  if (has_new) {
+    bool dup = false;
+    for (int64_t i = 0; i < B; ++i)
+      for (int64_t j = i + 1; j < B; ++j) {
+        if (hb[i] != hb[j]) continue;
+        if (hs[i] != hs[j] && hs[i] < hs[j] + sq && hs[j] < hs[i] + sq)
+          return fail(WDRZ_EINVAL, "debug check: rows %lld and %lld append overlapping regions of slot %d",
+                      (long long)i, (long long)j, hb[i]);
+        dup = true;
+      }
+    if (dup) fprintf(stderr, "wdrz debug: duplicate cache_batch_idx entries (identical append regions)\n");
+  }
+  return WDRZ_OK;
+}
+#endif
+
 }  // namespace
 
 namespace wdrz {
@@ -266,6 +305,11 @@ int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, co
     if ((rc = check_strides("k", kn_strides, eb)) || (rc = check_strides("v", vn_strides, eb))) return rc;
   }
   if (B == 0) return WDRZ_OK;
+#ifdef WDRZ_DEBUG_CHECKS
+  // Debug build: check the device metadata on the host before launching (the release kernels
+  // turn a bad row into NaN output without touching memory outside the caches).
+  if ((rc = debug_check_kv_metadata(cache_seqlens, cache_batch_idx, has_new, B, sq, n_slots, Lmax))) return rc;
+#endif
 
   wdrz::KvArgs a{};
   a.q = static_cast<const char*>(q);
