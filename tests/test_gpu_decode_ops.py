@@ -5,7 +5,8 @@ reference's own torch ops on the same GPU tensors.
   one unit in the last place of the 16-bit result of torch's LayerNorm (both compute in fp32;
   the reduction order differs), with at least 99% of the elements bit-identical.
 * masked_argmax: token ids identical to the reference's sequence (zero, masked_fill -65504, add,
-  repetition-penalty where, argmax; decoding.py:1729-1761, 854-855), ties included.
+  repetition-penalty where, argmax; decoding.py:1729-1761, 854-855), ties and NaN logits included
+  (a NaN is the maximum, as in torch.argmax).
 """
 import pytest
 import torch
@@ -74,6 +75,11 @@ def test_masked_argmax(cuda, dtype):
     top = logits.float().argmax(dim=-1)
     penalty[torch.arange(0, rows, 3, device=cuda), top[0::3]] = True
     logits[9] = -logits[9].abs()
+    # NaN logits: torch.argmax takes a NaN as the maximum, so does the kernel
+    logits[11, 1234] = float("nan")
+    logits[12, 60] = float("nan")
+    logits[12, 50] = float("nan")
+    logits[13] = float("nan")
     print(f"masked_argmax {dtype}", flush=True)
     for b, p in [(blocked, penalty), (blocked, None), (None, penalty), (None, None)]:
         got = masked_argmax(logits, b, p)

@@ -131,6 +131,15 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(AddLnArgs a) {
 }
 
 // ---- masked greedy sampling --------------------------------------------------------------
+// argmax order of torch.argmax: NaN above every number (the first NaN wins), otherwise the
+// larger value, ties to the lower index.
+__device__ __forceinline__ bool argmax_beats(float v, int i, float b, int bi) {
+  const bool vn = v != v, bn = b != b;
+  if (vn != bn) return vn;
+  if (vn) return i < bi;
+  return v > b || (v == b && i < bi);
+}
+
 template <typename T>
 __global__ __launch_bounds__(256) void masked_argmax_kernel(ArgmaxArgs a) {
   const int row = blockIdx.x;
@@ -146,17 +155,17 @@ __global__ __launch_bounds__(256) void masked_argmax_kernel(ArgmaxArgs a) {
     float v = Elem<T>::load1(a.logits, base + i);
     v = Elem<T>::round(v + ((bm && bm[i]) ? neg : 0.f));  // logits + additive_mask
     if (pm && pm[i]) v = Elem<T>::round(v > 0.f ? v / 1.2f : v * 1.2f);
-    if (v > best || (v == best && i < best_i)) {
+    if (argmax_beats(v, i, best, best_i)) {
       best = v;
       best_i = i;
     }
   }
-  // workgroup argmax, lowest index among equal maxima
+  // workgroup argmax in the same order
 #pragma unroll
   for (int o = 32; o >= 1; o >>= 1) {
     const float ob = __shfl_xor(best, o);
     const int oi = __shfl_xor(best_i, o);
-    if (ob > best || (ob == best && oi < best_i)) {
+    if (argmax_beats(ob, oi, best, best_i)) {
       best = ob;
       best_i = oi;
     }
@@ -170,7 +179,7 @@ __global__ __launch_bounds__(256) void masked_argmax_kernel(ArgmaxArgs a) {
   __syncthreads();
   if (tid == 0) {
     for (int w = 1; w < 4; ++w)
-      if (sb[w] > best || (sb[w] == best && si[w] < best_i)) {
+      if (argmax_beats(sb[w], si[w], best, best_i)) {
         best = sb[w];
         best_i = si[w];
       }
