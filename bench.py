@@ -555,6 +555,25 @@ def bench_decode_step(dev, steps: int, warmup: int) -> dict:
         log(f"[bench] decode step ({'fused add+LayerNorm' if fused else 'torch add, LayerNorm'}): {ms:.3f} ms "
             f"per step, {Bs / ms * 1e3:.0f} tokens/s")
         del graphs
+    # the step's logits (model.py:609-613): [64, 1280] x [1280, 51866] against the tied embedding,
+    # a plain library GEMM (hipBLASLt), timed on its own: 32 launches in one graph
+    with torch.no_grad():
+        h = torch.randn((Bs, H * D), device=dev).to(torch.bfloat16)
+        w = dec.token_embedding.weight.to(torch.bfloat16)
+        logits = torch.empty((Bs, n_vocab), dtype=torch.bfloat16, device=dev)
+        torch.matmul(h, w.T, out=logits)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(N_LAYERS):
+                torch.matmul(h, w.T, out=logits)
+        g.replay()
+        ms_l = timed_events(g.replay, 10, torch.cuda.current_stream()) / N_LAYERS
+        del g
+    lbytes = n_vocab * H * D * 2 + Bs * H * D * 2 + Bs * n_vocab * 2
+    res["logits_us"] = ms_l * 1e3
+    res["logits_gbs"] = lbytes / (ms_l * 1e-3) / 1e9
+    log(f"[bench] decode step logits GEMM: {ms_l * 1e3:.1f} us, {res['logits_gbs']:.0f} GB/s "
+        f"({100 * res['logits_gbs'] / PEAK_HBM_GBS:.1f}% of HBM)")
     del dec, pool
     torch.cuda.empty_cache()
     return {
@@ -563,6 +582,13 @@ def bench_decode_step(dev, steps: int, warmup: int) -> dict:
         "ms_per_step": round(res["fused"], 4),
         "tokens_per_s": round(Bs / res["fused"] * 1e3, 1),
         "ms_per_step_unfused_small_ops": round(res["unfused"], 4),
+        "logits": {
+            "workload": "tied-embedding logits [64, 1280] x [1280, 51866] bf16 (model.py:609-613), hipBLASLt",
+            "us": round(res["logits_us"], 2),
+            "roofline": {"bound": "hbm", "achieved": round(res["logits_gbs"], 1), "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                         "frac": round(res["logits_gbs"] / PEAK_HBM_GBS, 4), "traffic": None,
+                         "bytes": n_vocab * H * D * 2 + Bs * H * D * 2 + Bs * n_vocab * 2},
+        },
     }
 
 

@@ -149,6 +149,23 @@ int wdrz_attn_kvcache_noalloc(int dtype, const void* q, void* k_cache, void* v_c
                               float softmax_scale, int causal, void* stream);
 
 /*
+ * The MLP input projection of the decode step with its activation: Y = act(X W^T + b).
+ *
+ * Replaces: the first two modules of ResidualAttentionBlock.mlp, Linear(n_state, 4 n_state)
+ *           and nn.GELU() (src/whisperdrz/model.py:388-391, applied at model.py:434): the
+ *           library GEMM with bias, its rounding to the 16-bit type, then the exact (erf) GELU
+ *           and its rounding, in one launch.
+ * x: [M, K] rows (stride x_stride), w: [N, K] rows (the Linear's weight, stride w_stride),
+ * bias: [N] or NULL, y: [M, N] rows (stride y_stride); 16-bit types, fp32 accumulation.
+ * activation: 0 none, 1 GELU (0.5 v (1 + erf(v / sqrt 2))). K % 128 == 0, N % 8 == 0,
+ * pointers and row strides 16-byte aligned. Sized for the decode step's few rows (M <= 64 per
+ * workgroup row block; any M works).
+ */
+int wdrz_linear(int dtype, const void* x, int64_t x_stride, const void* w, int64_t w_stride,
+                const void* bias, void* y, int64_t y_stride, int64_t M, int64_t N, int64_t K,
+                int activation, void* stream);
+
+/*
  * Residual add + LayerNorm of the decode step.
  *
  * Replaces: the residual add closing a sub-layer and the LayerNorm opening the next

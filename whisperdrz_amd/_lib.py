@@ -35,6 +35,7 @@ EXPORTED_SYMBOLS = (
     "wdrz_attn_kvcache_noalloc",
     "wdrz_add_layernorm",
     "wdrz_masked_argmax",
+    "wdrz_linear",
     "wdrz_log_mel_workspace_size",
     "wdrz_log_mel",
     "wdrz_dtw_qk",
@@ -86,6 +87,11 @@ def _declare(lib: ctypes.CDLL) -> None:
         ctypes.c_int, _p, _i64, _p, _i64,  # dtype, x, x stride, delta, delta stride
         _p, _p, _p, _i64, _i64, _i64,  # weight, bias, y, y stride, rows, n
         ctypes.c_float, _p,  # eps, stream
+    ]
+    lib.wdrz_linear.restype = ctypes.c_int
+    lib.wdrz_linear.argtypes = [
+        ctypes.c_int, _p, _i64, _p, _i64, _p,  # dtype, x, x stride, w, w stride, bias
+        _p, _i64, _i64, _i64, _i64, ctypes.c_int, _p,  # y, y stride, M, N, K, activation, stream
     ]
     lib.wdrz_masked_argmax.restype = ctypes.c_int
     lib.wdrz_masked_argmax.argtypes = [

@@ -439,6 +439,40 @@ int wdrz_masked_argmax(int dtype, const void* logits, int64_t logits_stride, con
   return WDRZ_OK;
 }
 
+int wdrz_linear(int dtype, const void* x, int64_t x_stride, const void* w, int64_t w_stride, const void* bias,
+                void* y, int64_t y_stride, int64_t M, int64_t N, int64_t K, int activation, void* stream) {
+  g_last_error.clear();
+  if (dtype != WDRZ_BF16 && dtype != WDRZ_F16)
+    return fail(dtype == WDRZ_F32 ? WDRZ_EUNSUPPORTED : WDRZ_EINVAL, "dtype %d: only WDRZ_BF16 / WDRZ_F16", dtype);
+  if (activation != 0 && activation != 1) return fail(WDRZ_EINVAL, "activation %d is not 0 (none) or 1 (GELU)", activation);
+  if (M < 0 || N <= 0 || K <= 0) return fail(WDRZ_EINVAL, "bad sizes M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  if (K % 128 != 0 || N % 8 != 0)
+    return fail(WDRZ_EUNSUPPORTED, "K=%lld must be a multiple of 128 and N=%lld of 8", (long long)K, (long long)N);
+  if (M > (1 << 24) || N > (1 << 24) || K > (1 << 20)) return fail(WDRZ_EUNSUPPORTED, "sizes too large");
+  if (M == 0) return WDRZ_OK;  // nothing to read or write (an empty tensor's pointer may be NULL)
+  int rc;
+  if ((rc = check_ptr("x", x)) || (rc = check_ptr("w", w)) || (rc = check_ptr("y", y))) return rc;
+  if (bias && (reinterpret_cast<uintptr_t>(bias) & 1)) return fail(WDRZ_EINVAL, "bias is not 2-byte aligned");
+  if (x_stride < K || w_stride < K || y_stride < N) return fail(WDRZ_EINVAL, "row strides shorter than the rows");
+  if ((x_stride * 2) % 16 || (w_stride * 2) % 16 || (y_stride * 2) % 16)
+    return fail(WDRZ_EINVAL, "row strides are not 16-byte aligned");
+  wdrz::LinearArgs a{};
+  a.x = x;
+  a.w = w;
+  a.bias = bias;
+  a.y = y;
+  a.x_stride = x_stride;
+  a.w_stride = w_stride;
+  a.y_stride = y_stride;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.act = activation;
+  hipError_t err = wdrz::launch_linear(dtype, a, reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(WDRZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  return WDRZ_OK;
+}
+
 int wdrz_kv_fill(int dtype, const void* k_src, const void* v_src, const int64_t* src_strides, void* k_cache,
                  void* v_cache, const int64_t* cache_strides, const int64_t* slot_indices, int64_t B, int64_t T,
                  int64_t H, int64_t D, int64_t n_slots, int64_t Lmax, int64_t start_pos, void* stream) {

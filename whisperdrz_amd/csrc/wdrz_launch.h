@@ -138,6 +138,18 @@ struct ArgmaxArgs {
 };
 hipError_t launch_masked_argmax(int dtype, const ArgmaxArgs& a, hipStream_t stream);
 
+// Y[M, N] = act(X[M, K] W[N, K]^T + b[N]) in 16-bit types (act 0: none, 1: GELU, erf form).
+// Strides in elements (rows); K % 128 == 0, N % 8 == 0, rows 16-byte aligned.
+struct LinearArgs {
+  const void* x;
+  const void* w;
+  const void* bias;  // nullptr: no bias
+  void* y;
+  int64_t x_stride, w_stride, y_stride;
+  int M, N, K, act;
+};
+hipError_t launch_linear(int dtype, const LinearArgs& a, hipStream_t stream);
+
 // Log-mel front end over fp32 waveforms [B, n_samples] (row stride audio_stride elements).
 struct LogMelArgs {
   const float* audio;

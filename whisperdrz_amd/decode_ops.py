@@ -5,6 +5,8 @@
   ``ln`` at ``model.py:609-613``), one launch instead of two.
 * :func:`masked_argmax` — ``decode_batch``'s greedy sampling tail (``decoding.py:1729-1761``):
   additive -65504 mask, repetition penalty, argmax, one launch instead of six.
+* :func:`linear_gelu` — the MLP's ``Linear(n_state, 4 n_state)`` + ``GELU`` (``model.py:388-391``,
+  applied at ``model.py:434``): GEMM, bias, rounding and exact GELU in one launch.
 
 There is no fallback: CPU tensors, fp32 LayerNorm inputs and a missing library raise.
 """
@@ -18,7 +20,7 @@ import torch.nn as nn
 from . import _lib
 from .attention import _check_cuda, _dtype_code, _raise, _stream_handle
 
-__all__ = ["add_layernorm_", "layer_norm", "masked_argmax"]
+__all__ = ["add_layernorm_", "layer_norm", "linear_gelu", "masked_argmax"]
 
 _LN16 = {torch.bfloat16: _lib.WDRZ_BF16, torch.float16: _lib.WDRZ_F16}
 
@@ -90,3 +92,30 @@ def masked_argmax(logits: torch.Tensor, blocked: Optional[torch.Tensor] = None,
     if rc != _lib.WDRZ_OK:
         _raise(rc, "masked_argmax")
     return out
+
+
+def linear_gelu(x: torch.Tensor, lin: nn.Linear, gelu: bool = True) -> torch.Tensor:
+    """``GELU(lin(x))`` (``gelu=False``: ``lin(x)``) for 16-bit ``x [..., K]``, rounded like the
+    reference's two modules: the Linear's output to the storage type, then the GELU's."""
+    _check_cuda("x", x, x.device)
+    if x.dtype not in _LN16:
+        raise TypeError(f"x: dtype {x.dtype} is not supported (bfloat16, float16)")
+    xr = _rows(x, "x")
+    w = lin.weight.detach()
+    b = lin.bias.detach() if lin.bias is not None else None
+    if w.dtype != x.dtype or (b is not None and b.dtype != x.dtype):
+        raise TypeError("the Linear's parameters must have the activations' dtype")
+    if w.stride(-1) != 1 or w.shape[1] != xr.shape[1]:
+        raise ValueError("weight must be [N, K] with contiguous rows and K = x.shape[-1]")
+    if b is not None and not b.is_contiguous():
+        b = b.contiguous()
+    N = int(w.shape[0])
+    y = torch.empty(xr.shape[0], N, dtype=x.dtype, device=x.device)
+    rc = _lib.load().wdrz_linear(
+        _LN16[x.dtype], xr.data_ptr(), xr.stride(0), w.data_ptr(), w.stride(0),
+        b.data_ptr() if b is not None else None, y.data_ptr(), y.stride(0),
+        xr.shape[0], N, xr.shape[1], 1 if gelu else 0, _stream_handle(),
+    )
+    if rc != _lib.WDRZ_OK:
+        _raise(rc, "linear_gelu")
+    return y.view(*x.shape[:-1], N)

@@ -34,7 +34,7 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from .attention import flash_attn_with_kvcache, scaled_dot_product_attention
-from .decode_ops import add_layernorm_, layer_norm
+from .decode_ops import add_layernorm_, layer_norm, linear_gelu
 from .kv_cache import FlashKVCache, KVSlotPool
 
 # Batch buckets of the captured decode step (reference transcriber.py:18).
@@ -242,7 +242,7 @@ class TextDecoderStack(nn.Module):
             h = add_layernorm_(x, d, block.cross_attn_ln)
             d = block.cross_attn.forward_flash_step(h, c_kv, True, None, batch_idx)
             h = add_layernorm_(x, d, block.mlp_ln)
-            d = block.mlp(h)
+            d = block.mlp[2](linear_gelu(h, block.mlp[0]))
             h = add_layernorm_(x, d, blocks[i + 1].attn_ln if i + 1 < len(blocks) else self.ln)
         return h
 
