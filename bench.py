@@ -38,6 +38,7 @@ if ROOT not in sys.path:
 METRIC = "enc-attn TFLOP/s + decode-attn HBM GB/s at large-v3 shape, % of MI355X roofline"
 # MI355X published peaks (dense, no sparsity).
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_FP32_TFLOPS = 157.3
 PEAK_HBM_GBS = 8000.0
 
 H, D = 20, 64
@@ -123,6 +124,44 @@ def bench_encoder(dev, steps: int, warmup: int) -> dict:
             "flop_per_launch": flop_layer,
             "ms_per_launch": ms_launch,
         },
+    }
+
+
+def bench_config1(dev, steps: int, warmup: int) -> dict:
+    """Config 1 (the reference's CPU-runnable case) on the GPU: one encoder layer, B=1 H=20
+    L=1500 D=64 in fp32, non-causal, scale 1/8. The fp32 path runs on the VALU (fp32 FMAs in
+    kv_attn_kernel), so its roofline is the fp32 peak; 8 seeded input sets in rotation."""
+    from whisperdrz_amd import scaled_dot_product_attention
+
+    B, L, n_sets = 1, 1500, 8
+    flop = 4.0 * B * H * L * L * D
+    sets = []
+    for i in range(n_sets):
+        g = torch.Generator(device=dev).manual_seed(1000 + i)
+        qkv = torch.randn((3, B, L, H, D), generator=g, device=dev, dtype=torch.float32)
+        sets.append(tuple(x.permute(0, 2, 1, 3) for x in qkv))
+
+    def run():
+        for q, k, v in sets:
+            scaled_dot_product_attention(q, k, v, scale=0.125)
+
+    stream = torch.cuda.current_stream()
+    for _ in range(warmup):
+        run()
+    us = timed_events(run, steps, stream) * 1e3 / n_sets
+    tflops = flop / (us * 1e-6) / 1e12
+    log(f"[bench] config1 fp32 dense (B=1 H=20 L=1500): {us:.1f} us per layer, {tflops:.2f} TFLOP/s "
+        f"({100 * tflops / PEAK_FP32_TFLOPS:.1f}% of the fp32 peak)")
+    del sets
+    torch.cuda.empty_cache()
+    return {
+        "workload": "config1: one encoder self-attention layer B=1 H=20 L=1500 D=64 fp32, non-causal, scale 1/8 "
+                    "(the shape of cpu_baseline), 8 seeded input sets in rotation",
+        "us_per_layer": round(us, 2),
+        "tflops": round(tflops, 3),
+        "roofline": {"bound": "valu", "achieved": round(tflops, 3), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(tflops / PEAK_FP32_TFLOPS, 4), "traffic": None,
+                     "kernel": "kv_attn_kernel<F32> (fp32 FMAs on the VALU, no fp32 MFMA)"},
     }
 
 
@@ -671,7 +710,6 @@ def bench_cross_fill(dev, steps: int, warmup: int) -> dict:
 # --------------------------------------------------------------------------------------------
 
 MEL_B, MEL_N, MEL_MELS = 16, 480000, 128
-PEAK_FP32_TFLOPS = 157.3
 
 
 def mel_flop(n_frames: int) -> float:
@@ -1055,6 +1093,7 @@ def main() -> int:
         return 0
 
     enc = bench_encoder(dev, args.steps, args.warmup) if args.only in (None, "enc") else None
+    c1 = bench_config1(dev, args.steps, args.warmup) if args.only in (None, "enc") else None
     dec = bench_decode(dev, args.steps, args.warmup) if args.only in (None, "dec") else None
     dtw = bench_dtw(dev, args.steps, args.warmup) if args.only in (None, "dtw") else None
     mel = bench_logmel(dev, args.steps, args.warmup) if args.only in (None, "mel") else None
@@ -1102,6 +1141,7 @@ def main() -> int:
         },
         "roofline": enc["roofline"] if enc else None,
         "cpu_baseline": cpu,
+        "config1_fp32": c1,
         "decode": dec,
         "dtw_prep": dtw,
         "log_mel": mel,

@@ -65,7 +65,8 @@ int wdrz_abi_version(void);
  * [B, H, L, D] order (the reference passes rearranged, non-contiguous views of the
  * [B, T, H*D] projection output, model.py:282-284, so strides are honoured).
  * causal != 0 applies torch's is_causal mask (top-left aligned: query i sees keys j <= i).
- * dtype: WDRZ_BF16 / WDRZ_F16 use the MFMA kernel; WDRZ_F32 uses an fp32 kernel.
+ * dtype: WDRZ_BF16 / WDRZ_F16 use the bf16 / fp16 MFMA kernels; WDRZ_F32 the fp32 MFMA kernel
+ *        (v_mfma_f32_32x32x2_f32, fp32 accumulation).
  */
 int wdrz_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* o, int64_t B,
                   int64_t H, int64_t Lq, int64_t Lk, int64_t D, const int64_t* q_strides,

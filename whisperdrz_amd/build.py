@@ -22,7 +22,7 @@ CSRC = PKG_DIR / "csrc"
 LIB_NAME = "libwdrz_attn.so"
 LIB_PATH = PKG_DIR / LIB_NAME
 DEBUG_LIB_PATH = PKG_DIR / "libwdrz_attn_debug.so"
-SOURCES = ["attn_kvcache.hip", "attn_dense.hip", "dtw_prep.hip", "dtw_qk.hip", "logmel.hip", "decode_ops.hip", "kv_fill.hip", "kv_noalloc.hip", "linear.hip", "wdrz_capi.cpp"]
+SOURCES = ["attn_kvcache.hip", "attn_dense.hip", "attn_dense_f32.hip", "dtw_prep.hip", "dtw_qk.hip", "logmel.hip", "decode_ops.hip", "kv_fill.hip", "kv_noalloc.hip", "linear.hip", "wdrz_capi.cpp"]
 ARCH = "gfx950"
 
 

@@ -4,8 +4,7 @@
 // src/whisperdrz/model.py:20-95) for:
 //   * cached self-attention with fused in-place append of k_new / v_new (model.py:49-63):
 //     query t of batch row b sees keys j <= cache_seqlens[b] + t (bottom-right causal);
-//   * cross-attention over the full cache (model.py:64-67), non-causal;
-// and also serves as the fp32 dense SDPA kernel (model.py:288-296, top-left causal flag).
+//   * cross-attention over the full cache (model.py:64-67), non-causal.
 //
 // The decode work is a GEMV per (b, h): every key row is touched once, so the kernel is HBM
 // bound and uses no MFMA. A head row of K or V is 64 elements = one 16-byte load per lane
@@ -245,13 +244,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
   const bool bad = slot < 0 || slot >= a.n_slots || cs < 0 || (HAS_NEW && cs + a.sq > a.Lk);
 
   // Keys this query block needs: [0, key_lim).
-  int key_lim;
-  if (HAS_NEW)
-    key_lim = cs + t0 + nq;
-  else if (a.causal)
-    key_lim = min(a.Lk, t0 + nq);
-  else
-    key_lim = a.Lk;
+  const int key_lim = HAS_NEW ? cs + t0 + nq : a.Lk;
   // Splits that hold keys of this row; the others have nothing to do.
   const int n_split_b = bad ? 1 : max(1, (key_lim + a.split_len - 1) / a.split_len);
   if (split >= n_split_b) return;
@@ -286,7 +279,6 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
   for (int t = 0; t < SQ; ++t) {
     lim[t] = k_end - 1;
     if (HAS_NEW) lim[t] = min(lim[t], cs + t0 + t);
-    else if (a.causal) lim[t] = min(lim[t], t0 + t);
   }
 
   const int safe_slot = bad ? 0 : slot;
@@ -539,13 +531,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
   static_assert(kMaxSQ * 2 * (kHeadDim * 2 / 16) <= kWaves * 64, "one append piece per thread");
   const AppendPiece app = HAS_NEW ? kv_append_load<T>(a, b, 0, nq, h) : AppendPiece{};
   const bool bad = slot < 0 || slot >= a.n_slots || cs < 0 || (HAS_NEW && cs + a.sq > a.Lk);
-  int key_lim;
-  if (HAS_NEW)
-    key_lim = cs + nq;
-  else if (a.causal)
-    key_lim = min(a.Lk, nq);
-  else
-    key_lim = a.Lk;
+  const int key_lim = HAS_NEW ? cs + nq : a.Lk;
   const int n_split_b = bad ? 1 : max(1, (key_lim + a.split_len - 1) / a.split_len);
   if (split >= n_split_b) return;
   const int k_begin = split * a.split_len;
@@ -553,7 +539,6 @@ __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
   // last key this lane's query may see (slots >= nq see none)
   int lim = k_end - 1;
   if (HAS_NEW) lim = min(lim, cs + qi);
-  else if (a.causal) lim = min(lim, qi);
   if (qi >= nq) lim = -1;
 
   // Q^T operand halves: query qi (clamped), dims 32*dh + 8*gq .. +7

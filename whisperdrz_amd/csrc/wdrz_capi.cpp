@@ -212,34 +212,7 @@ int wdrz_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* 
   const float c = scale * 1.4426950408889634f;
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   hipError_t err;
-  if (dtype == WDRZ_F32) {
-    // fp32: the split-KV kernel with the query axis blocked by 8 (dense view of the cache:
-    // "slot" = b, position = l, head = h).
-    wdrz::KvArgs a{};
-    a.q = static_cast<const char*>(q);
-    a.kc = static_cast<char*>(const_cast<void*>(k));
-    a.vc = static_cast<char*>(const_cast<void*>(v));
-    a.o = static_cast<char*>(o);
-    a.B = (int)B;
-    a.sq = (int)Lq;
-    a.H = (int)H;
-    a.Lk = (int)Lk;
-    a.n_slots = (int)B;
-    a.n_qblocks = (int)((Lq + 7) / 8);
-    a.causal = causal ? 1 : 0;
-    // [B, H, L, D] strides -> (batch, position, head) byte strides.
-    const int64_t* S[4] = {q_strides, k_strides, v_strides, o_strides};
-    int64_t* Dst[4] = {a.qs, a.kcs, a.vcs, a.os};
-    for (int i = 0; i < 4; ++i) {
-      Dst[i][0] = S[i][0] * eb;
-      Dst[i][1] = S[i][2] * eb;
-      Dst[i][2] = S[i][1] * eb;
-    }
-    a.c = c;
-    a.n_splits = 1;
-    a.split_len = (int)Lk;  // the query blocks already fill the GPU; no workspace needed
-    err = wdrz::launch_kv_attn(dtype, a, st);
-  } else {
+  {
     wdrz::DenseArgs a{};
     a.q = q;
     a.k = k;
@@ -255,7 +228,8 @@ int wdrz_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* 
     for (int i = 0; i < 4; ++i)
       for (int j = 0; j < 3; ++j) Dst[i][j] = S[i][j];
     a.c = c;
-    err = wdrz::launch_dense_mfma(dtype, a, st);
+    // fp32 on the fp32 matrix cores, 16-bit types on the bf16 / fp16 ones
+    err = dtype == WDRZ_F32 ? wdrz::launch_dense_f32(a, st) : wdrz::launch_dense_mfma(dtype, a, st);
   }
   if (err != hipSuccess) return fail(WDRZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
   return WDRZ_OK;
@@ -326,7 +300,6 @@ int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, co
   a.Lk = (int)Lmax;
   a.n_slots = (int)n_slots;
   a.n_qblocks = (int)((sq + 7) / 8);
-  a.causal = 0;
   const int64_t* S[4] = {q_strides, kc_strides, vc_strides, o_strides};
   int64_t* Dst[4] = {a.qs, a.kcs, a.vcs, a.os};
   for (int i = 0; i < 4; ++i)

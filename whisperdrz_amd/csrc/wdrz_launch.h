@@ -23,7 +23,6 @@ struct KvArgs {
   float* ws_part;  // split partials (split mode with n_splits > 1)
   int* ws_count;   // per-row arrival counters, zero between calls
   int B, sq, H, Lk, n_slots, n_qblocks, n_splits, split_len;
-  int causal;  // top-left causal mask (dense path only; the append path is always causal)
   int64_t qs[3], kcs[3], vcs[3], kns[3], vns[3], os[3];
   float c;  // softmax scale * log2(e)
 };
@@ -50,6 +49,8 @@ struct DenseArgs {
   float c;                             // softmax scale * log2(e)
 };
 hipError_t launch_dense_mfma(int dtype, const DenseArgs& a, hipStream_t stream);
+// The same on the fp32 matrix cores (fp32 inputs and output; causal = top-left).
+hipError_t launch_dense_f32(const DenseArgs& a, hipStream_t stream);
 
 // DTW alignment prep over fp32 scores W [B, H, T, A] (strides in ELEMENTS, last one 1).
 constexpr int kDtwMaxRows = 512;  // T limit (Whisper's text context is 448)
