@@ -16,10 +16,12 @@
 //     8j + 4h + r of S^T, so at instruction kk = i both operands use that key in K slot h: P is
 //     the accumulator itself (no shuffles) and V^T is one 4-byte LDS read of row 8j + 4h + r.
 // At 64 MFMAs of 64 cycles per step against ~150 VALU instructions of softmax, the kernel is
-// bound by the fp32 matrix rate. One 256-thread workgroup (four 32-query wavefronts) shares
-// 32-key K and V tiles staged through registers into three LDS buffers (two steps ahead), one
-// barrier per step; each step issues the next step's S^T before its own softmax, so the matrix
-// pipe stays busy while the VALU works, and the output is rescaled only when a row max grows.
+// bound by the fp32 matrix rate. A 512-thread workgroup holds four 32-query groups, each served
+// by two wavefronts on the same SIMD that take alternate 32-key steps (so every SIMD has two
+// wavefronts to cover each other's stalls) and merge their (m, l, O) through LDS at the end.
+// 64-key K and V stages go through registers into three LDS buffers (two stages ahead), one
+// barrier per stage; each wavefront issues its next step's S^T before its own softmax, and the
+// output is rescaled only when a row max grows.
 #include <hip/hip_runtime.h>
 #include <math.h>
 #include <stdint.h>
@@ -30,10 +32,12 @@
 namespace wdrz {
 namespace {
 
-constexpr int kF32Waves = 4;
+constexpr int kF32Groups = 4;                 // 32-query groups per workgroup
+constexpr int kF32Waves = 2 * kF32Groups;     // two key halves per group
 constexpr int kF32Threads = kF32Waves * 64;
-constexpr int kF32BM = 32 * kF32Waves;  // queries per workgroup
-constexpr int kF32BS = 32;              // keys per step
+constexpr int kF32BM = 32 * kF32Groups;  // queries per workgroup
+constexpr int kF32BS = 32;               // keys per step (one wavefront)
+constexpr int kF32Stage = 2 * kF32BS;    // keys per LDS stage (both halves)
 constexpr int kF32Pitch = kHeadDim + 4;  // LDS row pitch in floats (16-byte pad: conflict-free b128 reads)
 
 __device__ __forceinline__ f32x16 mfma_f32(float a, float b, const f32x16& c) {
@@ -42,12 +46,14 @@ __device__ __forceinline__ f32x16 mfma_f32(float a, float b, const f32x16& c) {
 
 template <bool CAUSAL>
 __global__ __launch_bounds__(kF32Threads) void dense_f32_kernel(DenseArgs a) {
-  __shared__ __attribute__((aligned(16))) float sK[3][kF32BS * kF32Pitch];
-  __shared__ __attribute__((aligned(16))) float sV[3][kF32BS * kF32Pitch];
+  __shared__ __attribute__((aligned(16))) float sK[3][kF32Stage * kF32Pitch];
+  __shared__ __attribute__((aligned(16))) float sV[3][kF32Stage * kF32Pitch];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int qg = wave % kF32Groups;  // query group
+  const int kh = wave / kF32Groups;  // key half: steps 2u + kh of each 64-key stage u
   const int hl = lane >> 5;
   const int l32 = lane & 31;
 
@@ -62,13 +68,13 @@ __global__ __launch_bounds__(kF32Threads) void dense_f32_kernel(DenseArgs a) {
   const float* V = static_cast<const float*>(a.v) + b * a.vs[0] + h * a.vs[1];
   float* O = static_cast<float*>(a.o) + b * a.os[0] + h * a.os[1];
   const int q_blk0 = qblk * kF32BM;
-  const int q_wave0 = q_blk0 + wave * 32;
+  const int q_wave0 = q_blk0 + qg * 32;
   const int q_me = q_wave0 + l32;  // this lane's query (may be >= Lq: computed, not stored)
 
   // Keys the workgroup and this wavefront need (top-left causal: query i sees keys 0..i).
   const int k_lim = CAUSAL ? min(a.Lk, q_blk0 + kF32BM) : a.Lk;
   const int k_lim_w = CAUSAL ? min(a.Lk, q_wave0 + 32) : a.Lk;
-  const int n_steps = (k_lim + kF32BS - 1) / kF32BS;
+  const int n_units = (k_lim + kF32Stage - 1) / kF32Stage;
 
   // Q: 32 floats (head dims 32h .. 32h + 31) of this lane's query, pre-scaled by c.
   float qreg[32];
@@ -82,13 +88,13 @@ __global__ __launch_bounds__(kF32Threads) void dense_f32_kernel(DenseArgs a) {
     }
   }
 
-  // Tile staging: thread t moves 16-byte pieces t and t + 256 of the 32 x 64 K and V tiles.
+  // Tile staging: thread t moves 16-byte pieces t and t + 512 of the 64 x 64 K and V tiles.
   u32x4 rk[2], rv[2];
   auto gload = [&](int st) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int piece = tid + i * kF32Threads;
-      const int key = min(st * kF32BS + (piece >> 4), a.Lk - 1);
+      const int key = min(st * kF32Stage + (piece >> 4), a.Lk - 1);
       const int col = (piece & 15) * 4;
       rk[i] = load16(K + (int64_t)key * a.ks[2] + col);
       rv[i] = load16(V + (int64_t)key * a.vs[2] + col);
@@ -114,7 +120,7 @@ __global__ __launch_bounds__(kF32Threads) void dense_f32_kernel(DenseArgs a) {
     f32x16 sa, sb;
 #pragma unroll
     for (int x = 0; x < 16; ++x) sa[x] = sb[x] = 0.f;
-    const float* kr = &sK[buf][l32 * kF32Pitch + 32 * hl];
+    const float* kr = &sK[buf][(kh * kF32BS + l32) * kF32Pitch + 32 * hl];
 #pragma unroll
     for (int kq = 0; kq < 8; ++kq) {
       const f32x4 kv = *reinterpret_cast<const f32x4*>(kr + 4 * kq);
@@ -161,7 +167,7 @@ __global__ __launch_bounds__(kF32Threads) void dense_f32_kernel(DenseArgs a) {
   };
   // O^T += V^T P^T: instruction i uses key 8(i>>2) + 4h + (i&3) in K slot h
   auto pv = [&](int buf, const f32x16& p) __attribute__((always_inline)) {
-    const float* vr = &sV[buf][4 * hl * kF32Pitch + l32];
+    const float* vr = &sV[buf][(kh * kF32BS + 4 * hl) * kF32Pitch + l32];
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const float* row = vr + (8 * (i >> 2) + (i & 3)) * kF32Pitch;
@@ -170,44 +176,61 @@ __global__ __launch_bounds__(kF32Threads) void dense_f32_kernel(DenseArgs a) {
     }
   };
 
-  // Tiles are staged two steps ahead into three buffers: at the top of step s, tiles s and s+1
-  // are visible, so S(s+1) is issued before the softmax of step s and the matrix pipe has work
-  // while the softmax runs.
+  // Stages of 64 keys (the two halves' steps) go two stages ahead into three buffers: at the top
+  // of stage u, stages u and u+1 are visible, so S of the wavefront's step in stage u+1 is
+  // issued before its softmax of stage u and the matrix pipe has work while the softmax runs.
   gload(0);
   lstore(0);
-  if (n_steps > 1) {
+  if (n_units > 1) {
     gload(1);
     lstore(1);
   }
-  if (n_steps > 2) gload(2);
+  if (n_units > 2) gload(2);
   __syncthreads();
+  auto live = [&](int u) { return (2 * u + kh) * kF32BS < k_lim_w; };  // causal: keys end earlier
   f32x16 s_cur, s_nxt;
-  scores(0, s_cur);
-  auto step = [&](int st, f32x16& cur, f32x16& nxt) __attribute__((always_inline)) {
-    const bool live = st * kF32BS < k_lim_w;  // causal: this wavefront's keys end earlier
-    if (live) {
-      if (st + 1 < n_steps && (st + 1) * kF32BS < k_lim_w) scores((st + 1) % 3, nxt);
-      softmax(st, cur);
-      pv(st % 3, cur);
+  if (live(0)) scores(0, s_cur);
+  auto unit = [&](int u, f32x16& cur, f32x16& nxt) __attribute__((always_inline)) {
+    if (live(u)) {
+      if (u + 1 < n_units && live(u + 1)) scores((u + 1) % 3, nxt);
+      softmax(2 * u + kh, cur);
+      pv(u % 3, cur);
     }
-    // Buffer (st+2)%3 last held tile st-1, whose reads (K in step st-2, V in step st-1) came
+    // Buffer (u+2)%3 last held stage u-1, whose reads (K in stage u-2, V in stage u-1) came
     // before the previous barrier.
-    if (st + 2 < n_steps) {
-      lstore((st + 2) % 3);
-      if (st + 3 < n_steps) gload(st + 3);
+    if (u + 2 < n_units) {
+      lstore((u + 2) % 3);
+      if (u + 3 < n_units) gload(u + 3);
     }
     __syncthreads();
   };
-  int st = 0;
-  for (; st + 1 < n_steps; st += 2) {
-    step(st, s_cur, s_nxt);
-    step(st + 1, s_nxt, s_cur);
+  int u = 0;
+  for (; u + 1 < n_units; u += 2) {
+    unit(u, s_cur, s_nxt);
+    unit(u + 1, s_nxt, s_cur);
   }
-  if (st < n_steps) step(st, s_cur, s_nxt);
+  if (u < n_units) unit(u, s_cur, s_nxt);
 
-  // ---- normalise and store: lane holds dims 32 db + 8j + 4h + r (r = 0..3) of its query ----
-  if (q_me >= a.Lq) return;
-  const float inv = 1.f / (l_run + __shfl_xor(l_run, 32));
+  // ---- merge the two key halves of each query group through LDS (the tile area is free: the
+  // last stage ended with a barrier), then normalise and store ----
+  float* mg = &sK[0][0] + qg * (34 * 64);  // [34][64]: acc_o (32), m, l per lane
+  if (kh == 1) {
+#pragma unroll
+    for (int x = 0; x < 16; ++x) {
+      mg[x * 64 + lane] = acc_o[0][x];
+      mg[(16 + x) * 64 + lane] = acc_o[1][x];
+    }
+    mg[32 * 64 + lane] = m_run;
+    mg[33 * 64 + lane] = l_run;
+  }
+  __syncthreads();
+  if (kh == 1 || q_me >= a.Lq) return;
+  const float m1 = mg[32 * 64 + lane];
+  const float m = fmaxf(m_run, m1);  // finite: half 0 always sees key 0
+  const float a0 = fast_exp2(m_run - m), a1 = fast_exp2(m1 - m);
+  const float l_me = l_run * a0 + mg[33 * 64 + lane] * a1;
+  const float inv = 1.f / (l_me + __shfl_xor(l_me, 32));
+  // lane holds dims 32 db + 8j + 4h + r (r = 0..3) of its query
   float* orow = O + (int64_t)q_me * a.os[2];
 #pragma unroll
   for (int db = 0; db < 2; ++db)
@@ -215,7 +238,10 @@ __global__ __launch_bounds__(kF32Threads) void dense_f32_kernel(DenseArgs a) {
     for (int j = 0; j < 4; ++j) {
       f32x4 w;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) w[r] = acc_o[db][4 * j + r] * inv;
+      for (int r = 0; r < 4; ++r) {
+        const int x = 4 * j + r;
+        w[r] = (acc_o[db][x] * a0 + mg[(16 * db + x) * 64 + lane] * a1) * inv;
+      }
       store16(orow + 32 * db + 8 * j + 4 * hl, __builtin_bit_cast(u32x4, w));
     }
 }
