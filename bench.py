@@ -109,9 +109,30 @@ def bench_encoder(dev, steps: int, warmup: int) -> dict:
     log(f"[bench] encoder: {ms_step:.3f} ms/step, {tflops:.1f} TFLOP/s ({100 * tflops / PEAK_BF16_TFLOPS:.1f}% of bf16 peak)")
     del layers, outs
     torch.cuda.empty_cache()
+
+    # one 30-s window (B=1): a grid smaller than the chip, served by the key-split kernel
+    single = []
+    for i in range(8):
+        g = torch.Generator(device=dev).manual_seed(2500 + i)
+        qkv = torch.randn((3, 1, L, H, D), generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+        single.append(tuple(x.permute(0, 2, 1, 3) for x in qkv))
+
+    def step1():
+        for q, k, v in single:
+            scaled_dot_product_attention(q, k, v, scale=0.125)
+
+    for _ in range(warmup):
+        step1()
+    us1 = timed_events(step1, steps, stream) * 1e3 / len(single)
+    t1 = 4.0 * H * L * L * D / (us1 * 1e-6) / 1e12
+    log(f"[bench] encoder, one window (B=1): {us1:.1f} us per layer, {t1:.1f} TFLOP/s")
+    del single
+    torch.cuda.empty_cache()
     return {
         "ms_per_step": ms_step,
         "tflops": tflops,
+        "single_window": {"workload": "one encoder layer B=1 H=20 L=1500 D=64 bf16 (dense_split_kernel<Bf16, 1>)",
+                          "us_per_layer": round(us1, 2), "tflops": round(t1, 1)},
         "roofline": {
             "bound": "mfma",
             "achieved": round(achieved, 2),
@@ -1140,6 +1161,7 @@ def main() -> int:
             "parallelism": "single GPU",
         },
         "roofline": enc["roofline"] if enc else None,
+        "encoder_single_window": enc["single_window"] if enc else None,
         "cpu_baseline": cpu,
         "config1_fp32": c1,
         "decode": dec,

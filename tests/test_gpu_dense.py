@@ -55,6 +55,24 @@ def test_dense_parity(cuda, dtype, B, H, Lq, Lk, causal):
     assert_close(out, ref, dtype, "dense")
 
 
+# Non-causal 16-bit launches pick a kernel by grid size (one workgroup per CU): the key-split
+# kernel with 128-query blocks when B*H*ceil(Lq/128) <= 256 (every SHAPES entry above), with
+# 256-query blocks when B*H*ceil(Lq/256) <= 256, else the 512-query kernel. One shape per route:
+ROUTES = [
+    (1, 40, 1024, 300),  # 320 blocks of 128 > 256, 160 of 256: key split, 256-query blocks
+    (4, 20, 800, 333),   # 320 blocks of 256 > 256: the 512-query kernel
+    (1, 20, 1500, 1500),  # 240 blocks of 128: key split, 128-query blocks (a single window)
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("B,H,Lq,Lk", ROUTES)
+def test_dense_routes(cuda, dtype, B, H, Lq, Lk):
+    print(f"dense route dtype={dtype} B={B} H={H} Lq={Lq} Lk={Lk}", flush=True)
+    out, ref = _run(cuda, dtype, B, H, Lq, Lk, False, seed=77 + Lq)
+    assert_close(out, ref, dtype, "dense route")
+
+
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
 def test_dense_contiguous_bhld(cuda, dtype):
     out, ref = _run(cuda, dtype, 2, 2, 129, 77, False, seed=7, layout="bhld")

@@ -5,13 +5,15 @@
 // top-left causal). O = softmax(scale * Q K^T) V per (b, h), with an online softmax in the
 // log2 domain.
 //
-// Two kernels share the arithmetic below:
+// Three kernels share the arithmetic below:
 //   * dense_fwd_kernel (non-causal; the encoder): 512-thread workgroups of eight 64-query
 //     wavefronts (two per SIMD), K/V tiles of 64 keys in four LDS buffers, Q and O moved
 //     through LDS as whole rows. Its own comment block gives the details.
 //   * dense_mfma_kernel (causal): eight 32-query wavefronts per workgroup (~120 VGPRs, four
 //     wavefronts per SIMD), three LDS buffers with V transposed at staging time, and the
 //     causal diagonal handled per wavefront (keys past a wavefront's last query are skipped).
+//   * dense_split_kernel (non-causal, grids smaller than the chip): the same tile staging, with
+//     each query group's keys split over two wavefronts that merge at the end.
 // Each 64-key tile is consumed as two 32-key sub-steps.
 //
 // Transposed products. A wavefront computes S^T = K Q^T with v_mfma_f32_32x32x16 (A = K from
@@ -53,6 +55,7 @@ constexpr int kBN = 64;               // key rows per LDS tile
 constexpr int kBS = 32;               // key rows per sub-step
 constexpr int kPitchK = kHeadDim + 8; // K tile row pitch in elements (16-byte pad)
 constexpr int kNumBuf = 3;            // LDS tile buffers
+constexpr int kNumCus = 256;          // compute units of an MI355X
 constexpr float kTau = 8.0f;          // lazy-rescale threshold (log2 units), causal kernel
 constexpr float kSumLimit = 1024.0f;  // per-step row-sum limit of the non-causal kernel
 
@@ -662,6 +665,260 @@ __global__ __launch_bounds__(kFThreads, 1) void dense_fwd_kernel(DenseArgs a) {
   }
 }
 
+// ============================================================================================
+// Key-split kernel (non-causal, small grids): a workgroup holds four query groups of 32*QB
+// queries; each group is served by two wavefronts on the same SIMD (waves g and g+4), one per
+// 32-key half of every 64-key tile, which merge their (m, l, O) through LDS at the end. Per query
+// this is half the keys per wavefront of the other kernels, so a launch that would leave CUs idle
+// or run a short last round (the DTW decoder's 448 x 1500 cross-attention, single-window
+// encoder calls) gets two to four times as many workgroups of half the length.
+// ============================================================================================
+template <typename T, int QB>
+__global__ __launch_bounds__(512) void dense_split_kernel(DenseArgs a) {
+  constexpr int NW = 8, NG = 4;
+  constexpr int kThreads = NW * 64;
+  constexpr int kBM = 32 * QB * NG;  // query rows per workgroup
+  typedef typename Mfma<T>::op_t op_t;
+  typedef uint16_t e_t;
+  __shared__ __attribute__((aligned(16))) e_t sK[kNumBuf][kBN * kPitchK];
+  __shared__ __attribute__((aligned(16))) e_t sVt[kNumBuf][kHeadDim * kBN];
+  constexpr int kPart = 32 * QB + 2 * QB;  // floats per lane of a partial: O (2 x QB x 16), m, l
+  __shared__ float smerge[NG][kPart][64];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int grp = wave % NG;
+  const int kh = wave / NG;  // 32-key half of each tile
+  const int hl = lane >> 5;
+  const int l32 = lane & 31;
+
+  const int n_qblk = (a.Lq + kBM - 1) / kBM;
+  const int tile_id = remap_xcd(blockIdx.x, gridDim.x);
+  const int qblk = tile_id % n_qblk;
+  const int bh = tile_id / n_qblk;
+  const int b = bh / a.H, h = bh % a.H;
+
+  const e_t* Q = reinterpret_cast<const e_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
+  const e_t* K = reinterpret_cast<const e_t*>(a.k) + b * a.ks[0] + h * a.ks[1];
+  const e_t* V = reinterpret_cast<const e_t*>(a.v) + b * a.vs[0] + h * a.vs[1];
+  e_t* O = reinterpret_cast<e_t*>(a.o) + b * a.os[0] + h * a.os[1];
+
+  const int q_wave = qblk * kBM + grp * 32 * QB;
+  const float c = a.c;
+
+  op_t qreg[QB][4];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const int qi = min(q_wave + qb * 32 + l32, a.Lq - 1);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const u32x4 raw = load16(Q + qi * a.qs[2] + ks * 16 + hl * 8);
+      u32x4 sc;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        sc[e] = Mfma<T>::pack(Mfma<T>::widen_lo(raw[e]) * c, Mfma<T>::widen_hi(raw[e]) * c);
+      asm volatile("" : "+v"(sc));
+      qreg[qb][ks] = __builtin_bit_cast(op_t, sc);
+    }
+  }
+
+  const int n_tiles = (a.Lk + kBN - 1) / kBN;
+
+  // Tile staging, as in dense_mfma_kernel with eight wavefronts.
+  constexpr int kKPerThr = (kBN * kHeadDim / 8) / kThreads;
+  constexpr int kVDims = (kBN / 2) * kHeadDim / kThreads;
+  static_assert(kKPerThr == 1 && kVDims == 4, "tile staging shape");
+  u32x4 pk;
+  u32x2 pv[2];
+  const int vkp = tid / (kHeadDim / kVDims);
+  const int vd0 = (tid % (kHeadDim / kVDims)) * kVDims;
+  auto gload = [&](int kt) __attribute__((always_inline)) {
+    const int key = min(kt * kBN + (tid >> 3), a.Lk - 1);
+    pk = load16(K + key * a.ks[2] + (tid & 7) * 8);
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int kv = min(kt * kBN + 2 * vkp + i, a.Lk - 1);
+      pv[i] = *reinterpret_cast<const u32x2*>(V + kv * a.vs[2] + vd0);
+    }
+  };
+  auto lstore = [&](int buf) __attribute__((always_inline)) {
+    *reinterpret_cast<u32x4*>(&sK[buf][(tid >> 3) * kPitchK + (tid & 7) * 8]) = pk;
+#pragma unroll
+    for (int e = 0; e < kVDims / 2; ++e) {
+      const uint32_t lo0 = pv[0][e] & 0xffffu, hi0 = pv[0][e] >> 16;
+      const uint32_t lo1 = pv[1][e] & 0xffffu, hi1 = pv[1][e] >> 16;
+      *reinterpret_cast<uint32_t*>(&sVt[buf][vt_index(vd0 + 2 * e, 2 * vkp)]) = lo0 | (lo1 << 16);
+      *reinterpret_cast<uint32_t*>(&sVt[buf][vt_index(vd0 + 2 * e + 1, 2 * vkp)]) = hi0 | (hi1 << 16);
+    }
+  };
+
+  const int pm = l32;
+  const int pi_row = 16 * ((pm >> 3) >> 1) + 8 * ((pm >> 2) & 1) + 4 * ((pm >> 3) & 1) + (pm & 3);
+
+  f32x16 acc_o[2][QB];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < QB; ++j)
+#pragma unroll
+      for (int x = 0; x < 16; ++x) acc_o[i][j][x] = 0.f;
+  float m_run[QB], l_part[QB][4];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    m_run[qb] = 0.f;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) l_part[qb][j] = 0.f;
+  }
+  op_t pprev[QB][2];
+  bool seen = false;  // this wavefront has processed at least one key
+
+  gload(0);
+  lstore(0);
+  __syncthreads();
+
+  // Step t: S of this wavefront's half of tile t, PV of its half of tile t-1.
+  for (int t = 0; t <= n_tiles; ++t) {
+    const int buf = t % kNumBuf;
+    if (t + 1 < n_tiles) gload(t + 1);
+    const bool do_s = t < n_tiles && (2 * t + kh) * kBS < a.Lk;
+    const bool do_pv = t >= 1 && (2 * (t - 1) + kh) * kBS < a.Lk;
+    f32x16 sacc[QB];
+    mfma_priority<1>();
+    if (do_s) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const op_t ka = __builtin_bit_cast(
+            op_t, *reinterpret_cast<const u32x4*>(&sK[buf][(kh * 32 + pi_row) * kPitchK + ks * 16 + hl * 8]));
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) sacc[qb] = Mfma<T>::run(ka, qreg[qb][ks], ks == 0 ? f32x16{} : sacc[qb]);
+      }
+    }
+    if (do_pv) {
+      const int bufp = (t - 1) % kNumBuf;
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch) {
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          const op_t va = __builtin_bit_cast(
+              op_t, *reinterpret_cast<const u32x4*>(&sVt[bufp][vt_index(db * 32 + l32, kh * 32 + ch * 16 + hl * 8)]));
+#pragma unroll
+          for (int qb = 0; qb < QB; ++qb) acc_o[db][qb] = Mfma<T>::run(va, pprev[qb][ch], acc_o[db][qb]);
+        }
+      }
+    }
+    mfma_priority<0>();
+    if (do_s) {
+      const int k0 = (2 * t + kh) * kBS;
+      if (k0 + kBS > a.Lk) {
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb)
+#pragma unroll
+          for (int x = 0; x < 16; ++x)
+            if (k0 + 16 * (x >> 3) + 8 * hl + (x & 7) >= a.Lk) sacc[qb][x] = -INFINITY;
+      }
+      float mx[QB];
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+        float m4[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          m4[j] = fmaxf(fmaxf(sacc[qb][4 * j], sacc[qb][4 * j + 1]), fmaxf(sacc[qb][4 * j + 2], sacc[qb][4 * j + 3]));
+        mx[qb] = half_swap_max(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]))) - m_run[qb];
+      }
+      const bool first = !seen;
+      bool any_big = first;
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) any_big = any_big || mx[qb] > kTau;
+      if (__any(any_big)) {
+        asm volatile("" ::: "memory");
+#pragma unroll
+        for (int qb = 0; qb < QB; ++qb) {
+          const float delta = first ? mx[qb] : fmaxf(mx[qb], 0.f);
+          m_run[qb] += delta;
+          if (!first) {
+            const float alpha = fast_exp2(-delta);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) l_part[qb][j] *= alpha;
+#pragma unroll
+            for (int db = 0; db < 2; ++db)
+#pragma unroll
+              for (int x = 0; x < 16; ++x) acc_o[db][qb][x] *= alpha;
+          }
+        }
+      }
+      seen = true;
+#pragma unroll
+      for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch) {
+          u32x4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float p0 = fast_exp2(sacc[qb][ch * 8 + 2 * e] - m_run[qb]);
+            const float p1 = fast_exp2(sacc[qb][ch * 8 + 2 * e + 1] - m_run[qb]);
+            w[e] = Mfma<T>::pack(p0, p1);
+            l_part[qb][e] = l_part[qb][e] + p0 + p1;
+          }
+          pprev[qb][ch] = __builtin_bit_cast(op_t, w);
+        }
+      }
+    }
+    // Buffer (t+1)%3 last held tile t-2, read by S in step t-2 and PV in step t-1, both before
+    // the previous barrier.
+    if (t + 1 < n_tiles) {
+      lstore((t + 1) % kNumBuf);
+      __syncthreads();
+    }
+  }
+
+  // ---- merge the two halves of each group, normalise, store ----
+  float lsum[QB];
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) lsum[qb] = (l_part[qb][0] + l_part[qb][1]) + (l_part[qb][2] + l_part[qb][3]);
+  if (kh == 1) {
+#pragma unroll
+    for (int qb = 0; qb < QB; ++qb) {
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int x = 0; x < 16; ++x) smerge[grp][(qb * 2 + db) * 16 + x][lane] = acc_o[db][qb][x];
+      smerge[grp][32 * QB + qb][lane] = seen ? m_run[qb] : -INFINITY;
+      smerge[grp][33 * QB + qb][lane] = lsum[qb];
+    }
+  }
+  __syncthreads();
+  if (kh == 1) return;
+#pragma unroll
+  for (int qb = 0; qb < QB; ++qb) {
+    const float m1 = smerge[grp][32 * QB + qb][lane];
+    const float m = fmaxf(m_run[qb], m1);  // half 0 always sees key 0
+    const float a0 = fast_exp2(m_run[qb] - m), a1 = fast_exp2(m1 - m);
+    const float lq = lsum[qb] * a0 + smerge[grp][33 * QB + qb][lane] * a1;
+    const float inv = 1.f / (lq + __shfl_xor(lq, 32));
+    const int qi = q_wave + qb * 32 + l32;
+    if (qi < a.Lq) {
+      e_t* orow = O + qi * a.os[2];
+#pragma unroll
+      for (int db = 0; db < 2; ++db)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int d = db * 32 + i * 8 + hl * 4;
+          float v[4];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int x = i * 4 + r;
+            v[r] = (acc_o[db][qb][x] * a0 + smerge[grp][(qb * 2 + db) * 16 + x][lane] * a1) * inv;
+          }
+          u32x2 w;
+          w[0] = Mfma<T>::pack(v[0], v[1]);
+          w[1] = Mfma<T>::pack(v[2], v[3]);
+          *reinterpret_cast<u32x2*>(orow + d) = w;
+        }
+    }
+  }
+}
+
 // Causal / generic kernel shape: 32-query wavefronts, 8 per workgroup.
 constexpr int kQB = 1;
 constexpr int kNW = 8;
@@ -669,11 +926,20 @@ constexpr int kNW = 8;
 template <typename T>
 hipError_t launch_typed(const DenseArgs& a, hipStream_t stream) {
   if (!a.causal) {
-    const int n_qblk = (a.Lq + kFBM - 1) / kFBM;
-    const int64_t n = (int64_t)a.B * a.H * n_qblk;
+    // One workgroup per CU is what each kernel is shaped for. Small grids (a single window, the
+    // DTW decoder at B=1) take the key-split kernel with the largest query block that still
+    // yields no more workgroups than CUs; the rest the 512-query kernel.
+    const int64_t bh = (int64_t)a.B * a.H;
+    const int64_t n_split1 = bh * ((a.Lq + 127) / 128), n_split2 = bh * ((a.Lq + 255) / 256);
+    const int64_t n = bh * ((a.Lq + kFBM - 1) / kFBM);
     if (n <= 0) return hipSuccess;
     if (n > 0x7fffffff) return hipErrorInvalidValue;
-    hipLaunchKernelGGL((dense_fwd_kernel<T>), dim3((unsigned)n), dim3(kFThreads), 0, stream, a);
+    if (n_split1 <= kNumCus)
+      hipLaunchKernelGGL((dense_split_kernel<T, 1>), dim3((unsigned)n_split1), dim3(512), 0, stream, a);
+    else if (n_split2 <= kNumCus)
+      hipLaunchKernelGGL((dense_split_kernel<T, 2>), dim3((unsigned)n_split2), dim3(512), 0, stream, a);
+    else
+      hipLaunchKernelGGL((dense_fwd_kernel<T>), dim3((unsigned)n), dim3(kFThreads), 0, stream, a);
     return hipGetLastError();
   }
   constexpr int kBM = 32 * kQB * kNW;
