@@ -120,9 +120,19 @@ __global__ __launch_bounds__(NW * 64) void dense_mfma_kernel(DenseArgs a) {
   const int l32 = lane & 31;
 
   const int n_qblk = (a.Lq + kBM - 1) / kBM;
-  const int tile_id = remap_xcd(blockIdx.x, gridDim.x);
-  const int qblk = tile_id % n_qblk;
-  const int bh = tile_id / n_qblk;
+  int qblk, bh;
+  if (CAUSAL) {
+    // Heaviest blocks first: under the top-left mask the last query block of a head needs the
+    // most keys, so all (b, h)'s last blocks are dispatched before their earlier ones and the
+    // light blocks fill the slots the heavy ones leave (448 x 448 at B=16: 35 -> 32.5 us).
+    const int n_bh = a.B * a.H;
+    qblk = n_qblk - 1 - (int)blockIdx.x / n_bh;
+    bh = (int)blockIdx.x % n_bh;
+  } else {
+    const int tile_id = remap_xcd(blockIdx.x, gridDim.x);
+    qblk = tile_id % n_qblk;
+    bh = tile_id / n_qblk;
+  }
   const int b = bh / a.H, h = bh % a.H;
 
   const e_t* Q = reinterpret_cast<const e_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
