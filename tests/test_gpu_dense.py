@@ -57,11 +57,15 @@ def test_dense_parity(cuda, dtype, B, H, Lq, Lk, causal):
 
 # Non-causal 16-bit launches pick a kernel by grid size (one workgroup per CU): the key-split
 # kernel with 128-query blocks when B*H*ceil(Lq/128) <= 256 (every SHAPES entry above), with
-# 256-query blocks when B*H*ceil(Lq/256) <= 256, else the 512-query kernel. One shape per route:
+# 256-query blocks when B*H*ceil(Lq/256) <= 256, else the 512-query kernel, whose last, mostly
+# empty round is handed to the key-split kernel when it fits one. One shape per route:
 ROUTES = [
     (1, 40, 1024, 300),  # 320 blocks of 128 > 256, 160 of 256: key split, 256-query blocks
     (4, 20, 800, 333),   # 320 blocks of 256 > 256: the 512-query kernel
     (1, 20, 1500, 1500),  # 240 blocks of 128: key split, 128-query blocks (a single window)
+    # the 512-query kernel over the heads that fill whole rounds, the key split over the rest:
+    (1, 300, 448, 200),  # 256 heads + 44 heads in 128-query blocks (the DTW cross-attention's split)
+    (1, 300, 1024, 100),  # 256 heads + 44 heads in 256-query blocks
 ]
 
 

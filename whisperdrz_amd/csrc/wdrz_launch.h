@@ -45,6 +45,7 @@ struct DenseArgs {
   const void* v;
   void* o;
   int B, H, Lq, Lk, causal;
+  int bh0;                             // first (b * H + h) of a dense_split_kernel launch
   int64_t qs[3], ks[3], vs[3], os[3];  // b, h, l strides
   float c;                             // softmax scale * log2(e)
 };
