@@ -181,7 +181,8 @@ def bench_config1(dev, steps: int, warmup: int) -> dict:
         "us_per_layer": round(us, 2),
         "tflops": round(tflops, 3),
         "roofline": {"bound": "mfma", "achieved": round(tflops, 3), "peak": PEAK_FP32_TFLOPS, "unit": "TFLOP/s",
-                     "frac": round(tflops / PEAK_FP32_TFLOPS, 4), "traffic": None,
+                     "frac": round(tflops / PEAK_FP32_TFLOPS, 4), "traffic": measured_traffic("dense_f32_kernel<false>"),
+                     "traffic_source": "profiles/pmc_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE passes)",
                      "kernel": "dense_f32_kernel<false> (v_mfma_f32_32x32x2_f32)"},
     }
 
@@ -1001,8 +1002,8 @@ def pmc_sample(dev) -> None:
     """A short, fixed kernel sequence for hardware-counter passes (rocprofv3 --pmc):
     a calibration copy of 1 GiB (known HBM bytes), then 3 launches of the encoder kernel, of
     each decode kernel, of the DTW prep, compute_attention, the fused attention + prep, the
-    cross-cache fill and the log-mel front end at the
-    bench shapes (eager)."""
+    cross-cache fill, the log-mel front end, the fp32 config 1 layer, one bf16 window and the
+    decode step's fc1 + GELU at the bench shapes (eager)."""
     from whisperdrz_amd import flash_attn_with_kvcache, scaled_dot_product_attention
 
     n = 1 << 30
@@ -1080,6 +1081,21 @@ def pmc_sample(dev) -> None:
     audio = 0.1 * torch.randn((MEL_B, MEL_N), generator=g, device=dev)
     for _ in range(3):
         log_mel_spectrogram(audio, MEL_MELS, 3000)
+        torch.cuda.synchronize()
+    del audio
+    # config 1 (fp32 matrix cores), one bf16 window (the key-split kernel), the decode step's
+    # fused fc1 + GELU on three distinct (cold) weights
+    from whisperdrz_amd import linear_gelu
+
+    for dt in (torch.float32, torch.bfloat16):
+        for i in range(3):
+            qkv = torch.randn((3, 1, 1500, H, D), generator=g, device=dev).to(dt)
+            scaled_dot_product_attention(*(x.permute(0, 2, 1, 3) for x in qkv), scale=0.125)
+            torch.cuda.synchronize()
+    x = torch.randn((64, 1280), generator=g, device=dev).to(torch.bfloat16)
+    for i in range(3):
+        lin = torch.nn.Linear(1280, 5120).to(dev, torch.bfloat16)
+        linear_gelu(x, lin)
         torch.cuda.synchronize()
     log("[bench] pmc sample done")
 
