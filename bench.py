@@ -343,7 +343,27 @@ def bench_decode(dev, steps: int, warmup: int) -> dict:
         {"sum_L": sumL5, "bytes_self_per_layer": bytes5_self, "bytes_cross_per_layer": bytes5_cross},
         kernels=("kv_mq_kernel<wdrz::Bf16, true>", "kv_mq_kernel<wdrz::Bf16, false>"),
     )
-    del self_kv, cross_kv
+    # ---- prefill: a 224-token prompt into empty self caches (the window's first call) ----
+    sqp = 224
+    csp = torch.zeros(Bs, dtype=torch.int32, device=dev)
+    qp = [q_new(9000 + i, sqp) for i in range(8)]
+
+    def bodyp():
+        for i in range(8):
+            q, k, v = qp[i]
+            flash_attn_with_kvcache(q, self_kv[i][0], self_kv[i][1], k=k, v=v, cache_seqlens=csp,
+                                    cache_batch_idx=slots, softmax_scale=0.125, causal=True)
+
+    for _ in range(warmup):
+        bodyp()
+    us_p = timed_events(bodyp, steps, torch.cuda.current_stream()) * 1e3 / 8
+    flop_p = 4.0 * Bs * H * D * sqp * (sqp + 1) / 2
+    log(f"[bench] prefill sq={sqp} into empty caches: {us_p:.1f} us/layer, {flop_p / us_p / 1e6:.1f} TFLOP/s")
+    res["prefill_self_sq224"] = {
+        "workload": "64 streams append a 224-token prompt to empty 448-row self caches (causal), bf16; "
+                    "kv_mq_kernel in 16-row query blocks",
+        "us_per_layer": round(us_p, 2), "tflops": round(flop_p / us_p / 1e6, 2)}
+    del self_kv, cross_kv, qp
     torch.cuda.empty_cache()
     return res
 

@@ -503,13 +503,15 @@ __device__ __forceinline__ float group4_max(float x) {
   return fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
 }
 
-template <typename T, bool HAS_NEW>
+// SQ: query rows per workgroup, 8 (one block of sq <= 8 rows) or 16 (blocks of 16 rows of a
+// longer prefill; every MFMA query slot used).
+template <typename T, bool HAS_NEW, int SQ>
 // At most 128 VGPRs (four wavefronts per SIMD): measured 5% faster for config 5 than the
 // unconstrained 148 (three per SIMD, the row's 1280 workgroups then need 1.7 rounds).
 __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
   typedef typename Mfma16<T>::op_t op_t;
   constexpr int kWaves = kWavesPerWg;
-  constexpr int SQ = kMaxSQ;
+  static_assert(SQ <= 16, "16 query slots per MFMA tile");
   __shared__ float sm_acc[kWaves][SQ][kHeadDim];
   __shared__ float sm_m[kWaves][SQ];
   __shared__ float sm_l[kWaves][SQ];
@@ -521,30 +523,31 @@ __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
   const int qi = lane & 15;  // query slot of this lane
   const int gq = lane >> 4;  // 16-lane group
 
-  const int b = blockIdx.x;
+  const int b = blockIdx.x / a.n_qblocks;
+  const int t0 = (blockIdx.x % a.n_qblocks) * SQ;  // first query row of this block
   const int h = blockIdx.y;
   const int split = blockIdx.z;
-  const int nq = a.sq;
+  const int nq = min(SQ, a.sq - t0);
 
   const int slot = a.bidx ? a.bidx[b] : b;
   const int cs = HAS_NEW ? a.seqlens[b] : 0;
-  static_assert(kMaxSQ * 2 * (kHeadDim * 2 / 16) <= kWaves * 64, "one append piece per thread");
-  const AppendPiece app = HAS_NEW ? kv_append_load<T>(a, b, 0, nq, h) : AppendPiece{};
+  static_assert(SQ * 2 * (kHeadDim * 2 / 16) <= kWaves * 64, "one append piece per thread");
+  const AppendPiece app = HAS_NEW ? kv_append_load<T>(a, b, t0, nq, h) : AppendPiece{};
   const bool bad = slot < 0 || slot >= a.n_slots || cs < 0 || (HAS_NEW && cs + a.sq > a.Lk);
-  const int key_lim = HAS_NEW ? cs + nq : a.Lk;
+  const int key_lim = HAS_NEW ? cs + t0 + nq : a.Lk;
   const int n_split_b = bad ? 1 : max(1, (key_lim + a.split_len - 1) / a.split_len);
   if (split >= n_split_b) return;
   const int k_begin = split * a.split_len;
   const int k_end = bad ? k_begin : min(key_lim, k_begin + a.split_len);
   // last key this lane's query may see (slots >= nq see none)
   int lim = k_end - 1;
-  if (HAS_NEW) lim = min(lim, cs + qi);
+  if (HAS_NEW) lim = min(lim, cs + t0 + qi);
   if (qi >= nq) lim = -1;
 
-  // Q^T operand halves: query qi (clamped), dims 32*dh + 8*gq .. +7
+  // Q^T operand halves: query t0 + qi (clamped), dims 32*dh + 8*gq .. +7
   op_t qop[2];
   {
-    const char* qrow = a.q + b * a.qs[0] + min(qi, nq - 1) * a.qs[1] + h * a.qs[2];
+    const char* qrow = a.q + b * a.qs[0] + (t0 + min(qi, nq - 1)) * a.qs[1] + h * a.qs[2];
 #pragma unroll
     for (int dh = 0; dh < 2; ++dh) qop[dh] = __builtin_bit_cast(op_t, load16(qrow + (32 * dh + 8 * gq) * 2));
   }
@@ -647,7 +650,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
     for (int db = 0; db < 4; ++db) o[db] = Mfma16<T>::run(vop[db], pop, o[db]);
   }
 
-  if (HAS_NEW && !bad) kv_append_store(a, app, 0, h, split, slot, cs);
+  if (HAS_NEW && !bad) kv_append_store(a, app, t0, h, split, slot, cs);
 
   // row sums: the four lane groups hold different keys of the same query
   l += __shfl_xor(l, 16);
@@ -663,7 +666,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
     }
   }
   __syncthreads();
-  kv_finish<T, SQ, kWaves>(a, b, 0, nq, nq, h, split, n_split_b, bad, sm_acc, sm_m, sm_l);
+  kv_finish<T, SQ, kWaves>(a, b, t0, nq, a.n_qblocks > 1 ? SQ : nq, h, split, n_split_b, bad, sm_acc, sm_m, sm_l);
 }
 
 template <typename T>
@@ -672,11 +675,18 @@ hipError_t launch_typed(const KvArgs& a, hipStream_t stream) {
   const bool has_new = a.kn != nullptr;
   const int sq_blk = a.n_qblocks > 1 ? kMaxSQ : a.sq;
   if constexpr (ElemBytes<T>::value == 2) {
+    if (a.mq_rows == 16) {  // prefill in 16-row blocks on the matrix cores
+      if (has_new)
+        hipLaunchKernelGGL((kv_mq_kernel<T, true, 16>), grid, dim3(kWavesPerWg * 64), 0, stream, a);
+      else
+        hipLaunchKernelGGL((kv_mq_kernel<T, false, 16>), grid, dim3(kWavesPerWg * 64), 0, stream, a);
+      return hipGetLastError();
+    }
     if (a.n_qblocks == 1 && sq_blk >= 2) {
       if (has_new)
-        hipLaunchKernelGGL((kv_mq_kernel<T, true>), grid, dim3(kWavesPerWg * 64), 0, stream, a);
+        hipLaunchKernelGGL((kv_mq_kernel<T, true, kMaxSQ>), grid, dim3(kWavesPerWg * 64), 0, stream, a);
       else
-        hipLaunchKernelGGL((kv_mq_kernel<T, false>), grid, dim3(kWavesPerWg * 64), 0, stream, a);
+        hipLaunchKernelGGL((kv_mq_kernel<T, false, kMaxSQ>), grid, dim3(kWavesPerWg * 64), 0, stream, a);
       return hipGetLastError();
     }
   }

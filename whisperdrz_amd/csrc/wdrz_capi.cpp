@@ -299,7 +299,12 @@ int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, co
   a.H = (int)H;
   a.Lk = (int)Lmax;
   a.n_slots = (int)n_slots;
-  a.n_qblocks = (int)((sq + 7) / 8);
+  // Prefill (sq > 8) in 16-bit types runs on the multi-query MFMA kernel in 16-row blocks when
+  // those blocks fill the chip on their own (so the launch never splits its keys and needs no
+  // workspace); otherwise in blocks of 8 rows, as the workspace size query assumes.
+  const bool mq16 = eb == 2 && sq > 8 && B * ((sq + 15) / 16) * H >= 1024;
+  a.n_qblocks = (int)(mq16 ? (sq + 15) / 16 : (sq + 7) / 8);
+  a.mq_rows = mq16 ? 16 : 0;
   const int64_t* S[4] = {q_strides, kc_strides, vc_strides, o_strides};
   int64_t* Dst[4] = {a.qs, a.kcs, a.vcs, a.os};
   for (int i = 0; i < 4; ++i)

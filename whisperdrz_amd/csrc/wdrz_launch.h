@@ -23,6 +23,7 @@ struct KvArgs {
   float* ws_part;  // split partials (split mode with n_splits > 1)
   int* ws_count;   // per-row arrival counters, zero between calls
   int B, sq, H, Lk, n_slots, n_qblocks, n_splits, split_len;
+  int mq_rows;  // 16: query blocks of 16 rows on the multi-query MFMA kernel; 0: blocks of 8 (or one block)
   int64_t qs[3], kcs[3], vcs[3], kns[3], vns[3], os[3];
   float c;  // softmax scale * log2(e)
 };
