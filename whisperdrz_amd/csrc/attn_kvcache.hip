@@ -449,8 +449,9 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
 }
 
 // ============================================================================================
-// Multi-query rows on the matrix core (16-bit types, 2 <= sq <= 8: draft verify, prefill
-// chunks). With several queries per row the VALU form above spends most of its time on the
+// Multi-query rows on the matrix core (16-bit types: 2 <= sq <= 8 in one block, the draft
+// verify; longer prefills in blocks of 16 rows when those blocks fill the chip, see the C layer).
+// With several queries per row the VALU form above spends most of its time on the
 // per-query dot products, reductions and exps of every key; here a wavefront takes 32 keys
 // per step and computes
 //   S^T (32 keys x 16 query slots) = K . Q^T       with 4 v_mfma_f32_16x16x32,
@@ -460,7 +461,8 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
 // V rows go through a per-wavefront LDS tile and come back transposed by ds_read_b64_tr_b16.
 // The P^T operand is the S^T accumulator itself: lane l holds query l%16 and keys
 // 4*(l/16)..+3 of each 16-key block, i.e. keys {4g..4g+3, 16+4g..16+4g+3} for g = l/16, and the
-// V^T operand is read in that same key order. Query slots >= sq are computed and discarded.
+// V^T operand is read in that same key order. Query slots past the block's rows are computed and
+// discarded.
 // The four wavefronts of a workgroup take interleaved 32-key chunks of the row (or split);
 // their partials merge through LDS as in the VALU kernel.
 // ============================================================================================
