@@ -959,7 +959,7 @@ hipError_t launch_typed(const DenseArgs& a, hipStream_t stream) {
     }
     const int64_t bh_main = (n / kNumCus) * kNumCus / qf;  // heads filling whole rounds
     const int64_t bh_rest = bh - bh_main;
-    if (bh_rest > 0 && bh_rest * q2 <= kNumCus && bh_rest * qf * 2 <= kNumCus) {
+    if (bh_main > 0 && bh_rest > 0 && bh_rest * q2 <= kNumCus && bh_rest * qf * 2 <= kNumCus) {
       hipLaunchKernelGGL((dense_fwd_kernel<T>), dim3((unsigned)(bh_main * qf)), dim3(kFThreads), 0, stream, a);
       DenseArgs rest = a;
       rest.bh0 = (int)bh_main;
