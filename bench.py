@@ -144,6 +144,9 @@ def bench_encoder(dev, steps: int, warmup: int) -> dict:
             "kernel": "dense_fwd_kernel<Bf16>",
             "flop_per_launch": flop_layer,
             "ms_per_launch": ms_launch,
+            # softmax exponentials per layer (B*H*L^2) and their rate: the VALU side of the kernel
+            "exp_per_launch": float(B * H * L * L),
+            "exp_per_s": round(B * H * L * L / (ms_launch * 1e-3), 1),
         },
     }
 
