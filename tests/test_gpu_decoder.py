@@ -29,11 +29,11 @@ def _ref_dense(q, k, v, is_causal=False, scale=None):
     return sdpa_torch(q, k, v, scale=scale, causal=is_causal)
 
 
-def _make(cuda, dtype, seed=0):
+def _make(cuda, dtype, seed=0, n_state=N_STATE, n_head=N_HEAD):
     from whisperdrz_amd.decoder import TextDecoderStack
 
     torch.manual_seed(seed)
-    hip = TextDecoderStack(N_VOCAB, N_CTX, N_STATE, N_HEAD, N_LAYER).to(cuda, dtype).eval()
+    hip = TextDecoderStack(N_VOCAB, N_CTX, n_state, n_head, N_LAYER).to(cuda, dtype).eval()
     ref = copy.deepcopy(hip)
     ref.fused_small_ops = False  # the reference's separate add and LayerNorm
     for blk in ref.blocks:
@@ -43,10 +43,10 @@ def _make(cuda, dtype, seed=0):
     return hip, ref
 
 
-def _pool(cuda, dtype, n_slots):
+def _pool(cuda, dtype, n_slots, n_state=N_STATE, n_head=N_HEAD):
     from whisperdrz_amd.kv_cache import KVSlotPool
 
-    return KVSlotPool(N_LAYER, n_slots, N_HEAD, N_STATE // N_HEAD, self_len=N_CTX, cross_len=CROSS_LEN,
+    return KVSlotPool(N_LAYER, n_slots, n_head, n_state // n_head, self_len=N_CTX, cross_len=CROSS_LEN,
                       dtype=dtype, device=cuda)
 
 
@@ -141,3 +141,24 @@ def test_graph_replay_matches_eager(cuda):
             _close(out_g, out_e, dtype, f"graph replay {step}")
             assert torch.equal(p_graph.self_kv[0].seq_lens, p_eager.self_kv[0].seq_lens)
         assert graphs.hits[4] == 5 and graphs.misses == 0
+
+
+def test_width_not_multiple_of_128(cuda):
+    """A width whose MLP input the fused fc1 + GELU kernel does not take (K % 128 != 0: 320 =
+    5 heads x 64) keeps torch's Linear + GELU inside the fused step and still matches."""
+    dtype, n_state, n_head = torch.bfloat16, 320, 5
+    hip, ref = _make(cuda, dtype, n_state=n_state, n_head=n_head)
+    B, n_slots = 2, 3
+    slots = torch.tensor([2, 0], device=cuda)
+    g = torch.Generator(device=cuda).manual_seed(5)
+    xa = torch.randn(B, CROSS_LEN, n_state, generator=g, device=cuda).to(dtype)
+    prompt = torch.randint(0, N_VOCAB, (B, 3), generator=g, device=cuda)
+    ph, pr = _pool(cuda, dtype, n_slots, n_state, n_head), _pool(cuda, dtype, n_slots, n_state, n_head)
+    with torch.no_grad():
+        _close(hip.prefill_flash(prompt, xa, ph.self_kv, ph.cross_kv, slot_indices=slots),
+               ref.prefill_flash(prompt, xa, pr.self_kv, pr.cross_kv, slot_indices=slots), dtype, "prefill logits")
+        for _ in range(3):
+            tok = torch.randint(0, N_VOCAB, (B, 1), generator=g, device=cuda)
+            pos = ph.self_kv[0].seq_lens[slots].long()
+            _close(hip.forward_flash(tok, ph.self_kv, ph.cross_kv, pos, slot_indices=slots),
+                   ref.forward_flash(tok, pr.self_kv, pr.cross_kv, pos, slot_indices=slots), dtype, "step logits")

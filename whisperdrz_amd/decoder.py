@@ -242,7 +242,9 @@ class TextDecoderStack(nn.Module):
             h = add_layernorm_(x, d, block.cross_attn_ln)
             d = block.cross_attn.forward_flash_step(h, c_kv, True, None, batch_idx)
             h = add_layernorm_(x, d, block.mlp_ln)
-            d = block.mlp[2](linear_gelu(h, block.mlp[0]))
+            fc1 = block.mlp[0]
+            # the fused fc1 + GELU kernel takes K % 128 == 0 (every Whisper width); others keep torch's
+            d = block.mlp[2](linear_gelu(h, fc1)) if fc1.in_features % 128 == 0 else block.mlp(h)
             h = add_layernorm_(x, d, blocks[i + 1].attn_ln if i + 1 < len(blocks) else self.ln)
         return h
 
