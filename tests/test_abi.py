@@ -285,3 +285,31 @@ def test_median_filter_rejects_short_strides_and_empty_is_a_no_op(lib):
     assert lib.wdrz_median_filter(FAKE, 50, FAKE, 100, 4, 100, 7, None) == 1
     assert "row strides" in lib.wdrz_last_error().decode()
     assert lib.wdrz_median_filter(FAKE, 100, FAKE, 100, 0, 100, 7, None) == 0
+
+
+def call_linear(lib, **over):
+    args = dict(dtype=2, x=FAKE, xs=1280, w=FAKE, ws=1280, b=FAKE, y=FAKE, ys=5120, M=64, N=5120, K=1280, act=1)
+    args.update(over)
+    return lib.wdrz_linear(args["dtype"], args["x"], args["xs"], args["w"], args["ws"], args["b"], args["y"],
+                           args["ys"], args["M"], args["N"], args["K"], args["act"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(dtype=0), 2, "only WDRZ_BF16 / WDRZ_F16"),
+    (dict(act=2), 1, "activation 2"),
+    (dict(K=1216), 2, "multiple of 128"),
+    (dict(N=5124), 2, "multiple of 128 and N=5124 of 8"),
+    (dict(N=0), 1, "bad sizes"),
+    (dict(w=None), 1, "is NULL"),
+    (dict(y=FAKE + 8), 1, "16-byte aligned"),
+    (dict(b=FAKE + 1), 1, "2-byte aligned"),
+    (dict(xs=1000), 1, "shorter than the rows"),
+    (dict(xs=1284), 1, "16-byte aligned"),
+])
+def test_linear_rejects_bad_arguments(lib, over, code, msg):
+    assert call_linear(lib, **over) == code
+    assert msg in lib.wdrz_last_error().decode()
+
+
+def test_linear_zero_rows_is_a_no_op(lib):
+    assert call_linear(lib, M=0, x=None, w=None, y=None) == 0
