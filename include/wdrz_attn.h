@@ -182,6 +182,38 @@ int wdrz_add_layernorm(int dtype, void* x, int64_t x_stride, const void* delta,
                        int64_t y_stride, int64_t rows, int64_t n, float eps, void* stream);
 
 /*
+ * The MLP output projection of the decode step, split along K (the first half of a pair with
+ * wdrz_add_layernorm_partials).
+ *
+ * Replaces: the last module of ResidualAttentionBlock.mlp, Linear(4 n_state, n_state)
+ *           (src/whisperdrz/model.py:388-391, applied at model.py:434), whose K = 4 n_state is
+ *           long and whose output is narrow: the library GEMM runs few workgroups for it.
+ * x: [M, K] rows (stride x_stride), w: [N, K] rows (stride w_stride), 16-bit types.
+ * partials: fp32 [n_split][M][N], contiguous: split z holds sum over k in [z K / n_split,
+ * (z + 1) K / n_split) of x[m, k] w[n, k]; no bias, no rounding. n_split 2 or 4,
+ * K % (128 n_split) == 0, N % 8 == 0, pointers and row strides 16-byte aligned.
+ */
+int wdrz_linear_partials(int dtype, const void* x, int64_t x_stride, const void* w, int64_t w_stride,
+                         float* partials, int64_t M, int64_t N, int64_t K, int n_split, void* stream);
+
+/*
+ * Residual add + LayerNorm with the delta given as a Linear's split-K partials (the second half
+ * of the pair with wdrz_linear_partials).
+ *
+ * Replaces: x = x + mlp(mlp_ln(x)) and the LayerNorm that follows (src/whisperdrz/model.py:434
+ *           then 420 of the next block, or the final ln, model.py:609-613): the Linear's output
+ *           delta = round(sum over z of partials[z] + delta_bias), rounded to the 16-bit type
+ *           as the library GEMM's output is; then x = round(x + delta) in place and
+ *           y = LayerNorm(x) as wdrz_add_layernorm computes it.
+ * partials: fp32 [n_split][rows][n] contiguous; delta_bias: the Linear's bias [n] (16-bit);
+ * n_split 2 or 4; n a multiple of 8, <= 1536; 16-byte aligned pointers and row strides.
+ */
+int wdrz_add_layernorm_partials(int dtype, void* x, int64_t x_stride, const float* partials,
+                                int n_split, const void* delta_bias, const void* weight,
+                                const void* bias, void* y, int64_t y_stride, int64_t rows,
+                                int64_t n, float eps, void* stream);
+
+/*
  * Greedy sampling with the decode step's token constraints.
  *
  * Replaces: decode_batch's sampling tail (src/whisperdrz/decoding.py:1729-1761):

@@ -313,3 +313,58 @@ def test_linear_rejects_bad_arguments(lib, over, code, msg):
 
 def test_linear_zero_rows_is_a_no_op(lib):
     assert call_linear(lib, M=0, x=None, w=None, y=None) == 0
+
+
+def call_linear_partials(lib, **over):
+    args = dict(dtype=2, x=FAKE, xs=5120, w=FAKE, ws=5120, p=FAKE, M=64, N=1280, K=5120, ns=4)
+    args.update(over)
+    return lib.wdrz_linear_partials(args["dtype"], args["x"], args["xs"], args["w"], args["ws"], args["p"],
+                                    args["M"], args["N"], args["K"], args["ns"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(dtype=0), 2, "only WDRZ_BF16 / WDRZ_F16"),
+    (dict(ns=3), 2, "n_split 3 is not 2 or 4"),
+    (dict(K=5120 - 128), 2, "multiple of 128 * n_split"),
+    (dict(N=1284), 2, "N=1284 of 8"),
+    (dict(M=-1), 1, "bad sizes"),
+    (dict(p=None), 1, "partials is NULL"),
+    (dict(p=FAKE + 4), 1, "16-byte aligned"),
+    (dict(ws=4096), 1, "shorter than the rows"),
+    (dict(xs=5124), 1, "16-byte aligned"),
+])
+def test_linear_partials_rejects_bad_arguments(lib, over, code, msg):
+    assert call_linear_partials(lib, **over) == code
+    assert msg in lib.wdrz_last_error().decode()
+
+
+def test_linear_partials_zero_rows_is_a_no_op(lib):
+    assert call_linear_partials(lib, M=0, x=None, w=None, p=None) == 0
+
+
+def call_add_ln_partials(lib, **over):
+    args = dict(dtype=2, x=FAKE, xs=1280, p=FAKE, ns=4, db=FAKE, w=FAKE, b=FAKE, y=FAKE, ys=1280, rows=64,
+                n=1280, eps=1e-5)
+    args.update(over)
+    return lib.wdrz_add_layernorm_partials(args["dtype"], args["x"], args["xs"], args["p"], args["ns"], args["db"],
+                                           args["w"], args["b"], args["y"], args["ys"], args["rows"], args["n"],
+                                           args["eps"], None)
+
+
+@pytest.mark.parametrize("over,code,msg", [
+    (dict(dtype=0), 2, "only WDRZ_BF16 / WDRZ_F16"),
+    (dict(ns=8), 2, "n_split 8 is not 2 or 4"),
+    (dict(n=1284), 1, "multiple of 8"),
+    (dict(n=2048), 2, "exceeds the supported 1536"),
+    (dict(eps=-1.0), 1, "eps"),
+    (dict(db=None), 1, "delta_bias is NULL"),
+    (dict(p=FAKE + 4), 1, "partials is not 16-byte aligned"),
+    (dict(ys=1284), 1, "16-byte aligned"),
+])
+def test_add_layernorm_partials_rejects_bad_arguments(lib, over, code, msg):
+    assert call_add_ln_partials(lib, **over) == code
+    assert msg in lib.wdrz_last_error().decode()
+
+
+def test_add_layernorm_partials_zero_rows_is_a_no_op(lib):
+    assert call_add_ln_partials(lib, rows=0, x=None, p=None, db=None, w=None, b=None, y=None) == 0

@@ -4,6 +4,10 @@ reference's own torch ops on the same GPU tensors.
 * add_layernorm_: the new residual x + delta bit-identical to torch's add; the LayerNorm within
   one unit in the last place of the 16-bit result of torch's LayerNorm (both compute in fp32;
   the reduction order differs), with at least 99% of the elements bit-identical.
+* add_layernorm_partials_: the delta given as fp32 split-K partials of a Linear plus its bias; the
+  reference is torch's sequential fp32 sum of the partials plus the bias, rounded to the 16-bit
+  type (the Linear's output), then the same add and LayerNorm: the residual bit-identical, the
+  LayerNorm to the bar above.
 * masked_argmax: token ids identical to the reference's sequence (zero, masked_fill -65504, add,
   repetition-penalty where, argmax; decoding.py:1729-1761, 854-855), ties and NaN logits included
   (a NaN is the maximum, as in torch.argmax).
@@ -47,6 +51,48 @@ def test_add_layernorm(cuda, dtype, rows, n):
     y2 = layer_norm(x_keep, ln)
     assert torch.equal(x_keep, x)
     assert torch.all((y2.float() - ln(x).float()).abs() <= _ulp16(ln(x)) * 1.001)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("rows,n,n_split", [(64, 1280, 4), (3, 256, 2), (130, 1536, 4), (1, 8, 4), (5, 1032, 2)])
+def test_add_layernorm_partials(cuda, dtype, rows, n, n_split):
+    from whisperdrz_amd import add_layernorm_partials_
+
+    g = torch.Generator(device=cuda).manual_seed(rows * 5 + n + n_split)
+    x = (3.0 * torch.randn(rows, n, generator=g, device=cuda) + 0.5).to(dtype)
+    partials = torch.randn(n_split, rows, n, generator=g, device=cuda)
+    fc = torch.nn.Linear(8, n).to(cuda, dtype)  # only its bias is used
+    ln = torch.nn.LayerNorm(n).to(cuda, dtype)
+    with torch.no_grad():
+        fc.bias.copy_(0.5 * torch.randn(n, generator=g, device=cuda))
+        ln.weight.copy_(1.0 + 0.1 * torch.randn(n, generator=g, device=cuda))
+        ln.bias.copy_(0.1 * torch.randn(n, generator=g, device=cuda))
+    print(f"add_layernorm_partials {dtype} rows={rows} n={n} n_split={n_split}", flush=True)
+    acc = partials[0].clone()
+    for z in range(1, n_split):
+        acc = acc + partials[z]
+    delta_ref = (acc + fc.bias.float()).to(dtype)
+    x_ref = x + delta_ref
+    y_ref = ln(x_ref)
+    x_in = x.clone()
+    y = add_layernorm_partials_(x_in, partials, fc, ln)
+    torch.cuda.synchronize()
+    assert torch.equal(x_in, x_ref)
+    diff = (y.float() - y_ref.float()).abs()
+    assert torch.all(diff <= _ulp16(y_ref) * 1.001), float(diff.max())
+    assert (diff == 0).float().mean().item() >= 0.99
+
+
+def test_add_layernorm_partials_errors(cuda):
+    from whisperdrz_amd import add_layernorm_partials_
+
+    x = torch.randn(4, 2048, device=cuda).to(torch.bfloat16)
+    fc = torch.nn.Linear(8, 2048).to(cuda, torch.bfloat16)
+    ln = torch.nn.LayerNorm(2048).to(cuda, torch.bfloat16)
+    with pytest.raises(NotImplementedError, match="1536"):
+        add_layernorm_partials_(x, torch.zeros(4, 4, 2048, device=cuda), fc, ln)
+    with pytest.raises(ValueError):
+        add_layernorm_partials_(x, torch.zeros(4, 3, 2048, device=cuda), fc, ln)
 
 
 def _reference_sampling(logits, blocked, penalty):

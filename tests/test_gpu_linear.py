@@ -7,6 +7,10 @@ what both the kernel and torch's 16-bit modules compute up to the order of the K
 two units in the last place of the 16-bit result (one for each rounding a different sum order can
 flip) plus 2^-10 absolute (GELU's flat region near -0.75), with at least 97% of the elements
 bit-identical to the fp32 reference; against torch's own 16-bit modules the same bar.
+
+linear_partials (the MLP output projection split along K, wdrz_linear_partials): each fp32
+partial against the float64 product of its K slice, within 1e-5 of the sum of |x_k w_k| (fp32
+accumulation over at most a few thousand terms).
 """
 import pytest
 import torch
@@ -88,3 +92,42 @@ def test_linear_zero_rows_and_errors(cuda):
         linear_gelu(torch.randn(2, 96, device=cuda, dtype=torch.bfloat16), bad)
     lib = _lib.load()
     assert lib.wdrz_linear(_lib.WDRZ_BF16, None, 64, None, 64, None, None, 32, 1, 32, 128, 1, None) == _lib.WDRZ_EINVAL
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("M,N,K,n_split", [(64, 1280, 5120, 4), (1, 1280, 5120, 4), (5, 1280, 5120, 2),
+                                           (65, 1024, 4096, 4), (130, 40, 1024, 2), (3, 8, 512, 4)])
+def test_linear_partials(cuda, dtype, M, N, K, n_split):
+    from whisperdrz_amd import linear_partials
+
+    print(f"linear_partials {dtype} M={M} N={N} K={K} n_split={n_split}", flush=True)
+    g = torch.Generator(device=cuda).manual_seed(M * 3 + N + K + n_split)
+    lin = torch.nn.Linear(K, N).to(cuda, dtype)
+    with torch.no_grad():
+        lin.weight.copy_(torch.randn(N, K, generator=g, device=cuda) / K ** 0.5)
+    x = torch.randn(M, K, generator=g, device=cuda).to(dtype)
+    part = linear_partials(x, lin, n_split)
+    torch.cuda.synchronize()
+    assert part.dtype == torch.float32 and tuple(part.shape) == (n_split, M, N)
+    kc = K // n_split
+    w = lin.weight.double()
+    for z in range(n_split):
+        xs, ws = x[:, z * kc:(z + 1) * kc].double(), w[:, z * kc:(z + 1) * kc]
+        ref = xs @ ws.T
+        scale = xs.abs() @ ws.abs().T
+        err = (part[z].double() - ref).abs()
+        assert torch.all(err <= 1e-5 * scale + 1e-30), f"split {z}: max error {float(err.max())}"
+
+
+def test_linear_partials_errors(cuda):
+    from whisperdrz_amd import linear_partials
+
+    lin = torch.nn.Linear(1000, 64).to(cuda, torch.bfloat16)
+    x = torch.randn(4, 1000, device=cuda).to(torch.bfloat16)
+    with pytest.raises(NotImplementedError, match="multiple of 128"):
+        linear_partials(x, lin, 4)  # K = 1000
+    lin2 = torch.nn.Linear(1024, 64).to(cuda, torch.bfloat16)
+    x2 = torch.randn(4, 1024, device=cuda).to(torch.bfloat16)
+    with pytest.raises(NotImplementedError, match="n_split 3"):
+        linear_partials(x2, lin2, 3)
+

@@ -14,7 +14,8 @@ from .attention import (
     scaled_dot_product_attention,
 )
 from .audio import LogMelSpectrogram, log_mel_spectrogram
-from .decode_ops import add_layernorm_, layer_norm, linear_gelu, masked_argmax
+from .decode_ops import (add_layernorm_, add_layernorm_partials_, layer_norm, linear_gelu, linear_partials,
+                         masked_argmax)
 from .dtw import (compute_attention, dtw_attention_prep, dtw_prep, dtw_prep_batch, dtw_prep_workspace_size,
                   median_filter)
 
@@ -31,8 +32,10 @@ __all__ = [
     "probe",
     "LogMelSpectrogram",
     "add_layernorm_",
+    "add_layernorm_partials_",
     "layer_norm",
     "linear_gelu",
+    "linear_partials",
     "masked_argmax",
     "log_mel_spectrogram",
     "compute_attention",

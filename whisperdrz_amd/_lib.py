@@ -36,6 +36,8 @@ EXPORTED_SYMBOLS = (
     "wdrz_add_layernorm",
     "wdrz_masked_argmax",
     "wdrz_linear",
+    "wdrz_linear_partials",
+    "wdrz_add_layernorm_partials",
     "wdrz_log_mel_workspace_size",
     "wdrz_log_mel",
     "wdrz_dtw_qk",
@@ -92,6 +94,17 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.wdrz_linear.argtypes = [
         ctypes.c_int, _p, _i64, _p, _i64, _p,  # dtype, x, x stride, w, w stride, bias
         _p, _i64, _i64, _i64, _i64, ctypes.c_int, _p,  # y, y stride, M, N, K, activation, stream
+    ]
+    lib.wdrz_linear_partials.restype = ctypes.c_int
+    lib.wdrz_linear_partials.argtypes = [
+        ctypes.c_int, _p, _i64, _p, _i64, _p,  # dtype, x, x stride, w, w stride, partials
+        _i64, _i64, _i64, ctypes.c_int, _p,  # M, N, K, n_split, stream
+    ]
+    lib.wdrz_add_layernorm_partials.restype = ctypes.c_int
+    lib.wdrz_add_layernorm_partials.argtypes = [
+        ctypes.c_int, _p, _i64, _p, ctypes.c_int, _p,  # dtype, x, x stride, partials, n_split, delta bias
+        _p, _p, _p, _i64, _i64, _i64,  # weight, bias, y, y stride, rows, n
+        ctypes.c_float, _p,  # eps, stream
     ]
     lib.wdrz_masked_argmax.restype = ctypes.c_int
     lib.wdrz_masked_argmax.argtypes = [

@@ -56,16 +56,20 @@ __device__ __forceinline__ float wave_sum64(float v) {
 
 // ---- residual add + LayerNorm (16-bit rows of n <= 64*8*NC elements) -------------------------
 // NC = 16-byte chunks per lane (n <= 512 * NC). The LayerNorm weight and bias are loaded with the
-// row, so the only dependent round trip is the row itself.
-template <typename T, int NC>
+// row, so the only dependent round trip is the row itself. NP > 0: the delta is a Linear's output
+// given as NP fp32 split-K partials [NP][rows][n] plus its bias, rounded to the storage type
+// after the sum, as the Linear's own output is.
+template <typename T, int NC, int NP>
 __global__ __launch_bounds__(256) void add_layernorm_kernel(AddLnArgs a) {
   const int lane = threadIdx.x & 63;
   const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (row >= a.rows) return;
   const int nc = a.n >> 3;  // 8-element chunks
   char* xrow = static_cast<char*>(a.x) + row * a.x_stride * 2;
-  const char* drow = a.delta ? static_cast<const char*>(a.delta) + row * a.d_stride * 2 : nullptr;
+  const char* drow = NP ? nullptr : a.delta ? static_cast<const char*>(a.delta) + row * a.d_stride * 2 : nullptr;
+  const bool has_delta = NP > 0 || drow != nullptr;
   u32x4 xw[NC], dw[NC], ww[NC], bw[NC];
+  f32x4 pw[NC][NP > 0 ? 2 * NP : 1];
 #pragma unroll
   for (int c = 0; c < NC; ++c) {
     const int ci = lane + 64 * c;
@@ -73,6 +77,15 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(AddLnArgs a) {
     if (ci < nc) {
       xw[c] = *reinterpret_cast<const u32x4*>(xrow + ci * 16);
       if (drow) dw[c] = *reinterpret_cast<const u32x4*>(drow + ci * 16);
+      if constexpr (NP > 0) {
+        dw[c] = *reinterpret_cast<const u32x4*>(static_cast<const char*>(a.dbias) + ci * 16);
+#pragma unroll
+        for (int z = 0; z < NP; ++z) {
+          const float* pr = a.dpart + ((int64_t)z * a.rows + row) * a.n + ci * 8;
+          pw[c][2 * z] = *reinterpret_cast<const f32x4*>(pr);
+          pw[c][2 * z + 1] = *reinterpret_cast<const f32x4*>(pr + 4);
+        }
+      }
       ww[c] = *reinterpret_cast<const u32x4*>(static_cast<const char*>(a.weight) + ci * 16);
       bw[c] = *reinterpret_cast<const u32x4*>(static_cast<const char*>(a.bias) + ci * 16);
     }
@@ -85,20 +98,38 @@ __global__ __launch_bounds__(256) void add_layernorm_kernel(AddLnArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) v[c][i] = 0.f;
     if (ci < nc) {
+      float dl[8];
+      if constexpr (NP > 0) {
+        // the Linear's output: partials summed in split order, bias added, one rounding
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+          float t = pw[c][i >> 2][i & 3];
+#pragma unroll
+          for (int z = 1; z < NP; ++z) t += pw[c][2 * z + (i >> 2)][i & 3];
+          const float bb = (i & 1) ? Elem<T>::hi(dw[c][i >> 1]) : Elem<T>::lo(dw[c][i >> 1]);
+          dl[i] = Elem<T>::round(t + bb);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          dl[2 * j] = Elem<T>::lo(dw[c][j]);
+          dl[2 * j + 1] = Elem<T>::hi(dw[c][j]);
+        }
+      }
       u32x4 sw;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         float s0 = Elem<T>::lo(xw[c][j]), s1 = Elem<T>::hi(xw[c][j]);
-        if (drow) {
-          s0 = Elem<T>::round(s0 + Elem<T>::lo(dw[c][j]));
-          s1 = Elem<T>::round(s1 + Elem<T>::hi(dw[c][j]));
+        if (has_delta) {
+          s0 = Elem<T>::round(s0 + dl[2 * j]);
+          s1 = Elem<T>::round(s1 + dl[2 * j + 1]);
           sw[j] = Elem<T>::pack(s0, s1);
         }
         v[c][2 * j] = s0;
         v[c][2 * j + 1] = s1;
         sum += s0 + s1;
       }
-      if (drow) *reinterpret_cast<u32x4*>(xrow + ci * 16) = sw;  // the new residual
+      if (has_delta) *reinterpret_cast<u32x4*>(xrow + ci * 16) = sw;  // the new residual
     }
   }
   const float inv_n = 1.f / (float)a.n;
@@ -193,17 +224,34 @@ hipError_t launch_add_layernorm(int dtype, const AddLnArgs& a, hipStream_t strea
   if (a.rows == 0) return hipSuccess;
   const dim3 grid((unsigned)((a.rows + 3) / 4));
   const int nc = (a.n + 511) / 512;
-  switch (nc) {
-#define WDRZ_LN(NC)                                                                                  \
-  case NC:                                                                                           \
-    if (dtype == 2) hipLaunchKernelGGL((add_layernorm_kernel<Bf16, NC>), grid, dim3(256), 0, stream, a); \
-    else hipLaunchKernelGGL((add_layernorm_kernel<F16, NC>), grid, dim3(256), 0, stream, a);         \
+  const int np = a.dpart ? a.n_part : 0;
+  // the partials form keeps 2 NP fp32 quads per chunk in registers: n <= 1536 (NC <= 3)
+  if ((np != 0 && np != 2 && np != 4) || (np != 0 && nc > 3)) return hipErrorInvalidValue;
+#define WDRZ_LN3(NC, NP)                                                                                 \
+  if (dtype == 2) hipLaunchKernelGGL((add_layernorm_kernel<Bf16, NC, NP>), grid, dim3(256), 0, stream, a); \
+  else hipLaunchKernelGGL((add_layernorm_kernel<F16, NC, NP>), grid, dim3(256), 0, stream, a);
+#define WDRZ_LNP(NC)     \
+  case NC:               \
+    if (np == 0) {       \
+      WDRZ_LN3(NC, 0)    \
+    } else if (np == 2) { \
+      WDRZ_LN3(NC, 2)    \
+    } else {             \
+      WDRZ_LN3(NC, 4)    \
+    }                    \
     break;
-    WDRZ_LN(1) WDRZ_LN(2) WDRZ_LN(3) WDRZ_LN(4) WDRZ_LN(5) WDRZ_LN(6) WDRZ_LN(7) WDRZ_LN(8)
-#undef WDRZ_LN
+#define WDRZ_LN(NC)   \
+  case NC:            \
+    WDRZ_LN3(NC, 0)   \
+    break;
+  switch (nc) {
+    WDRZ_LNP(1) WDRZ_LNP(2) WDRZ_LNP(3) WDRZ_LN(4) WDRZ_LN(5) WDRZ_LN(6) WDRZ_LN(7) WDRZ_LN(8)
     default:
       return hipErrorInvalidValue;
   }
+#undef WDRZ_LN
+#undef WDRZ_LNP
+#undef WDRZ_LN3
   return hipGetLastError();
 }
 

@@ -53,7 +53,10 @@ constexpr int kLinPad = 8;      // 16-bit elements of row padding in LDS (16 byt
 constexpr int kLinLd = kLinChunk + kLinPad;
 constexpr int kLinWChunks = 10;  // chunks of W requested together (K = 1280 in one group)
 
-template <typename T, int ACT, int NJ, int kLinPf>
+// PART: split-K form. Workgroup z of grid dimension z covers K range [z Kc, (z + 1) Kc), Kc =
+// K / n_split, and stores its fp32 partial sums (no bias, no rounding, no activation) to
+// part[z][m][n]; the consumer adds the splits and the bias.
+template <typename T, int ACT, int NJ, int kLinPf, bool PART>
 __global__ __launch_bounds__(256) void linear_act_kernel(LinearArgs a) {
   typedef typename LinMfma<T>::op_t op_t;
   constexpr int kLinFeat = 16 * NJ;  // output features (N) per workgroup
@@ -66,8 +69,10 @@ __global__ __launch_bounds__(256) void linear_act_kernel(LinearArgs a) {
 
   // loader: thread t copies 16 bytes at K offset 8 (t % 16) of rows t / 16 + 16 q
   const int lr = tid >> 4, lk = (tid & 15) * 8;
-  const uint16_t* W = static_cast<const uint16_t*>(a.w);
-  const uint16_t* X = static_cast<const uint16_t*>(a.x);
+  const int k_len = PART ? a.K / a.n_split : a.K;
+  const int k_base = PART ? (int)blockIdx.z * k_len : 0;
+  const uint16_t* W = static_cast<const uint16_t*>(a.w) + k_base;
+  const uint16_t* X = static_cast<const uint16_t*>(a.x) + k_base;
   const uint16_t* wsrc[NJ];
   const uint16_t* xsrc[4];
 #pragma unroll
@@ -77,7 +82,7 @@ __global__ __launch_bounds__(256) void linear_act_kernel(LinearArgs a) {
   // rows past M are neither loaded nor stored (their LDS rows feed only their own outputs)
   const int rows = min(a.M - m0, kLinRows);
 
-  const int n_chunks = a.K / kLinChunk;
+  const int n_chunks = k_len / kLinChunk;
   // X (just written by the previous kernel, in L2): kLinPf chunks ahead in registers
   u32x4 rx[kLinPf][4];
   auto fetch_x = [&](int c, u32x4* x4) {
@@ -140,6 +145,15 @@ __global__ __launch_bounds__(256) void linear_act_kernel(LinearArgs a) {
   // acc[j] lane holds C[n = 16 j + 4 (lane / 16) + r][m = 16 wave + lane % 16], r = 0..3
   const int m = m0 + 16 * wave + li;
   if (m >= a.M) return;
+  if constexpr (PART) {
+    float* P = a.part + ((int64_t)blockIdx.z * a.M + m) * a.N;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int nb = n0 + 16 * j + (lane >> 4) * 4;
+      if (nb < a.N) *reinterpret_cast<f32x4*>(P + nb) = acc[j];
+    }
+    return;
+  }
   const uint16_t* B = static_cast<const uint16_t*>(a.bias);
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
@@ -164,9 +178,11 @@ __global__ __launch_bounds__(256) void linear_act_kernel(LinearArgs a) {
 
 template <typename T, int NJ, int PF>
 void launch_t(const LinearArgs& a, hipStream_t stream) {
-  const dim3 grid((unsigned)((a.N + 16 * NJ - 1) / (16 * NJ)), (unsigned)((a.M + kLinRows - 1) / kLinRows));
-  if (a.act) hipLaunchKernelGGL((linear_act_kernel<T, 1, NJ, PF>), grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((linear_act_kernel<T, 0, NJ, PF>), grid, dim3(256), 0, stream, a);
+  const dim3 grid((unsigned)((a.N + 16 * NJ - 1) / (16 * NJ)), (unsigned)((a.M + kLinRows - 1) / kLinRows),
+                  (unsigned)(a.part ? a.n_split : 1));
+  if (a.part) hipLaunchKernelGGL((linear_act_kernel<T, 0, NJ, PF, true>), grid, dim3(256), 0, stream, a);
+  else if (a.act) hipLaunchKernelGGL((linear_act_kernel<T, 1, NJ, PF, false>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((linear_act_kernel<T, 0, NJ, PF, false>), grid, dim3(256), 0, stream, a);
 }
 
 hipError_t launch_linear(int dtype, const LinearArgs& a, hipStream_t stream) {

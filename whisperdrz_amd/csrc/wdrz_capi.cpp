@@ -451,6 +451,75 @@ int wdrz_linear(int dtype, const void* x, int64_t x_stride, const void* w, int64
   return WDRZ_OK;
 }
 
+int wdrz_linear_partials(int dtype, const void* x, int64_t x_stride, const void* w, int64_t w_stride, float* partials,
+                         int64_t M, int64_t N, int64_t K, int n_split, void* stream) {
+  g_last_error.clear();
+  if (dtype != WDRZ_BF16 && dtype != WDRZ_F16)
+    return fail(dtype == WDRZ_F32 ? WDRZ_EUNSUPPORTED : WDRZ_EINVAL, "dtype %d: only WDRZ_BF16 / WDRZ_F16", dtype);
+  if (n_split != 2 && n_split != 4) return fail(WDRZ_EUNSUPPORTED, "n_split %d is not 2 or 4", n_split);
+  if (M < 0 || N <= 0 || K <= 0) return fail(WDRZ_EINVAL, "bad sizes M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  if (K % (128 * n_split) != 0 || N % 8 != 0)
+    return fail(WDRZ_EUNSUPPORTED, "K=%lld must be a multiple of 128 * n_split and N=%lld of 8", (long long)K,
+                (long long)N);
+  if (M > (1 << 24) || N > (1 << 24) || K > (1 << 20) || M * N * n_split > ((int64_t)1 << 31))
+    return fail(WDRZ_EUNSUPPORTED, "sizes too large");
+  if (M == 0) return WDRZ_OK;
+  int rc;
+  if ((rc = check_ptr("x", x)) || (rc = check_ptr("w", w)) || (rc = check_ptr("partials", partials))) return rc;
+  if (x_stride < K || w_stride < K) return fail(WDRZ_EINVAL, "row strides shorter than the rows");
+  if ((x_stride * 2) % 16 || (w_stride * 2) % 16) return fail(WDRZ_EINVAL, "row strides are not 16-byte aligned");
+  wdrz::LinearArgs a{};
+  a.x = x;
+  a.w = w;
+  a.x_stride = x_stride;
+  a.w_stride = w_stride;
+  a.M = (int)M;
+  a.N = (int)N;
+  a.K = (int)K;
+  a.part = partials;
+  a.n_split = n_split;
+  hipError_t err = wdrz::launch_linear(dtype, a, reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(WDRZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  return WDRZ_OK;
+}
+
+int wdrz_add_layernorm_partials(int dtype, void* x, int64_t x_stride, const float* partials, int n_split,
+                                const void* delta_bias, const void* weight, const void* bias, void* y,
+                                int64_t y_stride, int64_t rows, int64_t n, float eps, void* stream) {
+  g_last_error.clear();
+  if (dtype != WDRZ_BF16 && dtype != WDRZ_F16)
+    return fail(dtype == WDRZ_F32 ? WDRZ_EUNSUPPORTED : WDRZ_EINVAL, "dtype %d: only WDRZ_BF16 / WDRZ_F16", dtype);
+  if (n_split != 2 && n_split != 4) return fail(WDRZ_EUNSUPPORTED, "n_split %d is not 2 or 4", n_split);
+  if (rows < 0 || n <= 0 || n % 8 != 0)
+    return fail(WDRZ_EINVAL, "bad sizes rows=%lld n=%lld (n must be a positive multiple of 8)", (long long)rows,
+                (long long)n);
+  if (n > 1536) return fail(WDRZ_EUNSUPPORTED, "n=%lld exceeds the supported 1536", (long long)n);
+  if (rows > (1 << 24)) return fail(WDRZ_EUNSUPPORTED, "sizes too large");
+  if (!(eps >= 0.f)) return fail(WDRZ_EINVAL, "eps must be >= 0");
+  if (rows == 0) return WDRZ_OK;
+  int rc;
+  if ((rc = check_ptr("x", x)) || (rc = check_ptr("partials", partials)) || (rc = check_ptr("delta_bias", delta_bias)) ||
+      (rc = check_ptr("weight", weight)) || (rc = check_ptr("bias", bias)) || (rc = check_ptr("y", y)))
+    return rc;
+  if ((x_stride * 2) % 16 || (y_stride * 2) % 16) return fail(WDRZ_EINVAL, "row strides must be 16-byte aligned");
+  wdrz::AddLnArgs a{};
+  a.x = x;
+  a.weight = weight;
+  a.bias = bias;
+  a.y = y;
+  a.rows = rows;
+  a.n = (int)n;
+  a.x_stride = x_stride;
+  a.y_stride = y_stride;
+  a.eps = eps;
+  a.dpart = partials;
+  a.n_part = n_split;
+  a.dbias = delta_bias;
+  hipError_t err = wdrz::launch_add_layernorm(dtype, a, reinterpret_cast<hipStream_t>(stream));
+  if (err != hipSuccess) return fail(WDRZ_ELAUNCH, "kernel launch failed: %s", hipGetErrorString(err));
+  return WDRZ_OK;
+}
+
 int wdrz_kv_fill(int dtype, const void* k_src, const void* v_src, const int64_t* src_strides, void* k_cache,
                  void* v_cache, const int64_t* cache_strides, const int64_t* slot_indices, int64_t B, int64_t T,
                  int64_t H, int64_t D, int64_t n_slots, int64_t Lmax, int64_t start_pos, void* stream) {

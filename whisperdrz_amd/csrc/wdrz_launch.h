@@ -98,6 +98,11 @@ struct AddLnArgs {
   int n;
   int64_t x_stride, d_stride, y_stride;
   float eps;
+  // delta given as fp32 split-K partials [n_part][rows][n] of a Linear plus its 16-bit bias:
+  // delta = round(sum of the partials + bias), as the Linear's output (used when dpart != nullptr)
+  const float* dpart = nullptr;
+  int n_part = 0;
+  const void* dbias = nullptr;
 };
 hipError_t launch_add_layernorm(int dtype, const AddLnArgs& a, hipStream_t stream);
 
@@ -150,6 +155,8 @@ struct LinearArgs {
   void* y;
   int64_t x_stride, w_stride, y_stride;
   int M, N, K, act;
+  float* part = nullptr;  // split-K form: fp32 partials [n_split][M][N] instead of y
+  int n_split = 1;
 };
 hipError_t launch_linear(int dtype, const LinearArgs& a, hipStream_t stream);
 

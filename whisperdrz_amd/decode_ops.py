@@ -119,3 +119,56 @@ def linear_gelu(x: torch.Tensor, lin: nn.Linear, gelu: bool = True) -> torch.Ten
     if rc != _lib.WDRZ_OK:
         _raise(rc, "linear_gelu")
     return y.view(*x.shape[:-1], N)
+
+def linear_partials(x: torch.Tensor, lin: nn.Linear, n_split: int = 4) -> torch.Tensor:
+    """fp32 split-K partial products of ``lin`` (no bias) for 16-bit ``x [..., K]``: a tensor
+    ``[n_split, rows, N]`` whose sum over the first dimension is ``x @ lin.weight.T``; its
+    consumer (``add_layernorm_partials_``) adds the bias and rounds like the Linear's output."""
+    _check_cuda("x", x, x.device)
+    if x.dtype not in _LN16:
+        raise TypeError(f"x: dtype {x.dtype} is not supported (bfloat16, float16)")
+    xr = _rows(x, "x")
+    w = lin.weight.detach()
+    if w.dtype != x.dtype:
+        raise TypeError("the Linear's parameters must have the activations' dtype")
+    if w.stride(-1) != 1 or w.shape[1] != xr.shape[1]:
+        raise ValueError("weight must be [N, K] with contiguous rows and K = x.shape[-1]")
+    N = int(w.shape[0])
+    part = torch.empty(n_split, xr.shape[0], N, dtype=torch.float32, device=x.device)
+    rc = _lib.load().wdrz_linear_partials(
+        _LN16[x.dtype], xr.data_ptr(), xr.stride(0), w.data_ptr(), w.stride(0), part.data_ptr(),
+        xr.shape[0], N, xr.shape[1], n_split, _stream_handle(),
+    )
+    if rc != _lib.WDRZ_OK:
+        _raise(rc, "linear_partials")
+    return part
+
+
+def add_layernorm_partials_(x: torch.Tensor, partials: torch.Tensor, lin: nn.Linear,
+                            ln: nn.LayerNorm) -> torch.Tensor:
+    """In place ``x += lin(h)`` where ``partials = linear_partials(h, lin)`` (the sum of the
+    partials plus ``lin.bias``, rounded to ``x``'s type like the Linear's output), then returns
+    ``ln(x)`` as ``add_layernorm_`` does."""
+    _check_cuda("x", x, x.device)
+    if x.dtype not in _LN16:
+        raise TypeError(f"x: dtype {x.dtype} is not supported (bfloat16, float16)")
+    xr = _rows(x, "x")
+    n_split = int(partials.shape[0])
+    if partials.dtype != torch.float32 or tuple(partials.shape[1:]) != tuple(xr.shape) or not partials.is_contiguous():
+        raise ValueError("partials must be contiguous fp32 [n_split, rows, n] matching x")
+    if lin.bias is None:
+        raise ValueError("the Linear must have a bias")
+    db = lin.bias.detach()
+    w = ln.weight.detach()
+    b = ln.bias.detach()
+    if w.dtype != x.dtype or db.dtype != x.dtype:
+        raise TypeError("the LayerNorm and Linear parameters must have the activations' dtype")
+    y = torch.empty_like(xr)
+    rc = _lib.load().wdrz_add_layernorm_partials(
+        _LN16[x.dtype], xr.data_ptr(), xr.stride(0), partials.data_ptr(), n_split, db.data_ptr(),
+        w.data_ptr(), b.data_ptr(), y.data_ptr(), y.stride(0), xr.shape[0], xr.shape[1], float(ln.eps),
+        _stream_handle(),
+    )
+    if rc != _lib.WDRZ_OK:
+        _raise(rc, "add_layernorm_partials_")
+    return y.view(x.shape)

@@ -14,8 +14,10 @@ cached attention, so the HIP kernels can be exercised exactly as WhisperDRZ driv
   824-869).
 * ``TextDecoderStack._fused_blocks`` — the same blocks with each residual add fused into the
   next LayerNorm (``decode_ops.add_layernorm_``), the step's metadata (int32 slot map, every
-  layer's gathered lengths) computed once per step and the self-attention query / key / value
-  projections as one GEMM; the default for 16-bit GPU activations.
+  layer's gathered lengths) computed once per step, the self-attention query / key / value
+  projections as one GEMM, fc1 with its GELU as one kernel (``linear_gelu``) and fc2 as split-K
+  partials summed by the residual add (``linear_partials`` + ``add_layernorm_partials_``); the
+  default for 16-bit GPU activations.
 * ``BucketedDecodeGraphs`` — one captured decode step per batch bucket, replayed with static
   token / position / slot buffers (reference ``transcriber.py:18-173``); on ROCm
   ``torch.cuda.CUDAGraph`` is a hipGraph.
@@ -34,7 +36,7 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from .attention import flash_attn_with_kvcache, scaled_dot_product_attention
-from .decode_ops import add_layernorm_, layer_norm, linear_gelu
+from .decode_ops import add_layernorm_, add_layernorm_partials_, layer_norm, linear_gelu, linear_partials
 from .kv_cache import FlashKVCache, KVSlotPool
 
 # Batch buckets of the captured decode step (reference transcriber.py:18).
@@ -242,10 +244,16 @@ class TextDecoderStack(nn.Module):
             h = add_layernorm_(x, d, block.cross_attn_ln)
             d = block.cross_attn.forward_flash_step(h, c_kv, True, None, batch_idx)
             h = add_layernorm_(x, d, block.mlp_ln)
-            fc1 = block.mlp[0]
-            # the fused fc1 + GELU kernel takes K % 128 == 0 (every Whisper width); others keep torch's
-            d = block.mlp[2](linear_gelu(h, fc1)) if fc1.in_features % 128 == 0 else block.mlp(h)
-            h = add_layernorm_(x, d, blocks[i + 1].attn_ln if i + 1 < len(blocks) else self.ln)
+            fc1, fc2 = block.mlp[0], block.mlp[2]
+            ln_next = blocks[i + 1].attn_ln if i + 1 < len(blocks) else self.ln
+            # fused fc1 + GELU, then fc2 as 4 split-K fp32 partials that the residual add sums
+            # (with fc2's bias and rounding) before the next LayerNorm: every Whisper width
+            # (K % 128 == 0, 4 K % 512 == 0, n <= 1536); other widths keep torch's MLP
+            if fc1.in_features % 128 == 0 and fc2.in_features % 512 == 0 and fc2.out_features <= 1536 \
+                    and fc2.bias is not None:
+                h = add_layernorm_partials_(x, linear_partials(linear_gelu(h, fc1), fc2, 4), fc2, ln_next)
+            else:
+                h = add_layernorm_(x, block.mlp(h), ln_next)
         return h
 
     def prefill_flash(self, tokens: Tensor, xa: Tensor, self_kv: list[FlashKVCache], cross_kv: list[FlashKVCache],
