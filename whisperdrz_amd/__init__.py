@@ -14,7 +14,7 @@ from .attention import (
     scaled_dot_product_attention,
 )
 from .audio import LogMelSpectrogram, log_mel_spectrogram
-from .decode_ops import (add_layernorm_, add_layernorm_partials_, layer_norm, linear_gelu, linear_partials,
+from .decode_ops import (add_layernorm_, add_layernorm_partials_, layer_norm, linear, linear_gelu, linear_partials,
                          masked_argmax)
 from .dtw import (compute_attention, dtw_attention_prep, dtw_prep, dtw_prep_batch, dtw_prep_workspace_size,
                   median_filter)
@@ -34,6 +34,7 @@ __all__ = [
     "add_layernorm_",
     "add_layernorm_partials_",
     "layer_norm",
+    "linear",
     "linear_gelu",
     "linear_partials",
     "masked_argmax",

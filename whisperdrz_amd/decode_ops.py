@@ -94,15 +94,15 @@ def masked_argmax(logits: torch.Tensor, blocked: Optional[torch.Tensor] = None,
     return out
 
 
-def linear_gelu(x: torch.Tensor, lin: nn.Linear, gelu: bool = True) -> torch.Tensor:
-    """``GELU(lin(x))`` (``gelu=False``: ``lin(x)``) for 16-bit ``x [..., K]``, rounded like the
-    reference's two modules: the Linear's output to the storage type, then the GELU's."""
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor], gelu: bool = False) -> torch.Tensor:
+    """``x @ weight.T + bias`` (``gelu``: then the exact GELU) for 16-bit ``x [..., K]``, rounded
+    like torch's 16-bit modules: the Linear's output to the storage type, then the GELU's."""
     _check_cuda("x", x, x.device)
     if x.dtype not in _LN16:
         raise TypeError(f"x: dtype {x.dtype} is not supported (bfloat16, float16)")
     xr = _rows(x, "x")
-    w = lin.weight.detach()
-    b = lin.bias.detach() if lin.bias is not None else None
+    w = weight.detach()
+    b = bias.detach() if bias is not None else None
     if w.dtype != x.dtype or (b is not None and b.dtype != x.dtype):
         raise TypeError("the Linear's parameters must have the activations' dtype")
     if w.stride(-1) != 1 or w.shape[1] != xr.shape[1]:
@@ -117,8 +117,15 @@ def linear_gelu(x: torch.Tensor, lin: nn.Linear, gelu: bool = True) -> torch.Ten
         xr.shape[0], N, xr.shape[1], 1 if gelu else 0, _stream_handle(),
     )
     if rc != _lib.WDRZ_OK:
-        _raise(rc, "linear_gelu")
+        _raise(rc, "linear")
     return y.view(*x.shape[:-1], N)
+
+
+def linear_gelu(x: torch.Tensor, lin: nn.Linear, gelu: bool = True) -> torch.Tensor:
+    """``GELU(lin(x))`` (``gelu=False``: ``lin(x)``) for 16-bit ``x [..., K]``, rounded like the
+    reference's two modules: the Linear's output to the storage type, then the GELU's."""
+    return linear(x, lin.weight, lin.bias, gelu)
+
 
 def linear_partials(x: torch.Tensor, lin: nn.Linear, n_split: int = 4) -> torch.Tensor:
     """fp32 split-K partial products of ``lin`` (no bias) for 16-bit ``x [..., K]``: a tensor

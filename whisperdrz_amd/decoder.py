@@ -15,9 +15,10 @@ cached attention, so the HIP kernels can be exercised exactly as WhisperDRZ driv
 * ``TextDecoderStack._fused_blocks`` — the same blocks with each residual add fused into the
   next LayerNorm (``decode_ops.add_layernorm_``), the step's metadata (int32 slot map, every
   layer's gathered lengths) computed once per step, the self-attention query / key / value
-  projections as one GEMM, fc1 with its GELU as one kernel (``linear_gelu``) and fc2 as split-K
-  partials summed by the residual add (``linear_partials`` + ``add_layernorm_partials_``); the
-  default for 16-bit GPU activations.
+  projections as one GEMM (``decode_ops.linear``), fc1 with its GELU as one kernel
+  (``linear_gelu``), and the attention output projections and fc2 as split-K partials summed by
+  the residual add (``linear_partials`` + ``add_layernorm_partials_``); the default for 16-bit
+  GPU activations.
 * ``BucketedDecodeGraphs`` — one captured decode step per batch bucket, replayed with static
   token / position / slot buffers (reference ``transcriber.py:18-173``); on ROCm
   ``torch.cuda.CUDAGraph`` is a hipGraph.
@@ -36,7 +37,7 @@ import torch.nn.functional as F
 from torch import Tensor
 
 from .attention import flash_attn_with_kvcache, scaled_dot_product_attention
-from .decode_ops import add_layernorm_, add_layernorm_partials_, layer_norm, linear_gelu, linear_partials
+from .decode_ops import add_layernorm_, add_layernorm_partials_, layer_norm, linear, linear_gelu, linear_partials
 from .kv_cache import FlashKVCache, KVSlotPool
 
 # Batch buckets of the captured decode step (reference transcriber.py:18).
@@ -49,6 +50,16 @@ def bucket_for(batch: int, buckets: list[int]) -> int:
         if batch <= b:
             return b
     return batch
+
+
+def _out_add_layernorm(x: Tensor, o: Tensor, out: nn.Linear, ln: nn.LayerNorm) -> Tensor:
+    """``x += out(o)`` then ``ln(x)`` (the output projection at model.py:362, the residual adds at
+    420-432 and the next sub-layer's LayerNorm): the
+    attention's output projection as 2 split-K fp32 partials summed by the residual add (K a
+    multiple of 256, n_state <= 1536), else torch's Linear and the fused add + LayerNorm."""
+    if out.in_features % 256 == 0 and out.out_features <= 1536 and out.bias is not None:
+        return add_layernorm_partials_(x, linear_partials(o, out, 2), out, ln)
+    return add_layernorm_(x, out(o), ln)
 
 
 def lengths_matrix(self_kv: list[FlashKVCache]) -> Optional[Tensor]:
@@ -115,10 +126,13 @@ class MultiHeadAttention(nn.Module):
         return cached[1], cached[2]
 
     def forward_flash_step(self, x: Tensor, kv_cache: FlashKVCache, is_cross_attn: bool,
-                           cache_seqlens: Optional[Tensor], batch_idx: Optional[Tensor]) -> Tensor:
+                           cache_seqlens: Optional[Tensor], batch_idx: Optional[Tensor],
+                           project_out: bool = True) -> Tensor:
         """``forward_flash`` with the step's metadata computed once by the caller (the gathered
         ``cache_seqlens`` and the int32 slot map) and, for self-attention, the query / key /
-        value projections as one GEMM. Same arithmetic per output element."""
+        value projections as one GEMM (``decode_ops.linear`` when K % 128 == 0). Same arithmetic
+        per output element. ``project_out=False`` returns the attention output before ``out``
+        (the caller applies it, fused with the residual add)."""
         B, seq_len, _ = x.shape
         d = self.n_state // self.n_head
         if is_cross_attn:
@@ -127,11 +141,13 @@ class MultiHeadAttention(nn.Module):
                                   softmax_scale=d ** -0.5, causal=False)
         else:
             w, b = self.qkv_weight()
-            qkv = F.linear(x, w, b).view(B, seq_len, 3, self.n_head, d)
+            qkv = linear(x, w, b) if self.n_state % 128 == 0 else F.linear(x, w, b)
+            qkv = qkv.view(B, seq_len, 3, self.n_head, d)
             o = self.attn_kvcache(qkv[:, :, 0], kv_cache.k_cache, kv_cache.v_cache, k=qkv[:, :, 1], v=qkv[:, :, 2],
                                   cache_seqlens=cache_seqlens, cache_batch_idx=batch_idx, softmax_scale=d ** -0.5,
                                   causal=self.causal)
-        return self.out(o.reshape(B, seq_len, self.n_state))
+        o = o.reshape(B, seq_len, self.n_state)
+        return self.out(o) if project_out else o
 
     def forward_flash(self, x: Tensor, kv_cache: FlashKVCache, is_cross_attn: bool = False,
                       slot_indices: Optional[Tensor] = None) -> Tensor:
@@ -240,10 +256,10 @@ class TextDecoderStack(nn.Module):
             layer_lens = [s.seq_lens if slot_indices is None else s.seq_lens[slot_indices] for s in self_kv]
         h = layer_norm(x, blocks[0].attn_ln)
         for i, (block, s_kv, c_kv) in enumerate(zip(blocks, self_kv, cross_kv, strict=True)):
-            d = block.attn.forward_flash_step(h, s_kv, False, layer_lens[i], batch_idx)
-            h = add_layernorm_(x, d, block.cross_attn_ln)
-            d = block.cross_attn.forward_flash_step(h, c_kv, True, None, batch_idx)
-            h = add_layernorm_(x, d, block.mlp_ln)
+            o = block.attn.forward_flash_step(h, s_kv, False, layer_lens[i], batch_idx, project_out=False)
+            h = _out_add_layernorm(x, o, block.attn.out, block.cross_attn_ln)
+            o = block.cross_attn.forward_flash_step(h, c_kv, True, None, batch_idx, project_out=False)
+            h = _out_add_layernorm(x, o, block.cross_attn.out, block.mlp_ln)
             fc1, fc2 = block.mlp[0], block.mlp[2]
             ln_next = blocks[i + 1].attn_ln if i + 1 < len(blocks) else self.ln
             # fused fc1 + GELU, then fc2 as 4 split-K fp32 partials that the residual add sums
