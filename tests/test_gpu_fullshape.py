@@ -159,11 +159,12 @@ def test_config5_verify_equals_sequential(cuda, dtype):
 
 
 @pytest.mark.parametrize("dtype", LOWP)
-@pytest.mark.parametrize("sq", [9, 16, 37, 224])
+@pytest.mark.parametrize("sq", [9, 16, 37, 40, 224, 300])
 def test_prefill_self(cuda, dtype, sq):
     """Prefill of sq > 8 new tokens into 448-row slots (the prompt of a window): at 64 streams the
-    launch takes the multi-query MFMA kernel in 16-row blocks. Pre-append lengths uniform in
-    [0, 448 - sq], with an empty cache and a full one among them."""
+    launch takes the multi-query MFMA kernel in 16-row blocks below 40 new rows and the 256-query
+    prefill kernel from 40 on (300: two query blocks, the second ragged). Pre-append lengths
+    uniform in [0, 448 - sq], with an empty cache and a full one among them."""
     rng = np.random.default_rng(sq)
     L = rng.integers(sq, 448 + 1, size=B)
     L[0], L[1] = sq, 448

@@ -55,7 +55,7 @@ def _case(cuda, dtype, B, sq, H, n_slots, Lmax, layout, seed, self_attn=True, bi
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
-@pytest.mark.parametrize("sq", [1, 2, 5, 7, 8, 9, 17])
+@pytest.mark.parametrize("sq", [1, 2, 5, 7, 8, 9, 17, 40, 77])
 @pytest.mark.parametrize("layout", ["slot_major", "head_major"])
 def test_self_attention(cuda, dtype, sq, layout):
     print(f"self dtype={dtype} sq={sq} layout={layout}", flush=True)
@@ -182,6 +182,28 @@ def test_bad_slot_gives_nan_not_fault(cuda, sq, self_attn):
     if self_attn:
         snap_k[1, 5 : 5 + sq] = k[0]
     assert torch.equal(kc, snap_k)
+
+
+def test_prefill_bad_metadata_gives_nan_not_fault(cuda):
+    """The prefill kernel (sq >= 40): an out-of-range slot id and a row whose append would run past
+    the cache give NaN rows, no append and no memory access; the valid row is appended and finite."""
+    from whisperdrz_amd import flash_attn_with_kvcache
+
+    sq, Lmax = 70, 128
+    kc, vc = make_cache(3, Lmax, 2, D, torch.bfloat16, cuda, "slot_major", 1)
+    snap_k, snap_v = kc.clone(), vc.clone()
+    q = randn((3, sq, 2, D), 2, torch.bfloat16).to(cuda)
+    k = randn((3, sq, 2, D), 3, torch.bfloat16).to(cuda)
+    v = randn((3, sq, 2, D), 4, torch.bfloat16).to(cuda)
+    bidx = torch.tensor([1, 3, 2], dtype=torch.int32, device=cuda)   # slot 3 is outside the pool
+    seq = torch.tensor([5, 5, 60], dtype=torch.int32, device=cuda)   # 60 + 70 > 128
+    out = flash_attn_with_kvcache(q, kc, vc, k=k, v=v, cache_seqlens=seq, cache_batch_idx=bidx, causal=True)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out[0].float()).all()
+    assert torch.isnan(out[1].float()).all() and torch.isnan(out[2].float()).all()
+    snap_k[1, 5 : 5 + sq] = k[0]
+    snap_v[1, 5 : 5 + sq] = v[0]
+    assert torch.equal(kc, snap_k) and torch.equal(vc, snap_v)
 
 
 def test_workspace_reuse_across_shapes(cuda):

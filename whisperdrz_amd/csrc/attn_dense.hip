@@ -371,6 +371,238 @@ __global__ __launch_bounds__(NW * 64) void dense_mfma_kernel(DenseArgs a) {
   }
 }
 
+// ============================================================================================
+// Prefill into the slot caches (flash_attn_with_kvcache with many new rows, sq >= kPrefillMinSq;
+// reference src/whisperdrz/model.py:42-63): for batch row b, query t of the sq new rows sees keys
+// [0, cs + t] of the row's cache after the append, cs = cache_seqlens[b] -- keys below cs from
+// the cache slot, the others straight from k_new / v_new -- and the workgroup appends its own
+// query rows' new keys and values to the cache. The step structure is the causal kernel's above
+// (256 queries in eight 32-query wavefronts, K/V tiles of 64 keys through three LDS buffers, V
+// transposed at staging), so each new row's keys are read ~sq/256 times instead of once per
+// 16-query block. Rows with invalid metadata (slot outside the pool, cs < 0 or cs + sq past the
+// cache) get NaN output and no append.
+// ============================================================================================
+template <typename T>
+__global__ __launch_bounds__(512, 4) void kv_prefill_kernel(KvArgs a) {
+  constexpr int NW = 8;
+  constexpr int kThreads = NW * 64;
+  constexpr int kBM = 32 * NW;
+  typedef typename Mfma<T>::op_t op_t;
+  typedef uint16_t e_t;
+  __shared__ __attribute__((aligned(16))) e_t sK[kNumBuf][kBN * kPitchK];
+  __shared__ __attribute__((aligned(16))) e_t sVt[kNumBuf][kHeadDim * kBN];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int hl = lane >> 5;
+  const int l32 = lane & 31;
+
+  // heaviest query blocks (the last ones of a row) first, as in the causal kernel
+  const int n_qblk = (a.sq + kBM - 1) / kBM;
+  const int qblk = n_qblk - 1 - (int)blockIdx.x / a.B;
+  const int b = (int)blockIdx.x % a.B;
+  const int h = blockIdx.y;
+  const int slot = a.bidx ? a.bidx[b] : b;
+  const int cs = a.seqlens[b];
+  const int sq = a.sq;
+  const int q_wg = qblk * kBM;
+  const int q_wave = q_wg + wave * 32;
+
+  char* const Ob = a.o + (int64_t)b * a.os[0] + (int64_t)h * a.os[2];
+  if (slot < 0 || slot >= a.n_slots || cs < 0 || cs + sq > a.Lk) {
+    const int t = q_wave + l32;
+    if (t < sq) {
+      e_t* orow = reinterpret_cast<e_t*>(Ob + (int64_t)t * a.os[1]);
+      const e_t nan16 = __is_same(T, Bf16) ? (e_t)0x7fc0 : (e_t)0x7e00;
+#pragma unroll
+      for (int d = 32 * hl; d < 32 * hl + 32; ++d) orow[d] = nan16;
+    }
+    return;  // the whole workgroup: no barrier follows
+  }
+
+  const char* const Qb = a.q + (int64_t)b * a.qs[0] + (int64_t)h * a.qs[2];
+  const char* const Kc = a.kc + (int64_t)slot * a.kcs[0] + (int64_t)h * a.kcs[2];
+  const char* const Vc = a.vc + (int64_t)slot * a.vcs[0] + (int64_t)h * a.vcs[2];
+  const char* const Kn = a.kn + (int64_t)b * a.kns[0] + (int64_t)h * a.kns[2];
+  const char* const Vn = a.vn + (int64_t)b * a.vns[0] + (int64_t)h * a.vns[2];
+  char* const Kw = a.kc + (int64_t)slot * a.kcs[0] + (int64_t)h * a.kcs[2];
+  char* const Vw = a.vc + (int64_t)slot * a.vcs[0] + (int64_t)h * a.vcs[2];
+  const float c = a.c;
+
+  op_t qreg[4];
+  {
+    const int t = min(q_wave + l32, sq - 1);
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const u32x4 raw = load16(Qb + (int64_t)t * a.qs[1] + (ks * 16 + hl * 8) * 2);
+      u32x4 sc;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        sc[e] = Mfma<T>::pack(Mfma<T>::widen_lo(raw[e]) * c, Mfma<T>::widen_hi(raw[e]) * c);
+      asm volatile("" : "+v"(sc));
+      qreg[ks] = __builtin_bit_cast(op_t, sc);
+    }
+  }
+
+  // keys of this workgroup: [0, cs + min(sq, q_wg + kBM)); of this wavefront: up to its last row
+  const int k_lim = cs + min(sq, q_wg + kBM);
+  const int n_tiles = (k_lim + kBN - 1) / kBN;
+  const int n_sub = (k_lim + kBS - 1) / kBS;
+  const int n_sub_w = q_wave >= sq ? 0 : min(n_sub, (cs + min(sq, q_wave + 32) + kBS - 1) / kBS);
+  // new rows this workgroup appends: keys [app0, app1)
+  const int app0 = cs + q_wg, app1 = cs + min(sq, q_wg + kBM);
+
+  constexpr int kKPerThr = (kBN * kHeadDim / 8) / kThreads;
+  constexpr int kVDims = (kBN / 2) * kHeadDim / kThreads;
+  static_assert(kKPerThr == 1 && kVDims == 4, "tile staging shape");
+  u32x4 pk;
+  u32x2 pv[2];
+  const int vkp = tid / (kHeadDim / kVDims);
+  const int vd0 = (tid % (kHeadDim / kVDims)) * kVDims;
+  auto krow = [&](int key) -> const char* {
+    return key < cs ? Kc + (int64_t)key * a.kcs[1] : Kn + (int64_t)(key - cs) * a.kns[1];
+  };
+  auto vrow = [&](int key) -> const char* {
+    return key < cs ? Vc + (int64_t)key * a.vcs[1] : Vn + (int64_t)(key - cs) * a.vns[1];
+  };
+  auto gload = [&](int kt) __attribute__((always_inline)) {
+    pk = load16(krow(min(kt * kBN + (tid >> 3), k_lim - 1)) + (tid & 7) * 16);
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+      pv[i] = *reinterpret_cast<const u32x2*>(vrow(min(kt * kBN + 2 * vkp + i, k_lim - 1)) + vd0 * 2);
+  };
+  // tile kt into LDS buffer buf; the workgroup's own new rows also go to the cache
+  auto lstore = [&](int buf, int kt) __attribute__((always_inline)) {
+    const int kkey = kt * kBN + (tid >> 3);
+    if (kkey >= app0 && kkey < app1) *reinterpret_cast<u32x4*>(Kw + (int64_t)kkey * a.kcs[1] + (tid & 7) * 16) = pk;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int vkey = kt * kBN + 2 * vkp + i;
+      if (vkey >= app0 && vkey < app1) *reinterpret_cast<u32x2*>(Vw + (int64_t)vkey * a.vcs[1] + vd0 * 2) = pv[i];
+    }
+    *reinterpret_cast<u32x4*>(&sK[buf][(tid >> 3) * kPitchK + (tid & 7) * 8]) = pk;
+#pragma unroll
+    for (int e = 0; e < kVDims / 2; ++e) {
+      const uint32_t lo0 = pv[0][e] & 0xffffu, hi0 = pv[0][e] >> 16;
+      const uint32_t lo1 = pv[1][e] & 0xffffu, hi1 = pv[1][e] >> 16;
+      *reinterpret_cast<uint32_t*>(&sVt[buf][vt_index(vd0 + 2 * e, 2 * vkp)]) = lo0 | (lo1 << 16);
+      *reinterpret_cast<uint32_t*>(&sVt[buf][vt_index(vd0 + 2 * e + 1, 2 * vkp)]) = hi0 | (hi1 << 16);
+    }
+  };
+
+  const int pm = l32;
+  const int pi_row = 16 * ((pm >> 3) >> 1) + 8 * ((pm >> 2) & 1) + 4 * ((pm >> 3) & 1) + (pm & 3);
+
+  f32x16 acc_o[2];
+#pragma unroll
+  for (int x = 0; x < 16; ++x) acc_o[0][x] = acc_o[1][x] = 0.f;
+  float m_run = 0.f, l_part[4] = {0.f, 0.f, 0.f, 0.f};
+  op_t pprev[2];
+  const int qi = q_wave + l32;  // this lane's query row (past sq: a duplicate, never stored)
+
+  gload(0);
+  lstore(0, 0);
+  __syncthreads();
+
+  for (int s = 0; s <= n_sub; ++s) {
+    const int t = s >> 1;
+    const int kb = s & 1;
+    const int buf = t % kNumBuf;
+    if (kb == 0 && t + 1 < n_tiles) gload(t + 1);
+
+    const bool do_s = s < n_sub_w;
+    const bool do_pv = s >= 1 && s - 1 < n_sub_w;
+    f32x16 sacc;
+    mfma_priority<1>();
+    if (do_s) {
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const op_t ka = __builtin_bit_cast(
+            op_t, *reinterpret_cast<const u32x4*>(&sK[buf][(kb * 32 + pi_row) * kPitchK + ks * 16 + hl * 8]));
+        sacc = Mfma<T>::run(ka, qreg[ks], ks == 0 ? f32x16{} : sacc);
+      }
+    }
+    if (do_pv) {
+      const int sp = s - 1;
+      const int bufp = (sp >> 1) % kNumBuf;
+      const int kbp = sp & 1;
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+        for (int db = 0; db < 2; ++db) {
+          const op_t va = __builtin_bit_cast(
+              op_t, *reinterpret_cast<const u32x4*>(&sVt[bufp][vt_index(db * 32 + l32, kbp * 32 + ch * 16 + hl * 8)]));
+          acc_o[db] = Mfma<T>::run(va, pprev[ch], acc_o[db]);
+        }
+    }
+    mfma_priority<0>();
+    if (do_s) {
+      // mask: keys past this row's causal limit cs + qi (and past the workgroup's keys)
+      const int k0 = s * kBS;
+      if (k0 + kBS - 1 > cs + q_wave) {
+#pragma unroll
+        for (int x = 0; x < 16; ++x) {
+          const int key = k0 + 16 * (x >> 3) + 8 * hl + (x & 7);
+          if (key > cs + qi || key >= k_lim) sacc[x] = -INFINITY;
+        }
+      }
+      float m4[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        m4[j] = fmaxf(fmaxf(sacc[4 * j], sacc[4 * j + 1]), fmaxf(sacc[4 * j + 2], sacc[4 * j + 3]));
+      const float mx = half_swap_max(fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]))) - m_run;
+      if (__any(s == 0 || mx > kTau)) {
+        asm volatile("" ::: "memory");
+        const bool first = s == 0;
+        const float delta = first ? mx : fmaxf(mx, 0.f);
+        m_run += delta;
+        if (!first) {
+          const float alpha = fast_exp2(-delta);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) l_part[j] *= alpha;
+#pragma unroll
+          for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int x = 0; x < 16; ++x) acc_o[db][x] *= alpha;
+        }
+      }
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch) {
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float p0 = fast_exp2(sacc[ch * 8 + 2 * e] - m_run);
+          const float p1 = fast_exp2(sacc[ch * 8 + 2 * e + 1] - m_run);
+          w[e] = Mfma<T>::pack(p0, p1);
+          l_part[e] = l_part[e] + p0 + p1;
+        }
+        pprev[ch] = __builtin_bit_cast(op_t, w);
+      }
+    }
+    if (kb == 1 && t + 1 < n_tiles) {
+      lstore((t + 1) % kNumBuf, t + 1);
+      __syncthreads();
+    }
+  }
+
+  const float l_run = (l_part[0] + l_part[1]) + (l_part[2] + l_part[3]);
+  const float inv = 1.f / (l_run + __shfl_xor(l_run, 32));
+  if (qi < sq) {
+    e_t* orow = reinterpret_cast<e_t*>(Ob + (int64_t)qi * a.os[1]);
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int d = db * 32 + i * 8 + hl * 4;
+        u32x2 w;
+        w[0] = Mfma<T>::pack(acc_o[db][i * 4 + 0] * inv, acc_o[db][i * 4 + 1] * inv);
+        w[1] = Mfma<T>::pack(acc_o[db][i * 4 + 2] * inv, acc_o[db][i * 4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(orow + d) = w;
+      }
+  }
+}
+
 // Transposing LDS read (gfx950 ds_read_b64_tr_b16). Within each 16-lane group, lane i gets
 // element (i % 4) of the 8-byte chunks read by lanes 4c + i/4 (c = 0..3) of its group: with
 // every lane pointing at 4 consecutive dims of one key row, this turns a row-major
@@ -982,6 +1214,15 @@ hipError_t launch_typed(const DenseArgs& a, hipStream_t stream) {
 }
 
 }  // namespace
+
+hipError_t launch_kv_prefill(int dtype, const KvArgs& a, hipStream_t stream) {
+  const int n_qblk = (a.sq + 255) / 256;
+  const dim3 grid((unsigned)(a.B * n_qblk), (unsigned)a.H);
+  if (dtype == 2) hipLaunchKernelGGL(kv_prefill_kernel<Bf16>, grid, dim3(512), 0, stream, a);
+  else if (dtype == 1) hipLaunchKernelGGL(kv_prefill_kernel<F16>, grid, dim3(512), 0, stream, a);
+  else return hipErrorInvalidValue;
+  return hipGetLastError();
+}
 
 hipError_t launch_dense_mfma(int dtype, const DenseArgs& a, hipStream_t stream) {
   if (dtype == 1) return launch_typed<F16>(a, stream);

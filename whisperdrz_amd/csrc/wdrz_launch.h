@@ -38,6 +38,10 @@ void kv_workspace_layout(void* ws, int64_t units, KvArgs* a);
 // Launch the attention kernel: one workgroup per (row, key split); with n_splits > 1 the
 // partials merge in-launch through the workspace. dtype: 0 f32, 1 f16, 2 bf16.
 hipError_t launch_kv_attn(int dtype, const KvArgs& a, hipStream_t stream);
+// Prefill (16-bit, new rows given, sq >= kPrefillMinSq): 256-query causal MFMA blocks reading
+// keys below cache_seqlens from the slot and the rest from k_new / v_new, appending the new rows.
+constexpr int kPrefillMinSq = 40;
+hipError_t launch_kv_prefill(int dtype, const KvArgs& a, hipStream_t stream);
 
 // Dense MFMA attention (bf16 / fp16). Strides in ELEMENTS in [B, H, L, D] order.
 struct DenseArgs {
