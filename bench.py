@@ -344,7 +344,7 @@ def bench_decode(dev, steps: int, warmup: int) -> dict:
     res["config5_verify_self_plus_cross"] = run_graph(
         "config5 verify sq=5 (self+cross)", body5, bytes5_self + bytes5_cross,
         {"sum_L": sumL5, "bytes_self_per_layer": bytes5_self, "bytes_cross_per_layer": bytes5_cross},
-        kernels=("kv_mq_kernel<wdrz::Bf16, true>", "kv_mq_kernel<wdrz::Bf16, false>"),
+        kernels=("kv_mq_kernel<wdrz::Bf16, true, 8>", "kv_mq_kernel<wdrz::Bf16, false, 8>"),
     )
     # ---- prefill: a 224-token prompt into empty self caches (the window's first call) ----
     sqp = 224
@@ -1026,7 +1026,7 @@ def pmc_sample(dev) -> None:
     a calibration copy of 1 GiB (known HBM bytes), then 3 launches of the encoder kernel, of
     each decode kernel, of the DTW prep, compute_attention, the fused attention + prep, the
     cross-cache fill, the log-mel front end, the fp32 config 1 layer, one bf16 window and the
-    decode step's fc1 + GELU at the bench shapes (eager)."""
+    decode step's fc1 + GELU and split-K fc2, and the 224-row prefill at the bench shapes (eager)."""
     from whisperdrz_amd import flash_attn_with_kvcache, scaled_dot_product_attention
 
     n = 1 << 30
@@ -1120,6 +1120,24 @@ def pmc_sample(dev) -> None:
         lin = torch.nn.Linear(1280, 5120).to(dev, torch.bfloat16)
         linear_gelu(x, lin)
         torch.cuda.synchronize()
+    # the decode step's fc2 as split-K partials (three distinct weights), and the 224-row prefill
+    # into empty self caches (prefill kernel)
+    from whisperdrz_amd import linear_partials
+
+    x = torch.randn((64, 5120), generator=g, device=dev).to(torch.bfloat16)
+    for i in range(3):
+        lin = torch.nn.Linear(5120, 1280).to(dev, torch.bfloat16)
+        linear_partials(x, lin, 4)
+        torch.cuda.synchronize()
+    del x
+    zeros = torch.zeros(64, dtype=torch.int32, device=dev)
+    for i in range(3):
+        kv_s = _head_major_cache(64, 448, dev, 3100 + i)
+        qkv = torch.randn((3, 64, 224, H, D), generator=g, device=dev).to(torch.bfloat16)
+        flash_attn_with_kvcache(qkv[0], kv_s[0], kv_s[1], k=qkv[1], v=qkv[2], cache_seqlens=zeros,
+                                cache_batch_idx=slots, softmax_scale=0.125, causal=True)
+        torch.cuda.synchronize()
+        del kv_s, qkv
     log("[bench] pmc sample done")
 
 
