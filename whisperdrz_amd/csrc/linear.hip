@@ -187,11 +187,19 @@ void launch_t(const LinearArgs& a, hipStream_t stream) {
 
 hipError_t launch_linear(int dtype, const LinearArgs& a, hipStream_t stream) {
   if (a.M == 0 || a.N == 0) return hipSuccess;
-  // 16 features per workgroup (4 n_state / 16 = 320 workgroups for large-v3's fc1), X two
-  // chunks ahead: 32 features or five chunks ahead measured the same within noise at 64 rows and
-  // slower at 16
-  if (dtype == 2) launch_t<Bf16, 1, 2>(a, stream);
-  else launch_t<F16, 1, 2>(a, stream);
+  // 16 features per workgroup, X two chunks ahead; 32 features once 16 would give 320 or more
+  // workgroups (more than one per CU). Measured at 64 rows, 32 cold weights in a graph: fc1
+  // (5120 x 1280) 10.8 -> 10.1 us and fc2's split-K quarters (1280 x 5120) 10.3 -> 9.5 us with 32;
+  // the q/k/v projection (240 workgroups) 8.3 vs 9.9 us and the output projections' halves (160)
+  // 4.9 vs 5.7 us stay on 16; 64 features per workgroup is slower everywhere.
+  const int64_t wgs16 = (int64_t)((a.N + 15) / 16) * ((a.M + kLinRows - 1) / kLinRows) * (a.part ? a.n_split : 1);
+  if (wgs16 >= 320) {
+    if (dtype == 2) launch_t<Bf16, 2, 2>(a, stream);
+    else launch_t<F16, 2, 2>(a, stream);
+  } else {
+    if (dtype == 2) launch_t<Bf16, 1, 2>(a, stream);
+    else launch_t<F16, 1, 2>(a, stream);
+  }
   return hipGetLastError();
 }
 
