@@ -131,7 +131,7 @@ def bench_encoder(dev, steps: int, warmup: int) -> dict:
     return {
         "ms_per_step": ms_step,
         "tflops": tflops,
-        "single_window": {"workload": "one encoder layer B=1 H=20 L=1500 D=64 bf16 (dense_split_kernel<Bf16, 1>)",
+        "single_window": {"workload": "one encoder layer B=1 H=20 L=1500 D=64 bf16 (dense_split4_kernel<Bf16>)",
                           "us_per_layer": round(us1, 2), "tflops": round(t1, 1)},
         "roofline": {
             "bound": "mfma",
