@@ -362,10 +362,35 @@ def bench_decode(dev, steps: int, warmup: int) -> dict:
     us_p = timed_events(bodyp, steps, torch.cuda.current_stream()) * 1e3 / 8
     flop_p = 4.0 * Bs * H * D * sqp * (sqp + 1) / 2
     log(f"[bench] prefill sq={sqp} into empty caches: {us_p:.1f} us/layer, {flop_p / us_p / 1e6:.1f} TFLOP/s")
+    bytes_p = 6 * Bs * sqp * H * D * E  # Q, new K and V read, K and V appended, O written
     res["prefill_self_sq224"] = {
         "workload": "64 streams append a 224-token prompt to empty 448-row self caches (causal), bf16; "
-                    "kv_mq_kernel in 16-row query blocks",
-        "us_per_layer": round(us_p, 2), "tflops": round(flop_p / us_p / 1e6, 2)}
+                    "kv_prefill_kernel in 256-query blocks",
+        "us_per_layer": round(us_p, 2), "tflops": round(flop_p / us_p / 1e6, 2),
+        "roofline": {"bound": "hbm", "achieved": round(bytes_p / us_p / 1e3, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(bytes_p / us_p / 1e3 / PEAK_HBM_GBS, 4),
+                     "traffic": measured_traffic("kv_prefill_kernel<wdrz::Bf16>"), "bytes_per_layer": bytes_p}}
+
+    # ---- the same prompt's cross-attention over the 1500 encoder rows ----
+    def bodyc():
+        for i in range(8):
+            flash_attn_with_kvcache(qp[i][0], cross_kv[i][0], cross_kv[i][1], cache_batch_idx=slots,
+                                    softmax_scale=0.125, causal=False)
+
+    for _ in range(warmup):
+        bodyc()
+    us_c = timed_events(bodyc, steps, torch.cuda.current_stream()) * 1e3 / 8
+    flop_c = 4.0 * Bs * H * D * sqp * Lcross
+    bytes_c = 2 * Bs * Lcross * H * D * E + 2 * Bs * sqp * H * D * E  # K, V once; Q read, O written
+    log(f"[bench] prefill cross sq={sqp} over {Lcross} rows: {us_c:.1f} us/layer, {flop_c / us_c / 1e6:.1f} TFLOP/s, "
+        f"{bytes_c / us_c / 1e3:.0f} GB/s")
+    res["prefill_cross_sq224"] = {
+        "workload": f"64 streams, {sqp} prompt queries over {Lcross} cross rows (non-causal), bf16; "
+                    "kv_prefill_kernel in 256-query blocks",
+        "us_per_layer": round(us_c, 2), "tflops": round(flop_c / us_c / 1e6, 2),
+        "roofline": {"bound": "hbm", "achieved": round(bytes_c / us_c / 1e3, 1), "peak": PEAK_HBM_GBS,
+                     "unit": "GB/s", "frac": round(bytes_c / us_c / 1e3 / PEAK_HBM_GBS, 4), "traffic": None,
+                     "bytes_per_layer": bytes_c}}
     del self_kv, cross_kv, qp
     torch.cuda.empty_cache()
     return res

@@ -173,7 +173,9 @@ def test_prefill_self(cuda, dtype, sq):
 
 
 @pytest.mark.parametrize("dtype", LOWP)
-def test_prefill_cross(cuda, dtype):
-    """24 queries per stream over all 1500 cross rows (a prompt's cross-attention)."""
-    print(f"prefill cross dtype={dtype}", flush=True)
-    _run(cuda, dtype, 24, 1500, None, seed=71)
+@pytest.mark.parametrize("sq", [24, 64, 224])
+def test_prefill_cross(cuda, dtype, sq):
+    """sq queries per stream over all 1500 cross rows (a prompt's cross-attention): 16-row blocks
+    below 40 queries, the 256-query kernel from 40 on."""
+    print(f"prefill cross dtype={dtype} sq={sq}", flush=True)
+    _run(cuda, dtype, sq, 1500, None, seed=71 + sq, check_every=4 if sq > 64 else 1)

@@ -64,7 +64,7 @@ def test_self_attention(cuda, dtype, sq, layout):
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
 @pytest.mark.parametrize("Lmax", [1, 63, 100, 1500])
-@pytest.mark.parametrize("sq", [1, 5])
+@pytest.mark.parametrize("sq", [1, 5, 45])
 def test_cross_attention(cuda, dtype, Lmax, sq):
     print(f"cross dtype={dtype} Lmax={Lmax} sq={sq}", flush=True)
     _case(cuda, dtype, B=5, sq=sq, H=3, n_slots=7, Lmax=Lmax, layout="head_major", seed=200 + Lmax,

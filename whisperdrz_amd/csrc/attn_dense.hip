@@ -374,17 +374,18 @@ __global__ __launch_bounds__(NW * 64) void dense_mfma_kernel(DenseArgs a) {
 }
 
 // ============================================================================================
-// Prefill into the slot caches (flash_attn_with_kvcache with many new rows, sq >= kPrefillMinSq;
-// reference src/whisperdrz/model.py:42-63): for batch row b, query t of the sq new rows sees keys
+// Many-query cached attention (flash_attn_with_kvcache with sq >= kPrefillMinSq; reference
+// src/whisperdrz/model.py:42-67). Self (HAS_NEW, a prompt's prefill): for batch row b, query t of the sq new rows sees keys
 // [0, cs + t] of the row's cache after the append, cs = cache_seqlens[b] -- keys below cs from
 // the cache slot, the others straight from k_new / v_new -- and the workgroup appends its own
 // query rows' new keys and values to the cache. The step structure is the causal kernel's above
 // (256 queries in eight 32-query wavefronts, K/V tiles of 64 keys through three LDS buffers, V
 // transposed at staging), so each new row's keys are read ~sq/256 times instead of once per
-// 16-query block. Rows with invalid metadata (slot outside the pool, cs < 0 or cs + sq past the
-// cache) get NaN output and no append.
+// 16-query block. Cross (no new rows, the prompt's cross-attention): every query sees all Lk
+// cache rows and nothing is appended. Rows with invalid metadata (slot outside the pool; self:
+// cs < 0 or cs + sq past the cache) get NaN output and no append.
 // ============================================================================================
-template <typename T>
+template <typename T, bool HAS_NEW>
 __global__ __launch_bounds__(512, 4) void kv_prefill_kernel(KvArgs a) {
   constexpr int NW = 8;
   constexpr int kThreads = NW * 64;
@@ -406,13 +407,14 @@ __global__ __launch_bounds__(512, 4) void kv_prefill_kernel(KvArgs a) {
   const int b = (int)blockIdx.x % a.B;
   const int h = blockIdx.y;
   const int slot = a.bidx ? a.bidx[b] : b;
-  const int cs = a.seqlens[b];
+  // self: pre-append length; cross (no new rows): every cache row is a key
+  const int cs = HAS_NEW ? a.seqlens[b] : a.Lk;
   const int sq = a.sq;
   const int q_wg = qblk * kBM;
   const int q_wave = q_wg + wave * 32;
 
   char* const Ob = a.o + (int64_t)b * a.os[0] + (int64_t)h * a.os[2];
-  if (slot < 0 || slot >= a.n_slots || cs < 0 || cs + sq > a.Lk) {
+  if (slot < 0 || slot >= a.n_slots || (HAS_NEW && (cs < 0 || cs + sq > a.Lk))) {
     const int t = q_wave + l32;
     if (t < sq) {
       e_t* orow = reinterpret_cast<e_t*>(Ob + (int64_t)t * a.os[1]);
@@ -426,8 +428,8 @@ __global__ __launch_bounds__(512, 4) void kv_prefill_kernel(KvArgs a) {
   const char* const Qb = a.q + (int64_t)b * a.qs[0] + (int64_t)h * a.qs[2];
   const char* const Kc = a.kc + (int64_t)slot * a.kcs[0] + (int64_t)h * a.kcs[2];
   const char* const Vc = a.vc + (int64_t)slot * a.vcs[0] + (int64_t)h * a.vcs[2];
-  const char* const Kn = a.kn + (int64_t)b * a.kns[0] + (int64_t)h * a.kns[2];
-  const char* const Vn = a.vn + (int64_t)b * a.vns[0] + (int64_t)h * a.vns[2];
+  const char* const Kn = HAS_NEW ? a.kn + (int64_t)b * a.kns[0] + (int64_t)h * a.kns[2] : nullptr;
+  const char* const Vn = HAS_NEW ? a.vn + (int64_t)b * a.vns[0] + (int64_t)h * a.vns[2] : nullptr;
   char* const Kw = a.kc + (int64_t)slot * a.kcs[0] + (int64_t)h * a.kcs[2];
   char* const Vw = a.vc + (int64_t)slot * a.vcs[0] + (int64_t)h * a.vcs[2];
   const float c = a.c;
@@ -447,13 +449,15 @@ __global__ __launch_bounds__(512, 4) void kv_prefill_kernel(KvArgs a) {
     }
   }
 
-  // keys of this workgroup: [0, cs + min(sq, q_wg + kBM)); of this wavefront: up to its last row
-  const int k_lim = cs + min(sq, q_wg + kBM);
+  // keys of this workgroup: self [0, cs + min(sq, q_wg + kBM)), of this wavefront up to its last
+  // row; cross: all cs = Lk rows
+  const int k_lim = HAS_NEW ? cs + min(sq, q_wg + kBM) : cs;
   const int n_tiles = (k_lim + kBN - 1) / kBN;
   const int n_sub = (k_lim + kBS - 1) / kBS;
-  const int n_sub_w = q_wave >= sq ? 0 : min(n_sub, (cs + min(sq, q_wave + 32) + kBS - 1) / kBS);
-  // new rows this workgroup appends: keys [app0, app1)
-  const int app0 = cs + q_wg, app1 = cs + min(sq, q_wg + kBM);
+  const int n_sub_w =
+      q_wave >= sq ? 0 : HAS_NEW ? min(n_sub, (cs + min(sq, q_wave + 32) + kBS - 1) / kBS) : n_sub;
+  // new rows this workgroup appends: keys [app0, app1) (none for cross)
+  const int app0 = HAS_NEW ? cs + q_wg : 0, app1 = HAS_NEW ? cs + min(sq, q_wg + kBM) : 0;
 
   constexpr int kKPerThr = (kBN * kHeadDim / 8) / kThreads;
   constexpr int kVDims = (kBN / 2) * kHeadDim / kThreads;
@@ -463,10 +467,10 @@ __global__ __launch_bounds__(512, 4) void kv_prefill_kernel(KvArgs a) {
   const int vkp = tid / (kHeadDim / kVDims);
   const int vd0 = (tid % (kHeadDim / kVDims)) * kVDims;
   auto krow = [&](int key) -> const char* {
-    return key < cs ? Kc + (int64_t)key * a.kcs[1] : Kn + (int64_t)(key - cs) * a.kns[1];
+    return !HAS_NEW || key < cs ? Kc + (int64_t)key * a.kcs[1] : Kn + (int64_t)(key - cs) * a.kns[1];
   };
   auto vrow = [&](int key) -> const char* {
-    return key < cs ? Vc + (int64_t)key * a.vcs[1] : Vn + (int64_t)(key - cs) * a.vns[1];
+    return !HAS_NEW || key < cs ? Vc + (int64_t)key * a.vcs[1] : Vn + (int64_t)(key - cs) * a.vns[1];
   };
   auto gload = [&](int kt) __attribute__((always_inline)) {
     pk = load16(krow(min(kt * kBN + (tid >> 3), k_lim - 1)) + (tid & 7) * 16);
@@ -476,12 +480,14 @@ __global__ __launch_bounds__(512, 4) void kv_prefill_kernel(KvArgs a) {
   };
   // tile kt into LDS buffer buf; the workgroup's own new rows also go to the cache
   auto lstore = [&](int buf, int kt) __attribute__((always_inline)) {
-    const int kkey = kt * kBN + (tid >> 3);
-    if (kkey >= app0 && kkey < app1) *reinterpret_cast<u32x4*>(Kw + (int64_t)kkey * a.kcs[1] + (tid & 7) * 16) = pk;
+    if (HAS_NEW) {
+      const int kkey = kt * kBN + (tid >> 3);
+      if (kkey >= app0 && kkey < app1) *reinterpret_cast<u32x4*>(Kw + (int64_t)kkey * a.kcs[1] + (tid & 7) * 16) = pk;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
-      const int vkey = kt * kBN + 2 * vkp + i;
-      if (vkey >= app0 && vkey < app1) *reinterpret_cast<u32x2*>(Vw + (int64_t)vkey * a.vcs[1] + vd0 * 2) = pv[i];
+      for (int i = 0; i < 2; ++i) {
+        const int vkey = kt * kBN + 2 * vkp + i;
+        if (vkey >= app0 && vkey < app1) *reinterpret_cast<u32x2*>(Vw + (int64_t)vkey * a.vcs[1] + vd0 * 2) = pv[i];
+      }
     }
     *reinterpret_cast<u32x4*>(&sK[buf][(tid >> 3) * kPitchK + (tid & 7) * 8]) = pk;
 #pragma unroll
@@ -540,13 +546,13 @@ __global__ __launch_bounds__(512, 4) void kv_prefill_kernel(KvArgs a) {
     }
     mfma_priority<0>();
     if (do_s) {
-      // mask: keys past this row's causal limit cs + qi (and past the workgroup's keys)
+      // mask: keys past this row's causal limit cs + qi (self) and past the workgroup's keys
       const int k0 = s * kBS;
-      if (k0 + kBS - 1 > cs + q_wave) {
+      if (HAS_NEW ? k0 + kBS - 1 > cs + q_wave : k0 + kBS > k_lim) {
 #pragma unroll
         for (int x = 0; x < 16; ++x) {
           const int key = k0 + 16 * (x >> 3) + 8 * hl + (x & 7);
-          if (key > cs + qi || key >= k_lim) sacc[x] = -INFINITY;
+          if ((HAS_NEW && key > cs + qi) || key >= k_lim) sacc[x] = -INFINITY;
         }
       }
       float m4[4];
@@ -1446,9 +1452,16 @@ hipError_t launch_typed(const DenseArgs& a, hipStream_t stream) {
 hipError_t launch_kv_prefill(int dtype, const KvArgs& a, hipStream_t stream) {
   const int n_qblk = (a.sq + 255) / 256;
   const dim3 grid((unsigned)(a.B * n_qblk), (unsigned)a.H);
-  if (dtype == 2) hipLaunchKernelGGL(kv_prefill_kernel<Bf16>, grid, dim3(512), 0, stream, a);
-  else if (dtype == 1) hipLaunchKernelGGL(kv_prefill_kernel<F16>, grid, dim3(512), 0, stream, a);
-  else return hipErrorInvalidValue;
+  const bool has_new = a.kn != nullptr;
+  if (dtype == 2) {
+    if (has_new) hipLaunchKernelGGL((kv_prefill_kernel<Bf16, true>), grid, dim3(512), 0, stream, a);
+    else hipLaunchKernelGGL((kv_prefill_kernel<Bf16, false>), grid, dim3(512), 0, stream, a);
+  } else if (dtype == 1) {
+    if (has_new) hipLaunchKernelGGL((kv_prefill_kernel<F16, true>), grid, dim3(512), 0, stream, a);
+    else hipLaunchKernelGGL((kv_prefill_kernel<F16, false>), grid, dim3(512), 0, stream, a);
+  } else {
+    return hipErrorInvalidValue;
+  }
   return hipGetLastError();
 }
 

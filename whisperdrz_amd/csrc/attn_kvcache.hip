@@ -677,8 +677,9 @@ hipError_t launch_typed(const KvArgs& a, hipStream_t stream) {
   const bool has_new = a.kn != nullptr;
   const int sq_blk = a.n_qblocks > 1 ? kMaxSQ : a.sq;
   if constexpr (ElemBytes<T>::value == 2) {
-    // long prefills: 256-query causal blocks (attn_dense.hip), each new row's keys read ~sq/256 times
-    if (has_new && a.sq >= kPrefillMinSq) return launch_kv_prefill(__is_same(T, Bf16) ? 2 : 1, a, stream);
+    // many queries (a prompt's self and cross attention): 256-query MFMA blocks (attn_dense.hip),
+    // each key row read ~sq/256 times instead of once per 16-query block
+    if (a.sq >= kPrefillMinSq) return launch_kv_prefill(__is_same(T, Bf16) ? 2 : 1, a, stream);
     if (a.mq_rows == 16) {  // prefill in 16-row blocks on the matrix cores
       if (has_new)
         hipLaunchKernelGGL((kv_mq_kernel<T, true, 16>), grid, dim3(kWavesPerWg * 64), 0, stream, a);

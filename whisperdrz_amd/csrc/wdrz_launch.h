@@ -38,8 +38,9 @@ void kv_workspace_layout(void* ws, int64_t units, KvArgs* a);
 // Launch the attention kernel: one workgroup per (row, key split); with n_splits > 1 the
 // partials merge in-launch through the workspace. dtype: 0 f32, 1 f16, 2 bf16.
 hipError_t launch_kv_attn(int dtype, const KvArgs& a, hipStream_t stream);
-// Prefill (16-bit, new rows given, sq >= kPrefillMinSq): 256-query causal MFMA blocks reading
-// keys below cache_seqlens from the slot and the rest from k_new / v_new, appending the new rows.
+// Many-query cached attention (16-bit, sq >= kPrefillMinSq): 256-query MFMA blocks. Self (new
+// rows given): causal, keys below cache_seqlens from the slot and the rest from k_new / v_new, the
+// new rows appended. Cross (no new rows): all Lk cache rows, nothing appended.
 constexpr int kPrefillMinSq = 40;
 hipError_t launch_kv_prefill(int dtype, const KvArgs& a, hipStream_t stream);
 
