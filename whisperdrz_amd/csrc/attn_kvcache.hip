@@ -21,6 +21,12 @@
 // Append: keys at positions >= cache_seqlens[b] are read straight from k_new / v_new, never
 // from the cache, so the in-place write (done by the split whose key range holds the row)
 // cannot race with any read in the same launch.
+//
+// Which kernel serves a call (launch_typed): 16-bit calls of 2-8 query rows run on
+// kv_mq_kernel (MFMA over the rows, below), 9-39 rows in its 16-row blocks when those alone fill
+// the chip, and 40 or more rows (a prompt's self or cross attention) on kv_prefill_kernel in
+// attn_dense.hip (256-query MFMA blocks); single rows, the remaining multi-row shapes and fp32
+// caches run on kv_attn_kernel.
 #include "wdrz_common.h"
 #include "wdrz_launch.h"
 
