@@ -369,7 +369,7 @@ def bench_decode(dev, steps: int, warmup: int) -> dict:
         "us_per_layer": round(us_p, 2), "tflops": round(flop_p / us_p / 1e6, 2),
         "roofline": {"bound": "hbm", "achieved": round(bytes_p / us_p / 1e3, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(bytes_p / us_p / 1e3 / PEAK_HBM_GBS, 4),
-                     "traffic": measured_traffic("kv_prefill_kernel<wdrz::Bf16>"), "bytes_per_layer": bytes_p}}
+                     "traffic": measured_traffic("kv_prefill_kernel<wdrz::Bf16, true>"), "bytes_per_layer": bytes_p}}
 
     # ---- the same prompt's cross-attention over the 1500 encoder rows ----
     def bodyc():
