@@ -847,7 +847,7 @@ def logmel_cpu_baseline(budget_s: float = 8.0) -> dict:
     }
 
 
-DTW_KERNELS = ("dtw_rowcol_kernel<6>", "dtw_col_merge_kernel", "dtw_band_kernel<3, 384>")
+DTW_KERNELS = ("dtw_rowcol_kernel<6>", "dtw_col_merge_kernel", "dtw_seg_kernel")
 
 
 def dtw_cpu_baseline(budget_s: float = 12.0) -> dict:

@@ -64,6 +64,15 @@ def test_widths(cuda, width, A):
     (2, 2, 100, 1500, [150, 100], [1500, 1497]),
     (1, 2, 64, 2048, [64], [2047]),
     (1, 2, 20, 2100, [20], [2100]),             # A > 2048: separate row and column passes
+    # width 7 with A >= 256 (250-column wavefront segments; reflected columns at both ends of
+    # the first and last segment): one segment that is both, a last segment of 3 columns,
+    # T not a multiple of the 4 rows per wavefront
+    (2, 3, 21, 256, [21, 7], [256, 200]),
+    (1, 2, 9, 260, [9], [260]),
+    (2, 2, 13, 503, [13, 13], [503, 251]),
+    (1, 2, 6, 1504, [6], [1504]),
+    (1, 16, 5, 300, [5], [300]),                # the most heads this path unrolls
+    (1, 17, 5, 300, [5], [300]),                # one more: the column-strip filter
 ])
 def test_shapes(cuda, B, H, T, A, lens, caps):
     w = _scores((B, H, T, A), B * 1000 + T + A)
@@ -92,6 +101,19 @@ def test_strided_scores(cuda):
     out = dtw_prep(base.to(cuda)[:, :, :, :65], [21, 10], [65, 40], 7)
     torch.cuda.synchronize()
     _check(out, dtw_prep_ref(w.numpy(), [21, 10], [65, 40], 7), "dtw strided view")
+
+
+def test_strided_unaligned_rows_width7(cuda):
+    # rows that start 4 bytes past a 16-byte boundary and a row pitch that is not a multiple
+    # of 4: the separate row / column statistics passes, then the segment filter
+    base = _scores((2, 3, 11, 301), 9)
+    w = base[:, :, :, 1:290]
+    from whisperdrz_amd import dtw_prep
+
+    print("dtw strided unaligned width 7", flush=True)
+    out = dtw_prep(base.to(cuda)[:, :, :, 1:290], [11, 6], [289, 270], 7)
+    torch.cuda.synchronize()
+    _check(out, dtw_prep_ref(w.numpy(), [11, 6], [289, 270], 7), "dtw strided unaligned width 7")
 
 
 def test_batch_returns_host_array_and_is_deterministic(cuda):

@@ -13,8 +13,13 @@
 //   f[b,h,t,:]  = width-W median of z along c, reflect padding at 0 and A-1     (742-743)
 //   M[b,t,c]    = mean over h of f, c < C                                      (745-746)
 //
-// Three launches, each HBM-bound on W (4 bytes per valid score), all reading only the valid
-// columns c < caps[b]:
+// Width 7 (the reference's) with A >= 256, the path of every Whisper window: the statistics
+// in one pass (dtw_rowcol_kernel + dtw_col_merge_kernel, rows 16-byte aligned, A <= 2048)
+// and the filter in dtw_seg_kernel (one wavefront per 4 rows x 250 columns, no workgroup
+// barriers). Other widths and shapes take dtw_band_kernel (rows 16-byte aligned,
+// A <= 2048) or the three column-strip launches below.
+// The column-strip launches, each HBM-bound on W (4 bytes per valid score), all reading only
+// the valid columns c < caps[b]:
 //   dtw_row_stats_kernel   one wave per row (b,h,t): online max / sum of exp2 -> (m, 1/l);
 //                          16-byte loads when the rows are 16-byte aligned
 //   dtw_col_stats_kernel   one workgroup per (b, h, 64 columns): the column's p values stay in
@@ -801,21 +806,9 @@ __global__ __launch_bounds__(NT) void dtw_band_kernel(DtwArgs a) {
 
   issue(0, pf[0]);
   issue(1, pf[1]);
-  if constexpr (PAD == 3 && NT >= 384) {
-    // Whisper's shape (width 7, 1500 audio columns) fully unrolled: with no loop-carried load
-    // registers each wait covers exactly the head it consumes. (In a loop the compiler waits
-    // for every outstanding load at the top of each head.)
-    static_for<kBandMaxHeads / 2>([&](int i) __attribute__((always_inline)) {
-      if (2 * i < a.H) {
-        head(2 * i, pf[0]);
-        head(2 * i + 1, pf[1]);
-      }
-    });
-  } else {
-    for (int h = 0; h < a.H; h += 2) {
-      head(h, pf[0]);
-      head(h + 1, pf[1]);
-    }
+  for (int h = 0; h < a.H; h += 2) {
+    head(h, pf[0]);
+    head(h + 1, pf[1]);
   }
   if (tid < ((a.C + 3) >> 2)) {
 #pragma unroll
@@ -826,6 +819,154 @@ __global__ __launch_bounds__(NT) void dtw_band_kernel(DtwArgs a) {
         for (int i = 0; i < 4; ++i)
           if (4 * tid + i < a.C) dst[i] = acc[r][i] / (float)a.H;
       }
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------------------------
+// Width-7 normalise + median + head mean, one wavefront per (b, 4 rows, 250-column segment).
+// Lane L holds columns s0 - 3 + 4L .. +3 of each row (the segment's 250 output columns plus
+// 3 on each side), so every window lies inside its own wavefront's strip: the strip goes
+// through a wavefront-private LDS row and no workgroup barrier is needed. Every lane reads
+// its 4 columns with one 16-byte load (4-byte aligned) at an address clamped into the row;
+// in the first and last segment the lanes whose columns leave the row then take their values
+// from the strip at the reflected columns (torch's reflect padding), one LDS gather per row.
+// ---------------------------------------------------------------------------------------------
+constexpr int kSegOut = 250;
+constexpr int kSegRows = 4;  // rows per wavefront (2, 6 and 8 measured slower)
+constexpr int kSegPf = 2;    // heads in flight per wavefront (3 measured slower)
+constexpr int kSegWaves = 4;
+constexpr int kSegPitch = 272;  // floats per strip row (256 written + the last lanes' overrun)
+typedef float f32x4u __attribute__((ext_vector_type(4), aligned(4)));
+
+__global__ __launch_bounds__(kSegWaves * 64) void dtw_seg_kernel(DtwArgs a, int n_seg) {
+  __shared__ f32x4 strips[kSegWaves][kSegRows * kSegPitch / 4];
+  const int lane = threadIdx.x & 63;
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform: scalar indexing
+  const int n_rg = (a.T + kSegRows - 1) / kSegRows;
+  const int item = blockIdx.x * kSegWaves + w;
+  if (item >= a.B * n_rg * n_seg) return;  // whole wavefronts; no barriers below
+  const int seg = item % n_seg;
+  const int rest = item / n_seg;
+  const int t0 = (rest % n_rg) * kSegRows;
+  const int b = a.B - 1 - rest / n_rg;  // last batch row first: the statistics pass ended there
+  const int s0 = seg * kSegOut;
+  const int n_rows = min(kSegRows, a.T - t0);
+  const int cap = clamp_cap(a.caps[b], a.A);
+  const int len = a.lens[b];
+  const int n_out = min(kSegOut, a.C - s0);
+  const int oc = 4 * lane;
+  float* dst = a.out + b * a.os[0] + (int64_t)t0 * a.os[1] + s0 + oc;
+  if (cap <= 0 || len <= 0) {  // 0/0 in the reference: the whole batch row is NaN
+    for (int r = 0; r < n_rows; ++r)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (oc + i < n_out) dst[r * a.os[1] + i] = __builtin_nanf("");
+    return;
+  }
+  f32x4* const strip = strips[w];
+  const int sb = s0 - 3;                             // column of strip slot 0
+  const int lc = min(max(sb + 4 * lane, 0), a.A - 4);  // first column this lane loads
+  const bool edge = sb < 0 || sb + 4 * 64 > a.A;       // wave-uniform
+  bool valid[4];
+  int src[4];  // edge segments: the strip slot holding the reflected column of slot 4L + i
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    valid[i] = lc + i < cap;
+    int c = sb + 4 * lane + i;
+    c = c < 0 ? -c : c;
+    c = c > a.A - 1 ? 2 * (a.A - 1) - c : c;
+    c = min(max(c, 0), a.A - 1);
+    const int owner = (c - sb) >> 2;
+    src[i] = 4 * owner + c - min(max(sb + 4 * owner, 0), a.A - 4);
+  }
+
+  struct Prefetch {
+    f32x4u x[kSegRows];
+    f32x4u c[2];  // (mean, 1/std) of the 4 columns
+    float2 r[kSegRows];
+  };
+  Prefetch pf[kSegPf];
+  auto issue = [&](int h, Prefetch& q) __attribute__((always_inline)) {
+    h = min(h, a.H - 1);
+    const int64_t bh = (int64_t)b * a.H + h;
+    const float* rows = a.w + b * a.ws[0] + h * a.ws[1];
+    const float2* cs = a.cs + bh * a.cpitch + lc;
+    q.c[0] = *reinterpret_cast<const f32x4u*>(cs);
+    q.c[1] = *reinterpret_cast<const f32x4u*>(cs + 2);
+#pragma unroll
+    for (int r = 0; r < kSegRows; ++r) {
+      const int t = min(t0 + r, a.T - 1);
+      q.r[r] = a.rs[bh * a.T + t];
+      q.x[r] = *reinterpret_cast<const f32x4u*>(rows + (int64_t)t * a.ws[2] + lc);
+    }
+  };
+  float acc[kSegRows][4];
+#pragma unroll
+  for (int r = 0; r < kSegRows; ++r)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) acc[r][i] = 0.f;
+
+  auto head = [&](Prefetch& q, int h_next) __attribute__((always_inline)) {
+    const float cmean[4] = {q.c[0][0], q.c[0][2], q.c[1][0], q.c[1][2]};
+    const float crstd[4] = {q.c[0][1], q.c[0][3], q.c[1][1], q.c[1][3]};
+#pragma unroll
+    for (int r = 0; r < kSegRows; ++r) {
+      f32x4 z;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float v = (softmax_value(q.x[r][i], q.r[r]) - cmean[i]) * crstd[i];
+        z[i] = valid[i] ? v : 0.f;
+      }
+      strip[r * (kSegPitch / 4) + lane] = z;
+    }
+    issue(h_next, q);  // refill this slot
+    // The strip rows are written and read by this wavefront's own lanes: LDS executes one
+    // wavefront's instructions in order, so only the compiler must not reorder them.
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    if (edge) {
+      const float* sf = reinterpret_cast<const float*>(strip);
+      f32x4 g[kSegRows];
+#pragma unroll
+      for (int r = 0; r < kSegRows; ++r)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) g[r][i] = sf[r * kSegPitch + src[i]];
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+#pragma unroll
+      for (int r = 0; r < kSegRows; ++r) strip[r * (kSegPitch / 4) + lane] = g[r];
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    }
+#pragma unroll
+    for (int r = 0; r < kSegRows; ++r) {
+      float win[12];
+#pragma unroll
+      for (int j = 0; j < 3; ++j) {
+        const f32x4 v = strip[r * (kSegPitch / 4) + lane + j];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) win[4 * j + i] = v[i];
+      }
+      float x10[10];
+#pragma unroll
+      for (int i = 0; i < 10; ++i) x10[i] = win[i];
+      float med[4];
+      median7_x4(x10, med);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[r][i] += med[i];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+  };
+  static_for<kSegPf>([&](int i) __attribute__((always_inline)) { issue(i, pf[i]); });
+  // Whisper's shape fully unrolled: with no loop-carried load registers each wait covers
+  // exactly the head it consumes.
+  static_for<kBandMaxHeads>([&](int h) __attribute__((always_inline)) {
+    if (h < a.H) head(pf[h % kSegPf], h + kSegPf);
+  });
+#pragma unroll
+  for (int r = 0; r < kSegRows; ++r) {
+    if (r < n_rows) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (oc + i < n_out) dst[r * a.os[1] + i] = acc[r][i] / (float)a.H;
     }
   }
 }
@@ -1371,14 +1512,17 @@ hipError_t launch_dtw_prep(DtwArgs a, hipStream_t stream) {
     hipLaunchKernelGGL(dtw_col_stats_kernel, dim3((need + kColBlock - 1) / kColBlock, a.H, a.B), dim3(512), 0,
                        stream, a);
   }
+  if (a.pad == 3 && a.A >= 4 * 64 && a.H <= kBandMaxHeads) {  // the reference's width 7
+    const int n_seg = (a.C + kSegOut - 1) / kSegOut;
+    const int64_t waves = (int64_t)a.B * ((a.T + kSegRows - 1) / kSegRows) * n_seg;
+    hipLaunchKernelGGL(dtw_seg_kernel, dim3((unsigned)((waves + kSegWaves - 1) / kSegWaves)), dim3(kSegWaves * 64), 0,
+                       stream, a, n_seg);
+    return hipGetLastError();
+  }
   if (a.vec && a.A % 4 == 0 && a.A <= 4 * kBandMaxA4 && a.H <= kBandMaxHeads) {
     const dim3 grid((a.T + kBandRows - 1) / kBandRows, a.B);
-    const int nt = 128 * ((((a.A + 3) / 4) + 127) / 128);  // one float4 column per thread
-    if (a.pad == 3) {  // the reference's width 7: a block size per width of the audio axis
-      if (nt == 128) hipLaunchKernelGGL((dtw_band_kernel<3, 128>), grid, dim3(128), 0, stream, a);
-      else if (nt == 256) hipLaunchKernelGGL((dtw_band_kernel<3, 256>), grid, dim3(256), 0, stream, a);
-      else if (nt == 384) hipLaunchKernelGGL((dtw_band_kernel<3, 384>), grid, dim3(384), 0, stream, a);
-      else hipLaunchKernelGGL((dtw_band_kernel<3, 512>), grid, dim3(512), 0, stream, a);
+    if (a.pad == 3) {  // A < 256: one float4 column per thread
+      hipLaunchKernelGGL((dtw_band_kernel<3, 128>), grid, dim3(128), 0, stream, a);
       return hipGetLastError();
     }
     switch (a.pad) {
