@@ -243,10 +243,14 @@ __global__ __launch_bounds__(512) void dtw_col_stats_kernel(DtwArgs a) {
 // through LDS and the chunk's partial (mean, M2) per column is stored for dtw_col_merge_kernel.
 // ---------------------------------------------------------------------------------------------
 constexpr int kRcWaves = 4;
-// Workgroups of the fused pass that fit on the GPU at once (256 CUs x 3 four-wave workgroups at
-// up to 168 VGPRs). The rows of each (b, h) are cut into as many chunks as keep B*H*chunks
-// within one such round, so no workgroup runs in a second, mostly idle round.
+// Workgroups that fit on the GPU at once: 256 CUs x 3 four-wave workgroups at up to 168 VGPRs
+// (the workspace's chunking and the fused pass's), x 2 at up to 256 (dtw_rowcol_kernel). The
+// rows of each (b, h) are cut into as many chunks as keep B*H*chunks within one such round, so
+// no workgroup runs in a second, mostly idle round.
 constexpr int kRcSlots = 768;
+constexpr int kRcSlotsRowcol = 512;
+// Bytes of W the statistics pass leaves in the Infinity Cache for the filter pass.
+constexpr int64_t kMallKeepBytes = 224ll << 20;
 
 __device__ __forceinline__ void chan_merge(float na, float& ma, float& qa, float nb, float mb, float qb) {
   if (nb == 0.f) return;
@@ -256,9 +260,8 @@ __device__ __forceinline__ void chan_merge(float na, float& ma, float& qa, float
   qa += qb + d * d * (na * nb / n);
 }
 
-template <int NK>
-__global__ __launch_bounds__(256) void dtw_rowcol_kernel(DtwArgs a) {
-  const int chunk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+template <int NK, bool NT>
+__device__ __attribute__((always_inline)) inline void rowcol_body(const DtwArgs& a, int chunk, int h, int b) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int cap = clamp_cap(a.caps[b], a.A);
   const int len = a.lens[b];
@@ -292,7 +295,9 @@ __global__ __launch_bounds__(256) void dtw_rowcol_kernel(DtwArgs a) {
     const float* src = base + (int64_t)min(t, t_end - 1) * a.ws[2];
 #pragma unroll
     for (int j = 0; j < NK; ++j) {
-      const f32x4 v = *reinterpret_cast<const f32x4*>(src + colc[j]);
+      f32x4 v;
+      if constexpr (NT) v = __builtin_nontemporal_load(reinterpret_cast<const f32x4*>(src + colc[j]));
+      else v = *reinterpret_cast<const f32x4*>(src + colc[j]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) x[j][i] = v[i];
     }
@@ -339,16 +344,16 @@ __global__ __launch_bounds__(256) void dtw_rowcol_kernel(DtwArgs a) {
     }
   };
 
-  // Two rows in flight while a row is processed: three row buffers in rotation, six rows per
-  // unrolled iteration so each buffer keeps its role across iterations.
-  float xb[3][NK][4];
-  load_row(t_first, xb[0]);
-  load_row(t_first + 1, xb[1]);
-  for (int t6 = t_first; t6 < t_end; t6 += 6) {
-    static_for<6>([&](int r) __attribute__((always_inline)) {
-      const int t = t6 + r;
-      load_row(t + 2, xb[(r + 2) % 3]);
-      if (t < t_end) row_step(t, xb[r % 3]);
+  // Three rows in flight while a row is processed: four row buffers in rotation, eight rows
+  // per unrolled iteration so each buffer keeps its role across iterations.
+  constexpr int NB = 4;
+  float xb[NB][NK][4];
+  static_for<NB - 1>([&](int r) __attribute__((always_inline)) { load_row(t_first + r, xb[r]); });
+  for (int t8 = t_first; t8 < t_end; t8 += 2 * NB) {
+    static_for<2 * NB>([&](int r) __attribute__((always_inline)) {
+      const int t = t8 + r;
+      load_row(t + NB - 1, xb[(r + NB - 1) % NB]);
+      if (t < t_end) row_step(t, xb[r % NB]);
     });
   }
 
@@ -399,6 +404,16 @@ __global__ __launch_bounds__(256) void dtw_rowcol_kernel(DtwArgs a) {
       }
     }
   }
+}
+
+// Batch rows b < nt_b are read with nontemporal loads (streamed past the caches: 4.5 -> 5.3
+// TB/s); the last ones normally, so that they are still in the 256 MB Infinity Cache when the
+// filter pass, which starts from the last batch row, reads them again.
+template <int NK>
+__global__ __launch_bounds__(256) void dtw_rowcol_kernel(DtwArgs a) {
+  const int chunk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  if (b < a.nt_b) rowcol_body<NK, true>(a, chunk, h, b);
+  else rowcol_body<NK, false>(a, chunk, h, b);
 }
 
 // Final column statistics from the chunk partials: cs = (mean, 1/sqrt(max(var, 1e-12))) with
@@ -1463,8 +1478,8 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 }  // namespace
 
 // Rows per chunk of the fused statistics pass (a multiple of the 4 waves), from sizes only.
-int dtw_chunk_rows(int64_t B, int64_t H, int64_t T) {
-  int64_t n_chunks = kRcSlots / (B * H);
+int dtw_chunk_rows(int64_t B, int64_t H, int64_t T, int slots = kRcSlots) {
+  int64_t n_chunks = slots / (B * H);
   if (n_chunks < 1) n_chunks = 1;
   int64_t rows = (T + n_chunks - 1) / n_chunks;
   rows = (rows + kRcWaves - 1) / kRcWaves * kRcWaves;
@@ -1499,6 +1514,10 @@ hipError_t launch_dtw_prep(DtwArgs a, hipStream_t stream) {
   // Columns the filter reads: [0, min(A, C + pad)).
   const int need = a.C + a.pad < a.A ? a.C + a.pad : a.A;
   if (a.vec && a.A % 4 == 0 && a.A <= 2048) {
+    a.rc_rows = dtw_chunk_rows(a.B, a.H, a.T, kRcSlotsRowcol);  // no more chunks than the workspace's
+    const int64_t slab = (int64_t)a.H * a.T * a.A * 4;
+    const int64_t keep = kMallKeepBytes / slab;
+    a.nt_b = keep >= a.B ? 0 : (int)(a.B - keep);
     const dim3 grid((a.T + a.rc_rows - 1) / a.rc_rows, a.H, a.B);
     if (a.A <= 512) hipLaunchKernelGGL(dtw_rowcol_kernel<2>, grid, dim3(256), 0, stream, a);
     else if (a.A <= 1024) hipLaunchKernelGGL(dtw_rowcol_kernel<4>, grid, dim3(256), 0, stream, a);

@@ -74,6 +74,7 @@ struct DtwArgs {
   int cpitch;   // A rounded up to a multiple of 4
   int rc_rows;  // rows per chunk of the fused statistics pass
   int vec;     // rows of W start 16-byte aligned (set by the launcher)
+  int nt_b;    // statistics pass: batch rows below this are read nontemporally (set by the launcher)
   int64_t ws[3];  // W strides b, h, t
   int64_t os[2];  // out strides b, t
 };
