@@ -227,9 +227,13 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
   const int wave = tid / 64;
   const int lane = tid % 64;
 
-  const int b = blockIdx.x / a.n_qblocks;
-  const int t0 = (blockIdx.x % a.n_qblocks) * SQ;
-  const int h = blockIdx.y;
+  // Heads fastest in the dispatch order: the workgroups running at once read one slot's heads,
+  // which lie next to each other in the head-major cache (config 3: 17.4 -> 15.5 us against
+  // batch rows fastest).
+  const int h = (int)(blockIdx.x % (unsigned)a.H);
+  const int bq = (int)(blockIdx.x / (unsigned)a.H);
+  const int b = bq / a.n_qblocks;
+  const int t0 = (bq % a.n_qblocks) * SQ;
   const int split = blockIdx.z;
   const int nq = min(SQ, a.sq - t0);
 
@@ -531,9 +535,10 @@ __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
   const int qi = lane & 15;  // query slot of this lane
   const int gq = lane >> 4;  // 16-lane group
 
-  const int b = blockIdx.x / a.n_qblocks;
-  const int t0 = (blockIdx.x % a.n_qblocks) * SQ;  // first query row of this block
-  const int h = blockIdx.y;
+  const int h = (int)(blockIdx.x % (unsigned)a.H);  // heads fastest, as in kv_attn_kernel
+  const int bq = (int)(blockIdx.x / (unsigned)a.H);
+  const int b = bq / a.n_qblocks;
+  const int t0 = (bq % a.n_qblocks) * SQ;  // first query row of this block
   const int split = blockIdx.z;
   const int nq = min(SQ, a.sq - t0);
 
@@ -679,7 +684,9 @@ __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
 
 template <typename T>
 hipError_t launch_typed(const KvArgs& a, hipStream_t stream) {
-  dim3 grid(a.B * a.n_qblocks, a.H, a.n_splits);
+  const int64_t n_units = (int64_t)a.B * a.n_qblocks * a.H;
+  if (n_units > 0x7fffffff) return hipErrorInvalidValue;
+  dim3 grid((unsigned)n_units, 1, a.n_splits);
   const bool has_new = a.kn != nullptr;
   const int sq_blk = a.n_qblocks > 1 ? kMaxSQ : a.sq;
   if constexpr (ElemBytes<T>::value == 2) {
