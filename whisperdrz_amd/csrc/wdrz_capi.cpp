@@ -316,6 +316,7 @@ int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, co
     }
   a.c = softmax_scale * 1.4426950408889634f;
   const int64_t units = B * a.n_qblocks * H;
+  if (units > 0x7fffffff) return fail(WDRZ_EUNSUPPORTED, "B * ceil(sq / rows per block) * H exceeds 2^31 - 1");
   wdrz::kv_split_plan(units, Lmax, &a.n_splits, &a.split_len);
   const size_t need = wdrz::kv_workspace_bytes(units, sq < 8 ? sq : 8, a.n_splits);
   if (need > 0) {
