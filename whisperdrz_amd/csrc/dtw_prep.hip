@@ -850,7 +850,7 @@ __global__ __launch_bounds__(NT) void dtw_band_kernel(DtwArgs a) {
 constexpr int kSegOut = 250;
 constexpr int kSegRows = 4;  // rows per wavefront (2, 6 and 8 measured slower)
 constexpr int kSegPf = 2;    // heads in flight per wavefront (3 measured slower)
-constexpr int kSegWaves = 4;
+constexpr int kSegWaves = 4;  // independent wavefronts per workgroup (1, 2 and 8 measured slower)
 constexpr int kSegPitch = 272;  // floats per strip row (256 written + the last lanes' overrun)
 typedef float f32x4u __attribute__((ext_vector_type(4), aligned(4)));
 
