@@ -55,6 +55,11 @@ const char* wdrz_last_error(void);
 /* ABI version of this library (bumped on any signature change). */
 int wdrz_abi_version(void);
 
+/* Hash of the sources the library was built from (kernels, C-ABI layer, this header, build
+ * flags). No counterpart in the reference: the Python loader compares it with the tree it runs
+ * from and refuses a library built from other sources. */
+const char* wdrz_build_id(void);
+
 /*
  * Dense scaled-dot-product attention, O = softmax(scale * Q K^T [+ causal mask]) V, per (b, h).
  *
@@ -74,7 +79,9 @@ int wdrz_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* 
                   float scale, int causal, void* stream);
 
 /*
- * Workspace (bytes) that wdrz_attn_kvcache needs for these sizes. 0 means none is needed.
+ * Workspace (bytes) that wdrz_attn_kvcache needs for these sizes. 0 means none is needed:
+ * enough rows to fill the chip (B * ceil(sq / 8) * H >= 1024), or sq >= 40 (those calls never
+ * split their keys).
  * No counterpart in the reference: flash-attn allocates its split-KV scratch internally; this
  * library leaves allocation to the caller so calls can be captured into a hipGraph.
  */
@@ -106,8 +113,10 @@ size_t wdrz_attn_kvcache_workspace_size(int64_t B, int64_t sq, int64_t H, int64_
  *   (cache_seqlens is ignored, as in the fallback).
  * `causal` is accepted for signature parity; as in the fallback, the mask is decided by
  *   whether k_new is given.
- * Duplicate cache_batch_idx entries with k_new given write the same cache rows from several
- *   batch rows; which write lands is unspecified (as with flash-attn).
+ * Repeated cache_batch_idx entries with k_new given follow the reference fallback's order
+ *   (model.py:51-57): a cache position ends up holding the new row of the LAST batch row whose
+ *   region [cache_seqlens, cache_seqlens + sq) covers it, and every row attends over the cache
+ *   after all appends.
  * workspace: device buffer of at least wdrz_attn_kvcache_workspace_size(...) bytes, 256-byte
  *   aligned (may be NULL when that is 0). It holds per-row arrival counters and partials and
  *   must be all-zero when a call starts: zero-fill the buffer once after allocating it; every
@@ -135,7 +144,11 @@ int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, co
  * Limit: calls whose workspace (wdrz_attn_kvcache_workspace_size) exceeds
  * WDRZ_NOALLOC_SCRATCH_BYTES are rejected with WDRZ_EUNSUPPORTED (the split plan never asks
  * for more than ~4.33 MB at head_dim 64). The array is set up (address taken, cleared by a
- * kernel on `stream`) on the first call on each device and kept until the process ends.
+ * kernel on `stream`) on the first call on each device and kept until the process ends. The
+ * array is zero when the code object loads (a zero-initialised device global) and every completed
+ * call leaves it zero, so a first call made under graph capture, whose clearing kernel is then
+ * recorded into the graph rather than run, still starts from zero, both in eager calls made
+ * before the first replay and in every replay.
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU race; serialise
  * them or use wdrz_attn_kvcache with separate workspaces.
  */

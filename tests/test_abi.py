@@ -48,6 +48,14 @@ def test_abi_version(lib):
     assert lib.wdrz_abi_version() == _lib.ABI_VERSION
 
 
+def test_build_id_matches_the_tree(lib):
+    """The loaded library was built from these sources (load() refuses any other)."""
+    from whisperdrz_amd.build import source_hash
+
+    assert lib.wdrz_build_id().decode() == source_hash()
+    assert len(source_hash()) == 16
+
+
 def test_workspace_size_plan(lib):
     # many rows: one workgroup per row, no workspace; few rows: split keys, workspace needed
     assert lib.wdrz_attn_kvcache_workspace_size(64, 1, 20, 64, 448) == 0
@@ -56,6 +64,11 @@ def test_workspace_size_plan(lib):
     assert small > 0 and small % 4 == 0
     assert lib.wdrz_attn_kvcache_workspace_size(1, 5, 20, 64, 1500) > small
     assert lib.wdrz_attn_kvcache_workspace_size(0, 1, 20, 64, 448) == 0
+    # 40+ query rows never split their keys (the prefill kernel's route): no workspace, however
+    # few rows there are
+    assert lib.wdrz_attn_kvcache_workspace_size(1, 39, 20, 64, 448) > 0
+    assert lib.wdrz_attn_kvcache_workspace_size(1, 40, 20, 64, 448) == 0
+    assert lib.wdrz_attn_kvcache_workspace_size(1, 224, 20, 64, 1500) == 0
 
 
 def _strides(*s):
@@ -305,6 +318,7 @@ def call_linear(lib, **over):
     (dict(b=FAKE + 1), 1, "2-byte aligned"),
     (dict(xs=1000), 1, "shorter than the rows"),
     (dict(xs=1284), 1, "16-byte aligned"),
+    (dict(M=65535 * 64 + 1), 2, "sizes too large"),
 ])
 def test_linear_rejects_bad_arguments(lib, over, code, msg):
     assert call_linear(lib, **over) == code
@@ -360,6 +374,8 @@ def call_add_ln_partials(lib, **over):
     (dict(db=None), 1, "delta_bias is NULL"),
     (dict(p=FAKE + 4), 1, "partials is not 16-byte aligned"),
     (dict(ys=1284), 1, "16-byte aligned"),
+    (dict(xs=1272), 1, "shorter than the rows"),
+    (dict(ys=1272), 1, "shorter than the rows"),
 ])
 def test_add_layernorm_partials_rejects_bad_arguments(lib, over, code, msg):
     assert call_add_ln_partials(lib, **over) == code

@@ -41,16 +41,11 @@ def test_append_outside_the_cache_raises(cs, sq):
         check_kvcache_metadata(_arr(*cs), _arr(0), sq, 1, 448, True)
 
 
-def test_overlapping_append_regions_raise():
-    # rows 0 and 2 write [10, 15) and [12, 17) of slot 4
-    with pytest.raises(ValueError, match="rows 0 and 2 append overlapping regions of slot 4"):
-        check_kvcache_metadata(_arr(10, 0, 12), _arr(4, 1, 4), 5, 5, 448, True)
-
-
-def test_duplicate_slots_with_identical_regions_only_warn():
-    # the padded rows of a bucketed decode graph repeat an active slot with its own length
-    with pytest.warns(UserWarning, match="duplicate cache_batch_idx"):
-        check_kvcache_metadata(_arr(7, 3, 7), _arr(2, 0, 2), 1, 3, 448, True)
+def test_repeated_slots_are_valid():
+    # the padded rows of a bucketed decode graph repeat an active slot, with its length or not:
+    # the appends apply in batch order, as in the fallback (model.py:51-54)
+    check_kvcache_metadata(_arr(7, 3, 7), _arr(2, 0, 2), 1, 3, 448, True)
+    check_kvcache_metadata(_arr(10, 0, 12), _arr(4, 1, 4), 5, 5, 448, True)
 
 
 def _run(env_extra, code):

@@ -93,8 +93,29 @@ def test_config1_fp32_full_shape(cuda):
     print(f"config1 max|diff|={err:.3e} elementwise-within(rtol=1e-5, atol=1e-6)={frac:.6f}")
 
 
-def test_config2_layer_bf16_sample(cuda):
-    """Config 2 shape (B=16, H=20, L=1500, bf16): whole-batch run, two (b, h) pairs checked."""
+def _config2_oracle_heads():
+    """(b, h) pairs of config 2 that dense_fwd_kernel's timed grid puts on every XCD in every round
+    of workgroups, plus every head of the partial last round. The launch has 960 workgroups
+    (320 heads x 3 query blocks); hardware id i runs on XCD i % 8 in round i // 256 and computes
+    the logical tile 120 * (i % 8) + i // 8 (remap_xcd), i.e. head tile // 3."""
+    by_slot, last = {}, set()
+    for t in range(960):
+        xcd, local = t // 120, t % 120
+        hw = local * 8 + xcd
+        rnd = hw // 256
+        by_slot.setdefault((xcd, rnd), []).append(t // 3)
+        if rnd == 3:
+            last.add(t // 3)
+    sel = {v[len(v) // 2] for v in by_slot.values()} | last
+    assert len(by_slot) == 32
+    return sorted(sel)
+
+
+def test_config2_layer_bf16_all_heads(cuda):
+    """Config 2 shape (B=16, H=20, L=1500, bf16), the launch the bench times: all 320 heads
+    against a float64 evaluation of softmax(q k^T / 8) v on the GPU, and the 88 heads that cover
+    every XCD in every round of the remapped grid (all heads of the partial last round among
+    them) against the float64 numpy oracle; 2e-2 max-abs."""
     B, H, L, D = 16, 20, 1500, 64
     q = randn((B, L, H, D), 11, torch.bfloat16).to(cuda)
     k = randn((B, L, H, D), 12, torch.bfloat16).to(cuda)
@@ -105,7 +126,16 @@ def test_config2_layer_bf16_sample(cuda):
         q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3), scale=0.125
     )
     torch.cuda.synchronize()
-    for b, h in ((0, 0), (15, 19), (7, 11)):
+    worst = 0.0
+    for b in range(B):  # every head, float64 on the device
+        qb, kb, vb = (x[b].permute(1, 0, 2).double() for x in (q, k, v))
+        ref = torch.softmax(qb @ kb.transpose(1, 2) * 0.125, dim=-1) @ vb
+        err = (out[b].double() - ref).abs().max().item()
+        worst = max(worst, err)
+        assert err <= 2e-2, f"config2 b={b}: max|diff|={err:.3e}"
+    print(f"config2 all 320 heads: max|diff|={worst:.3e}", flush=True)
+    for bh in _config2_oracle_heads():  # the CPU oracle on every XCD x round position
+        b, h = divmod(bh, H)
         ref = sdpa_ref(
             to_np(q[b : b + 1, :, h : h + 1].permute(0, 2, 1, 3)),
             to_np(k[b : b + 1, :, h : h + 1].permute(0, 2, 1, 3)),

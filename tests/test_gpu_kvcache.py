@@ -14,14 +14,18 @@ pytestmark = pytest.mark.gpu
 D = 64
 
 
-def _case(cuda, dtype, B, sq, H, n_slots, Lmax, layout, seed, self_attn=True, bidx_mode="perm", cs=None):
+def _case(cuda, dtype, B, sq, H, n_slots, Lmax, layout, seed, self_attn=True, bidx_mode="perm", cs=None,
+          bidx_np=None):
     from whisperdrz_amd import flash_attn_with_kvcache
 
     rng = np.random.default_rng(seed)
     kc, vc = make_cache(n_slots, Lmax, H, D, dtype, cuda, layout, seed)
     kc0, vc0 = to_np(kc), to_np(vc)
     q = randn((B, sq, H, D), seed + 10, dtype).to(cuda)
-    if bidx_mode == "perm":
+    if bidx_np is not None:
+        bidx_np = np.asarray(bidx_np, dtype=np.int32)
+        bidx = torch.from_numpy(bidx_np).to(cuda)
+    elif bidx_mode == "perm":
         bidx_np = rng.permutation(n_slots)[:B].astype(np.int32)
         bidx = torch.from_numpy(bidx_np).to(cuda)
     else:
@@ -86,6 +90,48 @@ def test_split_kv_paths(cuda, B, H, Lmax, self_attn):
     assert kvcache_workspace_size(B, 1, H, D, Lmax) > 0
     _case(cuda, torch.bfloat16, B=B, sq=1, H=H, n_slots=B + 2, Lmax=Lmax, layout="head_major", seed=300 + B,
           self_attn=self_attn)
+
+
+def _dup_metadata(B, sq, n_slots, Lmax, case, seed):
+    """Slot ids with repeats and the lengths the case asks for."""
+    rng = np.random.default_rng(seed)
+    bidx = rng.permutation(n_slots)[:B].astype(np.int32)
+    cs = rng.integers(0, Lmax - sq + 1, size=B).astype(np.int32)
+    pairs = [(0, B - 1), (1, B // 2), (2, 3)]
+    for j, (src, dst) in enumerate(pairs):
+        bidx[dst] = bidx[src]
+        if case == "identical":  # bucket padding: a stale slot id with that slot's length
+            cs[dst] = cs[src]
+        elif case == "overlap":  # regions overlapping by part of the new rows (or shifted by one)
+            delta = max(1, sq // 2) * (1 if j % 2 == 0 else -1)
+            cs[dst] = cs[src] + delta if 0 <= cs[src] + delta <= Lmax - sq else cs[src] - delta
+        else:  # "disjoint": one row appends right behind the other
+            cs[dst] = min(Lmax - sq, cs[src] + sq)
+    if case == "three":  # three rows on one slot, the middle one appending over both others
+        bidx[1] = bidx[2] = bidx[0]
+        cs[1] = max(0, cs[0] - 1)
+        cs[2] = cs[0]
+    return bidx, np.clip(cs, 0, Lmax - sq).astype(np.int32)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("sq", [1, 5, 12, 48])
+@pytest.mark.parametrize("B", [6, 64, 70])
+@pytest.mark.parametrize("case", ["identical", "overlap", "disjoint", "three"])
+def test_duplicate_slots_follow_reference_order(cuda, dtype, sq, B, case):
+    """Repeated cache_batch_idx entries (bucket padding, transcriber.py:76-78, 165-167): the
+    fallback appends row by row (model.py:51-54), so the last batch row covering a position wins,
+    and every row attends over the cache after all appends (model.py:55-57). B=6 takes the
+    split-KV path, 64 the one-row-per-workgroup path, 70 the metadata scan beyond one wavefront;
+    sq 1 / 5 / 12 / 48 reach kv_attn_kernel, kv_mq_kernel (bf16), the 8-row blocks and
+    kv_prefill_kernel (bf16)."""
+    if dtype == torch.float32 and sq == 48 and B == 70:
+        pytest.skip("fp32 keeps the VALU kernel at every sq; one fp32 case per batch shape is enough")
+    print(f"dup case={case} dtype={dtype} sq={sq} B={B}", flush=True)
+    n_slots, Lmax, H = B + 4, 448, 3
+    bidx, cs = _dup_metadata(B, sq, n_slots, Lmax, case, 1000 + sq + B)
+    _case(cuda, dtype, B=B, sq=sq, H=H, n_slots=n_slots, Lmax=Lmax, layout="head_major", seed=700 + sq + B,
+          cs=cs, bidx_np=bidx)
 
 
 def test_config3_shape_fp32_tolerance(cuda):
@@ -236,3 +282,42 @@ def test_workspace_reuse_across_shapes(cuda):
             torch.cuda.synchronize()
             assert_close(out, ref, torch.bfloat16, f"reuse case {i}")
             assert int(torch.count_nonzero(ws)) == 0, "workspace not left all-zero"
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("self_attn", [True, False])
+def test_many_rows_need_no_workspace(cuda, dtype, self_attn):
+    """sq >= 40 on a small batch (one window's prompt): no workspace is asked for or needed; the
+    call through the C ABI with a NULL workspace matches the reference."""
+    import ctypes
+
+    from whisperdrz_amd import _lib
+
+    lib = _lib.load()
+    B, sq, H, Lmax = 1, 40, 20, 448
+    assert lib.wdrz_attn_kvcache_workspace_size(B, sq, H, D, Lmax) == 0
+    print(f"no-workspace sq=40 dtype={dtype} self={self_attn}", flush=True)
+    kc, vc = make_cache(2, Lmax, H, D, dtype, cuda, "head_major", 41)
+    kc0, vc0 = to_np(kc), to_np(vc)
+    q = randn((B, sq, H, D), 42, dtype).to(cuda)
+    k = randn((B, sq, H, D), 43, dtype).to(cuda) if self_attn else None
+    v = randn((B, sq, H, D), 44, dtype).to(cuda) if self_attn else None
+    cs = np.array([100], dtype=np.int32)
+    seq = torch.from_numpy(cs).to(cuda)
+    bidx_np = np.array([1], dtype=np.int32)
+    bidx = torch.from_numpy(bidx_np).to(cuda)
+    out = torch.empty_like(q)
+    st = lambda t: (ctypes.c_int64 * 4)(*t.stride())
+    code = {torch.bfloat16: _lib.WDRZ_BF16, torch.float32: _lib.WDRZ_F32}[dtype]
+    rc = lib.wdrz_attn_kvcache(code, q.data_ptr(), kc.data_ptr(), vc.data_ptr(),
+                               k.data_ptr() if self_attn else None, v.data_ptr() if self_attn else None,
+                               seq.data_ptr() if self_attn else None, bidx.data_ptr(), out.data_ptr(), B, sq, H, D, 2,
+                               Lmax, st(q), st(kc), st(vc), st(k if self_attn else q), st(v if self_attn else q),
+                               st(out), ctypes.c_float(0.125), int(self_attn), None, 0,
+                               torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.wdrz_last_error().decode()
+    torch.cuda.synchronize()
+    ref, kref, vref = kvcache_ref(to_np(q), kc0, vc0, to_np(k) if self_attn else None,
+                                  to_np(v) if self_attn else None, cs if self_attn else None, bidx_np, 0.125)
+    assert_close(out, ref, dtype, "sq=40 without workspace")
+    assert np.array_equal(to_np(kc), kref) and np.array_equal(to_np(vc), vref)

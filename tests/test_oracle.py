@@ -10,7 +10,10 @@ row, wrong slot mapping) fails at least one of them:
   * an sq-token causal query equals sq sequential 1-token steps;
   * rows past cache_seqlens + sq and slots not named by cache_batch_idx do not influence the
     result and are not written;
-  * the numpy float64 and torch restatements agree (they share no code).
+  * the numpy float64 and torch restatements agree (they share no code);
+  * batch rows naming the same slot (bucket padding): every cache position holds the new row of
+    the LAST batch row covering it, built here position by position, and every row attends over
+    that final cache.
 """
 import math
 
@@ -182,3 +185,45 @@ def test_decode_lengths_range_and_determinism():
     a = decode_lengths(3, 64, 1, 448)
     assert a.min() >= 1 and a.max() <= 448 and len(a) == 64
     np.testing.assert_array_equal(a, decode_lengths(3, 64, 1, 448))
+
+
+def _last_writer_cache(kc, kn, cs, idx, sq):
+    """The post-append cache built position by position: the highest batch row covering p wins."""
+    out = kc.copy()
+    S, Lmax = kc.shape[:2]
+    for s in range(S):
+        for p in range(Lmax):
+            cover = [i for i in range(len(idx)) if idx[i] == s and cs[i] <= p < cs[i] + sq]
+            if cover:
+                w = max(cover)
+                out[s, p] = kn[w, p - cs[w]]
+    return out
+
+
+@pytest.mark.parametrize("case", ["identical", "overlap", "disjoint", "three"])
+def test_kvcache_duplicate_slots_last_row_wins(case):
+    """model.py:49-57 appends row by row before gathering: with repeated slot ids the last row
+    covering a position wins, and every row reads the cache after all appends."""
+    B, sq, H, S, Lmax, D = 5, 3, 2, 4, 12, 8
+    q, kc, vc, kn, vn, _, _ = _kv_case(B=B, sq=sq, H=H, S=S, Lmax=Lmax, D=D, seed=7)
+    idx = {"identical": [2, 0, 2, 1, 3], "overlap": [2, 0, 2, 1, 2], "disjoint": [1, 0, 3, 1, 2],
+           "three": [3, 3, 0, 3, 1]}[case]
+    cs = {"identical": [4, 0, 4, 6, 2], "overlap": [4, 0, 6, 6, 5], "disjoint": [0, 2, 1, 3, 5],
+          "three": [2, 3, 0, 4, 8]}[case]
+    idx, cs = np.array(idx), np.array(cs)
+    out, k2, v2 = kvcache_ref(q, kc, vc, kn, vn, cs, idx, 0.3)
+    kf, vf = _last_writer_cache(kc, kn, cs, idx, sq), _last_writer_cache(vc, vn, cs, idx, sq)
+    np.testing.assert_array_equal(k2, kf)
+    np.testing.assert_array_equal(v2, vf)
+    for b in range(B):
+        for t in range(sq):
+            n = cs[b] + t + 1
+            for h in range(H):
+                w = np.exp(kf[idx[b], :n, h] @ q[b, t, h] * 0.3)
+                np.testing.assert_allclose(out[b, t, h], (w[:, None] * vf[idx[b], :n, h]).sum(0) / w.sum(), rtol=1e-10)
+    # the torch restatement follows the same order
+    tk, tv = torch.from_numpy(kc.copy()), torch.from_numpy(vc.copy())
+    o_t = kvcache_torch(torch.from_numpy(q), tk, tv, torch.from_numpy(kn), torch.from_numpy(vn),
+                        torch.from_numpy(cs), torch.from_numpy(idx), 0.3)
+    np.testing.assert_array_equal(tk.numpy(), kf)
+    np.testing.assert_allclose(o_t.numpy(), out, rtol=1e-9, atol=1e-12)

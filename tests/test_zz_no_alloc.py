@@ -98,3 +98,64 @@ def test_noalloc_reports_errors(cuda):
                                        torch.cuda.current_stream().cuda_stream)
     assert rc == _lib.WDRZ_EUNSUPPORTED
     assert "head_dim" in lib.wdrz_last_error().decode()
+
+
+_CAPTURE_SCRIPT = r"""
+import ctypes, sys
+import torch
+sys.path.insert(0, {root!r})
+from whisperdrz_amd import _lib
+from tests._util import make_cache, randn
+from tests.test_zz_no_alloc import _call
+
+lib = _lib.load()
+cuda = torch.device("cuda", 0)
+B, sq, H, Lmax, D = 2, 5, 20, 1500, 64
+need = lib.wdrz_attn_kvcache_workspace_size(B, sq, H, D, Lmax)
+assert need > 0
+kc, vc = make_cache(B + 1, Lmax, H, D, torch.bfloat16, cuda, "head_major", 3)
+kc2, vc2 = kc.clone(), vc.clone()
+q = randn((B, sq, H, D), 4, torch.bfloat16).to(cuda)
+k = randn((B, sq, H, D), 5, torch.bfloat16).to(cuda)
+v = randn((B, sq, H, D), 6, torch.bfloat16).to(cuda)
+seq = torch.tensor([7, 900], dtype=torch.int32, device=cuda)
+bidx = torch.tensor([2, 0], dtype=torch.int32, device=cuda)
+out_na = torch.zeros((B, sq, H, D), dtype=torch.bfloat16, device=cuda)
+out_ws = torch.zeros_like(out_na)
+ws = torch.zeros(need, dtype=torch.uint8, device=cuda)
+torch.cuda.synchronize()
+g = torch.cuda.CUDAGraph()
+with torch.cuda.graph(g):  # the process's first no-alloc call: its set-up happens under capture
+    _call(lib, True, q, kc, vc, k, v, seq, bidx, out_na, None)
+torch.cuda.synchronize()
+for rep in range(3):
+    out_na.zero_()
+    g.replay()
+    torch.cuda.synchronize()
+    _call(lib, False, q, kc2, vc2, k, v, seq, bidx, out_ws, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(out_na, out_ws), f"replay {{rep}}: output differs from the workspace entry point"
+    assert torch.equal(kc, kc2) and torch.equal(vc, vc2), f"replay {{rep}}: caches differ"
+    # an eager no-alloc call between replays shares the scratch array with the graph
+    out_e = torch.zeros_like(out_na)
+    _call(lib, True, q, kc, vc, k, v, seq, bidx, out_e, None)
+    torch.cuda.synchronize()
+    assert torch.equal(out_e, out_ws), f"eager call after replay {{rep}} differs"
+print("capture-ok")
+"""
+
+
+def test_noalloc_first_call_under_graph_capture(cuda):
+    """The first no-alloc call of a process made inside hipGraph capture (its clearing kernel is
+    recorded, not run), replayed three times with eager calls between: every replay and every
+    eager call bit-identical to the workspace entry point. Runs in a fresh process so that the
+    per-device set-up has not happened yet."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    print("noalloc capture: fresh process", flush=True)
+    proc = subprocess.run([sys.executable, "-c", _CAPTURE_SCRIPT.format(root=root)], cwd=root,
+                          capture_output=True, text=True, timeout=110)
+    assert proc.returncode == 0 and "capture-ok" in proc.stdout, proc.stdout + proc.stderr

@@ -29,6 +29,7 @@ WDRZ_OK, WDRZ_EINVAL, WDRZ_EUNSUPPORTED, WDRZ_ELAUNCH, WDRZ_EWORKSPACE = 0, 1, 2
 EXPORTED_SYMBOLS = (
     "wdrz_last_error",
     "wdrz_abi_version",
+    "wdrz_build_id",
     "wdrz_attn_fwd",
     "wdrz_attn_kvcache_workspace_size",
     "wdrz_attn_kvcache",
@@ -141,6 +142,9 @@ def _declare(lib: ctypes.CDLL) -> None:
         _p, ctypes.c_size_t, _p,  # workspace, bytes, stream
     ]
 
+    lib.wdrz_build_id.restype = ctypes.c_char_p
+    lib.wdrz_build_id.argtypes = []
+
     lib.wdrz_kv_fill.restype = ctypes.c_int
     lib.wdrz_kv_fill.argtypes = [
         ctypes.c_int, _p, _p, _i64p, _p, _p, _i64p, _p,  # dtype, k/v src, src strides, k/v cache, cache strides, slots
@@ -179,6 +183,14 @@ def load() -> ctypes.CDLL:
             raise RuntimeError(
                 f"{LIB_PATH} has ABI {lib.wdrz_abi_version()}, expected {ABI_VERSION}; rebuild it"
             )
+        # the library must have been built from the sources next to it
+        from .build import source_hash
+
+        built, tree = lib.wdrz_build_id().decode(), source_hash()
+        if built != tree:
+            _load_error = (f"{LIB_PATH} was built from other sources (build id {built}, tree {tree}); "
+                           "rebuild it (python -m whisperdrz_amd.build)")
+            raise RuntimeError(_load_error)
         _lib = lib
         return lib
 

@@ -11,10 +11,12 @@ host-side debugging.
 """
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
 import sys
+from concurrent.futures import ThreadPoolExecutor
 from pathlib import Path
 
 PKG_DIR = Path(__file__).resolve().parent
@@ -24,6 +26,22 @@ LIB_PATH = PKG_DIR / LIB_NAME
 DEBUG_LIB_PATH = PKG_DIR / "libwdrz_attn_debug.so"
 SOURCES = ["attn_kvcache.hip", "attn_dense.hip", "attn_dense_f32.hip", "dtw_prep.hip", "dtw_qk.hip", "logmel.hip", "decode_ops.hip", "kv_fill.hip", "kv_noalloc.hip", "linear.hip", "wdrz_capi.cpp"]
 ARCH = "gfx950"
+
+
+def source_hash() -> str:
+    """Hash of everything the library is built from: the kernel and C-ABI sources, the public
+    header and this build script (flags). Stamped into the library (wdrz_build_id) so that a
+    library built from other sources is refused at load time."""
+    h = hashlib.sha256()
+    files = sorted(p for p in CSRC.iterdir() if p.suffix in (".hip", ".cpp", ".h"))
+    files += sorted((PKG_DIR.parent / "include").glob("*.h"))
+    files.append(Path(__file__).resolve())
+    for f in files:
+        h.update(f.name.encode())
+        h.update(b"\0")
+        h.update(f.read_bytes())
+        h.update(b"\0")
+    return h.hexdigest()[:16]
 
 
 def hipcc() -> str:
@@ -57,22 +75,29 @@ def build_library(debug: bool = False, verbose: bool = False) -> Path:
         "dtw_prep.hip": ["-fno-honor-nans"],  # NaN outputs are written explicitly, never computed
         "dtw_qk.hip": ["-fno-honor-nans"],
     }
-    objs = []
+    objs, cmds = [], []
+    build_id = f'-DWDRZ_BUILD_ID="{source_hash()}"'
     for src in SOURCES:
         obj = out_dir / (src + ".o")
         cmd = [hipcc(), *common, "-c", str(CSRC / src), "-o", str(obj)]
+        if src == "wdrz_capi.cpp":
+            cmd.append(build_id)
         if src.endswith(".hip"):
             cmd[1:1] = ["-x", "hip"]
             cmd += device_flags + per_file.get(src, [])
         if verbose:
             print(" ".join(cmd), flush=True)
-        proc = subprocess.run(cmd, capture_output=True, text=True)
-        if proc.returncode != 0:
-            raise RuntimeError(f"hipcc failed for {src}:\n{proc.stderr}")
+        cmds.append((src, cmd))
         objs.append(str(obj))
+    # the sources compile independently: run the compilers side by side
+    jobs = max(1, min(len(cmds), int(os.environ.get("MAX_JOBS", os.cpu_count() or 1))))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        for (src, _), proc in zip(cmds, pool.map(lambda c: subprocess.run(c[1], capture_output=True, text=True), cmds)):
+            if proc.returncode != 0:
+                raise RuntimeError(f"hipcc failed for {src}:\n{proc.stderr}")
     # the host-checked twin: the C-ABI layer again, with WDRZ_DEBUG_CHECKS
     capi_dbg = out_dir / "wdrz_capi.debug.o"
-    cmd = [hipcc(), *common, "-DWDRZ_DEBUG_CHECKS", "-c", str(CSRC / "wdrz_capi.cpp"), "-o", str(capi_dbg)]
+    cmd = [hipcc(), *common, "-DWDRZ_DEBUG_CHECKS", build_id, "-c", str(CSRC / "wdrz_capi.cpp"), "-o", str(capi_dbg)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for wdrz_capi.cpp (debug checks):\n{proc.stderr}")

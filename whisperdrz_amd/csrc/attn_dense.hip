@@ -44,6 +44,7 @@
 // Grid. One workgroup per (b, h, query block), flattened and remapped so that the query blocks
 // of one (b, h) land on the same XCD (work-group ids are dealt round-robin over the 8 XCDs):
 // they then share K/V through that XCD's L2.
+#include "kv_dup.h"
 #include "wdrz_common.h"
 #include "wdrz_launch.h"
 
@@ -425,6 +426,9 @@ __global__ __launch_bounds__(512, 4) void kv_prefill_kernel(KvArgs a) {
     return;  // the whole workgroup: no barrier follows
   }
 
+  // other rows naming this slot (kv_dup.h): the positions they win are staged from their new
+  // rows, and this workgroup stores only the positions it wins
+  const KvDup dup = HAS_NEW ? kv_dup_scan(a, b, slot) : KvDup{INT_MAX, INT_MIN, 0ull, 0};
   const char* const Qb = a.q + (int64_t)b * a.qs[0] + (int64_t)h * a.qs[2];
   const char* const Kc = a.kc + (int64_t)slot * a.kcs[0] + (int64_t)h * a.kcs[2];
   const char* const Vc = a.vc + (int64_t)slot * a.vcs[0] + (int64_t)h * a.vcs[2];
@@ -466,11 +470,24 @@ __global__ __launch_bounds__(512, 4) void kv_prefill_kernel(KvArgs a) {
   u32x2 pv[2];
   const int vkp = tid / (kHeadDim / kVDims);
   const int vd0 = (tid % (kHeadDim / kVDims)) * kVDims;
+  auto dup_row = [&](int key, const char* nb, const int64_t (&ns)[3], const char* crow, int64_t cstr) -> const char* {
+    int cw = 0;
+    const int w = kv_dup_winner(a, dup, slot, key, cw);
+    return w >= 0 ? nb + (int64_t)w * ns[0] + (int64_t)h * ns[2] + (int64_t)(key - cw) * ns[1] : crow + (int64_t)key * cstr;
+  };
   auto krow = [&](int key) -> const char* {
+    if (HAS_NEW && kv_dup_in_window(dup, key)) return dup_row(key, a.kn, a.kns, Kc, a.kcs[1]);
     return !HAS_NEW || key < cs ? Kc + (int64_t)key * a.kcs[1] : Kn + (int64_t)(key - cs) * a.kns[1];
   };
   auto vrow = [&](int key) -> const char* {
+    if (HAS_NEW && kv_dup_in_window(dup, key)) return dup_row(key, a.vn, a.vns, Vc, a.vcs[1]);
     return !HAS_NEW || key < cs ? Vc + (int64_t)key * a.vcs[1] : Vn + (int64_t)(key - cs) * a.vns[1];
+  };
+  // this row's new key `key` is stored unless a later row naming the slot covers it too
+  auto owns = [&](int key) -> bool {
+    if (!kv_dup_in_window(dup, key)) return true;
+    int cw = 0;
+    return kv_dup_winner(a, dup, slot, key, cw) == b;
   };
   auto gload = [&](int kt) __attribute__((always_inline)) {
     pk = load16(krow(min(kt * kBN + (tid >> 3), k_lim - 1)) + (tid & 7) * 16);
@@ -482,11 +499,11 @@ __global__ __launch_bounds__(512, 4) void kv_prefill_kernel(KvArgs a) {
   auto lstore = [&](int buf, int kt) __attribute__((always_inline)) {
     if (HAS_NEW) {
       const int kkey = kt * kBN + (tid >> 3);
-      if (kkey >= app0 && kkey < app1) *reinterpret_cast<u32x4*>(Kw + (int64_t)kkey * a.kcs[1] + (tid & 7) * 16) = pk;
+      if (kkey >= app0 && kkey < app1 && owns(kkey)) *reinterpret_cast<u32x4*>(Kw + (int64_t)kkey * a.kcs[1] + (tid & 7) * 16) = pk;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int vkey = kt * kBN + 2 * vkp + i;
-        if (vkey >= app0 && vkey < app1) *reinterpret_cast<u32x2*>(Vw + (int64_t)vkey * a.vcs[1] + vd0 * 2) = pv[i];
+        if (vkey >= app0 && vkey < app1 && owns(vkey)) *reinterpret_cast<u32x2*>(Vw + (int64_t)vkey * a.vcs[1] + vd0 * 2) = pv[i];
       }
     }
     *reinterpret_cast<u32x4*>(&sK[buf][(tid >> 3) * kPitchK + (tid & 7) * 8]) = pk;

@@ -27,6 +27,7 @@
 // the chip, and 40 or more rows (a prompt's self or cross attention) on kv_prefill_kernel in
 // attn_dense.hip (256-query MFMA blocks); single rows, the remaining multi-row shapes and fp32
 // caches run on kv_attn_kernel.
+#include "kv_dup.h"
 #include "wdrz_common.h"
 #include "wdrz_launch.h"
 
@@ -89,11 +90,18 @@ __device__ __forceinline__ AppendPiece kv_append_load(const KvArgs& a, int b, in
                  p.rr * 16);
   return p;
 }
+// With other rows naming the same slot (kv_dup.h) a position is stored only by the row that
+// wins it, the last batch row covering it.
 __device__ __forceinline__ void kv_append_store(const KvArgs& a, const AppendPiece& p, int t0, int h, int split,
-                                                int slot, int cs) {
+                                                int b, int slot, int cs, const KvDup& dup) {
   const int lo = split * a.split_len, hi = lo + a.split_len;
   const int pos = cs + t0 + p.t;
-  if (p.on && pos >= lo && pos < hi)
+  bool own = true;
+  if (p.on && kv_dup_in_window(dup, pos)) {
+    int cw = 0;
+    own = kv_dup_winner(a, dup, slot, pos, cw) == b;
+  }
+  if (p.on && own && pos >= lo && pos < hi)
     store16((p.which ? a.vc + slot * a.vcs[0] + (int64_t)pos * a.vcs[1] + h * a.vcs[2]
                      : a.kc + slot * a.kcs[0] + (int64_t)pos * a.kcs[1] + h * a.kcs[2]) +
                 p.rr * 16,
@@ -239,6 +247,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
 
   const int slot = a.bidx ? a.bidx[b] : b;
   const int cs = HAS_NEW ? a.seqlens[b] : 0;
+  const KvDup dup = HAS_NEW ? kv_dup_scan(a, b, slot) : KvDup{INT_MAX, INT_MIN, 0ull, 0};
   // Loads that need no metadata are issued while it arrives: the queries and the rows to
   // append (stored after the key loop, when they have long arrived).
   u32x4 qraw[SQ];
@@ -304,7 +313,17 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
       const int kk = min(base + u * G, k_end - 1);
       const char* kp;
       const char* vp;
-      if (HAS_NEW && kk >= cs) {
+      if (HAS_NEW && kv_dup_in_window(dup, kk)) {  // another row naming this slot appends here
+        int cw = 0;
+        const int w = kv_dup_winner(a, dup, safe_slot, kk, cw);
+        if (w >= 0) {
+          kp = a.kn + w * a.kns[0] + h * a.kns[2] + r * 16 + (int64_t)(kk - cw) * a.kns[1];
+          vp = a.vn + w * a.vns[0] + h * a.vns[2] + r * 16 + (int64_t)(kk - cw) * a.vns[1];
+        } else {
+          kp = kc_row + (int64_t)kk * a.kcs[1];
+          vp = vc_row + (int64_t)kk * a.vcs[1];
+        }
+      } else if (HAS_NEW && kk >= cs) {
         kp = kn_row + (int64_t)(kk - cs) * a.kns[1];
         vp = vn_row + (int64_t)(kk - cs) * a.vns[1];
       } else {
@@ -425,7 +444,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
     }
   }
 
-  if (HAS_NEW && !bad) kv_append_store(a, app, t0, h, split, slot, cs);
+  if (HAS_NEW && !bad) kv_append_store(a, app, t0, h, split, b, slot, cs, dup);
 
   // Merge lane groups inside the wavefront (groups differ in lane bits >= log2(LPK)).
 #pragma unroll
@@ -544,6 +563,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
 
   const int slot = a.bidx ? a.bidx[b] : b;
   const int cs = HAS_NEW ? a.seqlens[b] : 0;
+  const KvDup dup = HAS_NEW ? kv_dup_scan(a, b, slot) : KvDup{INT_MAX, INT_MIN, 0ull, 0};
   static_assert(SQ * 2 * (kHeadDim * 2 / 16) <= kWaves * 64, "one append piece per thread");
   const AppendPiece app = HAS_NEW ? kv_append_load<T>(a, b, t0, nq, h) : AppendPiece{};
   const bool bad = slot < 0 || slot >= a.n_slots || cs < 0 || (HAS_NEW && cs + a.sq > a.Lk);
@@ -570,10 +590,18 @@ __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
   const char* vc_row = a.vc + safe_slot * a.vcs[0] + h * a.vcs[2];
   const char* kn_row = HAS_NEW ? a.kn + b * a.kns[0] + h * a.kns[2] : nullptr;
   const char* vn_row = HAS_NEW ? a.vn + b * a.vns[0] + h * a.vns[2] : nullptr;
+  // key rows another row naming this slot appends come from that row's k_new / v_new (kv_dup.h)
+  auto dup_ptr = [&](int key, const char* nb, const int64_t (&ns)[3], const char* crow, int64_t cstr) -> const char* {
+    int cw = 0;
+    const int w = kv_dup_winner(a, dup, safe_slot, key, cw);
+    return w >= 0 ? nb + w * ns[0] + h * ns[2] + (int64_t)(key - cw) * ns[1] : crow + (int64_t)key * cstr;
+  };
   auto k_ptr = [&](int key) __attribute__((always_inline)) {
+    if (HAS_NEW && kv_dup_in_window(dup, key)) return dup_ptr(key, a.kn, a.kns, kc_row, a.kcs[1]);
     return (HAS_NEW && key >= cs) ? kn_row + (int64_t)(key - cs) * a.kns[1] : kc_row + (int64_t)key * a.kcs[1];
   };
   auto v_ptr = [&](int key) __attribute__((always_inline)) {
+    if (HAS_NEW && kv_dup_in_window(dup, key)) return dup_ptr(key, a.vn, a.vns, vc_row, a.vcs[1]);
     return (HAS_NEW && key >= cs) ? vn_row + (int64_t)(key - cs) * a.vns[1] : vc_row + (int64_t)key * a.vcs[1];
   };
 
@@ -663,7 +691,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
     for (int db = 0; db < 4; ++db) o[db] = Mfma16<T>::run(vop[db], pop, o[db]);
   }
 
-  if (HAS_NEW && !bad) kv_append_store(a, app, t0, h, split, slot, cs);
+  if (HAS_NEW && !bad) kv_append_store(a, app, t0, h, split, b, slot, cs, dup);
 
   // row sums: the four lane groups hold different keys of the same query
   l += __shfl_xor(l, 16);

@@ -134,9 +134,8 @@ int dtw_qk_heads(int dtype, const void* const* q_heads, const int64_t* q_strides
 #ifdef WDRZ_DEBUG_CHECKS
 // Copies the slot ids and pre-append lengths of a cached-attention call to the host
 // (synchronously) and checks every row: slot in [0, n_slots), length >= 0, and with an append
-// length + sq <= Lmax. Append regions [cs, cs + sq) of rows naming the same slot must not
-// overlap; duplicate slot ids with identical regions (the padded rows of a bucketed decode
-// graph) are reported once on stderr but allowed, as the reference tolerates them.
+// length + sq <= Lmax. Rows that name the same slot are valid: the kernels apply their appends in
+// batch order, as the reference fallback does (model.py:51-54).
 int debug_check_kv_metadata(const int32_t* seqlens, const int32_t* bidx, bool has_new, int64_t B, int64_t sq,
                             int64_t n_slots, int64_t Lmax) {
   std::vector<int32_t> hs(B, 0), hb(B);
@@ -152,18 +151,6 @@ int debug_check_kv_metadata(const int32_t* seqlens, const int32_t* bidx, bool ha
     if (has_new && (hs[i] < 0 || hs[i] + sq > Lmax))
       return fail(WDRZ_EINVAL, "debug check: row %lld appends [%d, %lld) outside the cache [0, %lld)", (long long)i,
                   hs[i], (long long)(hs[i] + sq), (long long)Lmax);
-  }
-  if (has_new) {
-    bool dup = false;
-    for (int64_t i = 0; i < B; ++i)
-      for (int64_t j = i + 1; j < B; ++j) {
-        if (hb[i] != hb[j]) continue;
-        if (hs[i] != hs[j] && hs[i] < hs[j] + sq && hs[j] < hs[i] + sq)
-          return fail(WDRZ_EINVAL, "debug check: rows %lld and %lld append overlapping regions of slot %d",
-                      (long long)i, (long long)j, hb[i]);
-        dup = true;
-      }
-    if (dup) fprintf(stderr, "wdrz debug: duplicate cache_batch_idx entries (identical append regions)\n");
   }
   return WDRZ_OK;
 }
@@ -188,6 +175,11 @@ extern "C" {
 const char* wdrz_last_error(void) { return g_last_error.c_str(); }
 
 int wdrz_abi_version(void) { return 1; }
+
+#ifndef WDRZ_BUILD_ID
+#define WDRZ_BUILD_ID "unknown"
+#endif
+const char* wdrz_build_id(void) { return WDRZ_BUILD_ID; }
 
 int wdrz_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* o, int64_t B, int64_t H,
                   int64_t Lq, int64_t Lk, int64_t D, const int64_t* q_strides, const int64_t* k_strides,
@@ -238,6 +230,9 @@ int wdrz_attn_fwd(int dtype, const void* q, const void* k, const void* v, void* 
 size_t wdrz_attn_kvcache_workspace_size(int64_t B, int64_t sq, int64_t H, int64_t D, int64_t Lmax) {
   (void)D;
   if (B <= 0 || sq <= 0 || H <= 0 || Lmax <= 0) return 0;
+  // kPrefillMinSq or more query rows never split their keys (16-bit types run them on the
+  // 256-query prefill kernel, fp32 on one workgroup per 8-row block): no workspace
+  if (sq >= wdrz::kPrefillMinSq) return 0;
   const int64_t n_qblocks = (sq + 7) / 8;
   const int64_t units = B * n_qblocks * H;
   int n_splits, split_len;
@@ -317,7 +312,12 @@ int wdrz_attn_kvcache(int dtype, const void* q, void* k_cache, void* v_cache, co
   a.c = softmax_scale * 1.4426950408889634f;
   const int64_t units = B * a.n_qblocks * H;
   if (units > 0x7fffffff) return fail(WDRZ_EUNSUPPORTED, "B * ceil(sq / rows per block) * H exceeds 2^31 - 1");
-  wdrz::kv_split_plan(units, Lmax, &a.n_splits, &a.split_len);
+  if (sq >= wdrz::kPrefillMinSq) {  // never split (see wdrz_attn_kvcache_workspace_size)
+    a.n_splits = 1;
+    a.split_len = (int)Lmax;
+  } else {
+    wdrz::kv_split_plan(units, Lmax, &a.n_splits, &a.split_len);
+  }
   const size_t need = wdrz::kv_workspace_bytes(units, sq < 8 ? sq : 8, a.n_splits);
   if (need > 0) {
     if (!workspace || workspace_bytes < need)
@@ -376,6 +376,8 @@ int wdrz_add_layernorm(int dtype, void* x, int64_t x_stride, const void* delta, 
   if (delta && (rc = check_ptr("delta", delta))) return rc;
   if ((x_stride * 2) % 16 || (y_stride * 2) % 16 || (delta && (delta_stride * 2) % 16))
     return fail(WDRZ_EINVAL, "row strides must be 16-byte aligned");
+  if (rows > 1 && (x_stride < n || y_stride < n || (delta && delta_stride < n)))
+    return fail(WDRZ_EINVAL, "row strides shorter than the rows");
   if (rows == 0) return WDRZ_OK;
   wdrz::AddLnArgs a{};
   a.x = x;
@@ -427,7 +429,8 @@ int wdrz_linear(int dtype, const void* x, int64_t x_stride, const void* w, int64
   if (M < 0 || N <= 0 || K <= 0) return fail(WDRZ_EINVAL, "bad sizes M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
   if (K % 128 != 0 || N % 8 != 0)
     return fail(WDRZ_EUNSUPPORTED, "K=%lld must be a multiple of 128 and N=%lld of 8", (long long)K, (long long)N);
-  if (M > (1 << 24) || N > (1 << 24) || K > (1 << 20)) return fail(WDRZ_EUNSUPPORTED, "sizes too large");
+  // ceil(M / 64) row blocks go in grid.y, which holds at most 65535
+  if (M > 65535 * 64 || N > (1 << 24) || K > (1 << 20)) return fail(WDRZ_EUNSUPPORTED, "sizes too large");
   if (M == 0) return WDRZ_OK;  // nothing to read or write (an empty tensor's pointer may be NULL)
   int rc;
   if ((rc = check_ptr("x", x)) || (rc = check_ptr("w", w)) || (rc = check_ptr("y", y))) return rc;
@@ -462,7 +465,7 @@ int wdrz_linear_partials(int dtype, const void* x, int64_t x_stride, const void*
   if (K % (128 * n_split) != 0 || N % 8 != 0)
     return fail(WDRZ_EUNSUPPORTED, "K=%lld must be a multiple of 128 * n_split and N=%lld of 8", (long long)K,
                 (long long)N);
-  if (M > (1 << 24) || N > (1 << 24) || K > (1 << 20) || M * N * n_split > ((int64_t)1 << 31))
+  if (M > 65535 * 64 || N > (1 << 24) || K > (1 << 20) || M * N * n_split > ((int64_t)1 << 31))
     return fail(WDRZ_EUNSUPPORTED, "sizes too large");
   if (M == 0) return WDRZ_OK;
   int rc;
@@ -503,6 +506,7 @@ int wdrz_add_layernorm_partials(int dtype, void* x, int64_t x_stride, const floa
       (rc = check_ptr("weight", weight)) || (rc = check_ptr("bias", bias)) || (rc = check_ptr("y", y)))
     return rc;
   if ((x_stride * 2) % 16 || (y_stride * 2) % 16) return fail(WDRZ_EINVAL, "row strides must be 16-byte aligned");
+  if (rows > 1 && (x_stride < n || y_stride < n)) return fail(WDRZ_EINVAL, "row strides shorter than the rows");
   wdrz::AddLnArgs a{};
   a.x = x;
   a.weight = weight;

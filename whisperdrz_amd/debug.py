@@ -14,7 +14,6 @@ reference's torch fallback, like ``flash_kernel(flash=False)`` at src/whisperdrz
 from __future__ import annotations
 
 import os
-import warnings
 from typing import Optional
 
 import numpy as np
@@ -40,10 +39,10 @@ def check_kvcache_metadata(cache_seqlens: Optional[np.ndarray], cache_batch_idx:
     """Check the metadata of one ``flash_attn_with_kvcache`` call (host arrays).
 
     Raises ``ValueError`` for a row whose slot id is outside ``[0, n_slots)`` or, with an
-    append, whose region ``[cs, cs + sq)`` leaves the cache or overlaps a different region of
-    the same slot (two rows writing the same cache rows with different data). Duplicate slot ids
-    with identical regions, as the padded rows of a bucketed decode graph produce
-    (transcriber.py:76-78, 165-169), only warn.
+    append, whose region ``[cs, cs + sq)`` leaves the cache. Rows naming the same slot (the
+    padded rows of a bucketed decode graph, transcriber.py:76-78, 165-169) are valid: the kernels
+    apply their appends in batch order, the last row covering a position winning, as the
+    fallback's loop does (model.py:51-54).
     """
     if cache_batch_idx is None and cache_seqlens is None:
         return
@@ -60,17 +59,3 @@ def check_kvcache_metadata(cache_seqlens: Optional[np.ndarray], cache_batch_idx:
     if bad.size:
         i = int(bad[0])
         raise ValueError(f"row {i} appends [{int(cs[i])}, {int(cs[i]) + sq}) outside the cache [0, {max_seq})")
-    order = np.lexsort((cs, slots))
-    s_sorted, c_sorted = slots[order], cs[order]
-    same_slot = s_sorted[1:] == s_sorted[:-1]
-    if not same_slot.any():
-        return
-    differ = c_sorted[1:] != c_sorted[:-1]
-    overlap = same_slot & differ & (c_sorted[1:] < c_sorted[:-1] + sq)
-    if overlap.any():
-        k = int(np.flatnonzero(overlap)[0])
-        a, b = int(order[k]), int(order[k + 1])
-        raise ValueError(f"rows {a} and {b} append overlapping regions of slot {int(s_sorted[k])}")
-    if (same_slot & ~differ).any():
-        warnings.warn("duplicate cache_batch_idx entries with identical append regions (padded rows?)",
-                      stacklevel=3)
