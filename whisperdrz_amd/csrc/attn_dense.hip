@@ -426,14 +426,39 @@ __global__ __launch_bounds__(512, 4) void kv_prefill_kernel(KvArgs a) {
     return;  // the whole workgroup: no barrier follows
   }
 
-  // other rows naming this slot (kv_dup.h): the positions they win are staged from their new
-  // rows, and this workgroup stores only the positions it wins
-  const KvDup dup = HAS_NEW ? kv_dup_scan(a, b, slot) : KvDup{INT_MAX, INT_MIN, 0ull, 0};
+  // other rows appending to this slot (kv_dup.h): usually none
+  const KvDup dup = HAS_NEW ? kv_dup_classify(a, b, slot, cs) : KvDup{b, false};
+  if (HAS_NEW && dup.general) {
+    // generic path: this workgroup's queries, then the new rows of its query block that it wins
+    __shared__ float sm_q[NW][kHeadDim];
+    const int nq = min(kBM, sq - q_wg);
+    kv_generic_rows<T, NW>(a, b, h, slot, cs, q_wg, nq, 0, a.Lk, true, sm_q,
+                           [&](int t, int d, float o, float m, float l) {
+                             (void)m;
+                             char* orow = Ob + (int64_t)(q_wg + t) * a.os[1];
+                             if constexpr (__is_same(T, Bf16))
+                               reinterpret_cast<__bf16*>(orow)[d] = (__bf16)(o / l);
+                             else
+                               reinterpret_cast<_Float16*>(orow)[d] = (_Float16)(o / l);
+                           });
+    for (int idx = tid; idx < nq * 2 * 8; idx += kThreads) {
+      const int t = idx / 16, which = (idx / 8) & 1, piece = idx % 8;
+      int cw = 0;
+      if (kv_dup_winner(a, slot, cs + q_wg + t, cw) != b) continue;
+      const char* src = which ? a.vn + (int64_t)b * a.vns[0] + (int64_t)(q_wg + t) * a.vns[1] + (int64_t)h * a.vns[2]
+                              : a.kn + (int64_t)b * a.kns[0] + (int64_t)(q_wg + t) * a.kns[1] + (int64_t)h * a.kns[2];
+      char* dst = which ? a.vc + (int64_t)slot * a.vcs[0] + (int64_t)(cs + q_wg + t) * a.vcs[1] + (int64_t)h * a.vcs[2]
+                        : a.kc + (int64_t)slot * a.kcs[0] + (int64_t)(cs + q_wg + t) * a.kcs[1] + (int64_t)h * a.kcs[2];
+      reinterpret_cast<u32x4*>(dst)[piece] = reinterpret_cast<const u32x4*>(src)[piece];
+    }
+    return;
+  }
   const char* const Qb = a.q + (int64_t)b * a.qs[0] + (int64_t)h * a.qs[2];
   const char* const Kc = a.kc + (int64_t)slot * a.kcs[0] + (int64_t)h * a.kcs[2];
   const char* const Vc = a.vc + (int64_t)slot * a.vcs[0] + (int64_t)h * a.vcs[2];
-  const char* const Kn = HAS_NEW ? a.kn + (int64_t)b * a.kns[0] + (int64_t)h * a.kns[2] : nullptr;
-  const char* const Vn = HAS_NEW ? a.vn + (int64_t)b * a.vns[0] + (int64_t)h * a.vns[2] : nullptr;
+  // the new rows: those of the last row appending this same region (this row when alone)
+  const char* const Kn = HAS_NEW ? a.kn + (int64_t)dup.src * a.kns[0] + (int64_t)h * a.kns[2] : nullptr;
+  const char* const Vn = HAS_NEW ? a.vn + (int64_t)dup.src * a.vns[0] + (int64_t)h * a.vns[2] : nullptr;
   char* const Kw = a.kc + (int64_t)slot * a.kcs[0] + (int64_t)h * a.kcs[2];
   char* const Vw = a.vc + (int64_t)slot * a.vcs[0] + (int64_t)h * a.vcs[2];
   const float c = a.c;
@@ -461,7 +486,7 @@ __global__ __launch_bounds__(512, 4) void kv_prefill_kernel(KvArgs a) {
   const int n_sub_w =
       q_wave >= sq ? 0 : HAS_NEW ? min(n_sub, (cs + min(sq, q_wave + 32) + kBS - 1) / kBS) : n_sub;
   // new rows this workgroup appends: keys [app0, app1) (none for cross)
-  const int app0 = HAS_NEW ? cs + q_wg : 0, app1 = HAS_NEW ? cs + min(sq, q_wg + kBM) : 0;
+  const int app0 = HAS_NEW && dup.src == b ? cs + q_wg : 0, app1 = HAS_NEW && dup.src == b ? cs + min(sq, q_wg + kBM) : 0;
 
   constexpr int kKPerThr = (kBN * kHeadDim / 8) / kThreads;
   constexpr int kVDims = (kBN / 2) * kHeadDim / kThreads;
@@ -470,24 +495,11 @@ __global__ __launch_bounds__(512, 4) void kv_prefill_kernel(KvArgs a) {
   u32x2 pv[2];
   const int vkp = tid / (kHeadDim / kVDims);
   const int vd0 = (tid % (kHeadDim / kVDims)) * kVDims;
-  auto dup_row = [&](int key, const char* nb, const int64_t (&ns)[3], const char* crow, int64_t cstr) -> const char* {
-    int cw = 0;
-    const int w = kv_dup_winner(a, dup, slot, key, cw);
-    return w >= 0 ? nb + (int64_t)w * ns[0] + (int64_t)h * ns[2] + (int64_t)(key - cw) * ns[1] : crow + (int64_t)key * cstr;
-  };
   auto krow = [&](int key) -> const char* {
-    if (HAS_NEW && kv_dup_in_window(dup, key)) return dup_row(key, a.kn, a.kns, Kc, a.kcs[1]);
     return !HAS_NEW || key < cs ? Kc + (int64_t)key * a.kcs[1] : Kn + (int64_t)(key - cs) * a.kns[1];
   };
   auto vrow = [&](int key) -> const char* {
-    if (HAS_NEW && kv_dup_in_window(dup, key)) return dup_row(key, a.vn, a.vns, Vc, a.vcs[1]);
     return !HAS_NEW || key < cs ? Vc + (int64_t)key * a.vcs[1] : Vn + (int64_t)(key - cs) * a.vns[1];
-  };
-  // this row's new key `key` is stored unless a later row naming the slot covers it too
-  auto owns = [&](int key) -> bool {
-    if (!kv_dup_in_window(dup, key)) return true;
-    int cw = 0;
-    return kv_dup_winner(a, dup, slot, key, cw) == b;
   };
   auto gload = [&](int kt) __attribute__((always_inline)) {
     pk = load16(krow(min(kt * kBN + (tid >> 3), k_lim - 1)) + (tid & 7) * 16);
@@ -499,11 +511,11 @@ __global__ __launch_bounds__(512, 4) void kv_prefill_kernel(KvArgs a) {
   auto lstore = [&](int buf, int kt) __attribute__((always_inline)) {
     if (HAS_NEW) {
       const int kkey = kt * kBN + (tid >> 3);
-      if (kkey >= app0 && kkey < app1 && owns(kkey)) *reinterpret_cast<u32x4*>(Kw + (int64_t)kkey * a.kcs[1] + (tid & 7) * 16) = pk;
+      if (kkey >= app0 && kkey < app1) *reinterpret_cast<u32x4*>(Kw + (int64_t)kkey * a.kcs[1] + (tid & 7) * 16) = pk;
 #pragma unroll
       for (int i = 0; i < 2; ++i) {
         const int vkey = kt * kBN + 2 * vkp + i;
-        if (vkey >= app0 && vkey < app1 && owns(vkey)) *reinterpret_cast<u32x2*>(Vw + (int64_t)vkey * a.vcs[1] + vd0 * 2) = pv[i];
+        if (vkey >= app0 && vkey < app1) *reinterpret_cast<u32x2*>(Vw + (int64_t)vkey * a.vcs[1] + vd0 * 2) = pv[i];
       }
     }
     *reinterpret_cast<u32x4*>(&sK[buf][(tid >> 3) * kPitchK + (tid & 7) * 8]) = pk;

@@ -90,18 +90,12 @@ __device__ __forceinline__ AppendPiece kv_append_load(const KvArgs& a, int b, in
                  p.rr * 16);
   return p;
 }
-// With other rows naming the same slot (kv_dup.h) a position is stored only by the row that
-// wins it, the last batch row covering it.
+// `own`: this row stores its region (it is the last row appending there, kv_dup.h).
 __device__ __forceinline__ void kv_append_store(const KvArgs& a, const AppendPiece& p, int t0, int h, int split,
-                                                int b, int slot, int cs, const KvDup& dup) {
+                                                int slot, int cs, bool own) {
   const int lo = split * a.split_len, hi = lo + a.split_len;
   const int pos = cs + t0 + p.t;
-  bool own = true;
-  if (p.on && kv_dup_in_window(dup, pos)) {
-    int cw = 0;
-    own = kv_dup_winner(a, dup, slot, pos, cw) == b;
-  }
-  if (p.on && own && pos >= lo && pos < hi)
+  if (own && p.on && pos >= lo && pos < hi)
     store16((p.which ? a.vc + slot * a.vcs[0] + (int64_t)pos * a.vcs[1] + h * a.vcs[2]
                      : a.kc + slot * a.kcs[0] + (int64_t)pos * a.kcs[1] + h * a.kcs[2]) +
                 p.rr * 16,
@@ -216,6 +210,38 @@ __device__ __forceinline__ void kv_finish(const KvArgs& a, int b, int t0, int nq
   if (tid == 0) __hip_atomic_store(a.ws_count + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// A row whose keys another row's append region overlaps other than exactly (kv_dup.h): the
+// generic path computes its queries' partials into wavefront 0's LDS slots (the others empty),
+// appends the positions this row wins, and hands over to the usual merge.
+template <typename T, int SQ, int kWaves>
+__device__ __forceinline__ void kv_general_row(const KvArgs& a, const AppendPiece& app, int b, int h, int slot, int cs,
+                                               int t0, int nq, int sq_stride, int split, int n_split_b, int k_begin,
+                                               int k_end, float (&sm_acc)[kWaves][SQ][kHeadDim], float (&sm_m)[kWaves][SQ],
+                                               float (&sm_l)[kWaves][SQ]) {
+  __shared__ float sm_q[kWaves][kHeadDim];
+  kv_generic_rows<T, kWaves>(a, b, h, slot, cs, t0, nq, k_begin, k_end, true, sm_q,
+                             [&](int t, int d, float o, float m, float l) {
+                               sm_acc[0][t][d] = o;
+                               if (d == 0) {
+                                 sm_m[0][t] = m;
+                                 sm_l[0][t] = l;
+                               }
+                             });
+  for (int idx = threadIdx.x; idx < (kWaves - 1) * SQ * kHeadDim; idx += kWaves * 64) {
+    const int w = 1 + idx / (SQ * kHeadDim), t = (idx / kHeadDim) % SQ, d = idx % kHeadDim;
+    sm_acc[w][t][d] = 0.f;
+    if (d == 0) {
+      sm_m[w][t] = kNegBig;
+      sm_l[w][t] = 0.f;
+    }
+  }
+  int cw = 0;
+  const bool own = app.on && kv_dup_winner(a, slot, cs + t0 + app.t, cw) == b;
+  kv_append_store(a, app, t0, h, split, slot, cs, own);
+  __syncthreads();
+  kv_finish<T, SQ, kWaves>(a, b, t0, nq, sq_stride, h, split, n_split_b, false, sm_acc, sm_m, sm_l);
+}
+
 template <typename T, int SQ, bool HAS_NEW>
 __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
   constexpr int kThreads = kWavesPerWg * 64;
@@ -247,7 +273,8 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
 
   const int slot = a.bidx ? a.bidx[b] : b;
   const int cs = HAS_NEW ? a.seqlens[b] : 0;
-  const KvDup dup = HAS_NEW ? kv_dup_scan(a, b, slot) : KvDup{INT_MAX, INT_MIN, 0ull, 0};
+  // other rows appending to this slot (kv_dup.h): usually none
+  const KvDup dup = HAS_NEW ? kv_dup_classify(a, b, slot, cs) : KvDup{b, false};
   // Loads that need no metadata are issued while it arrives: the queries and the rows to
   // append (stored after the key loop, when they have long arrived).
   u32x4 qraw[SQ];
@@ -269,6 +296,11 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
   if (split >= n_split_b) return;
   const int k_begin = split * a.split_len;
   const int k_end = bad ? k_begin : min(key_lim, k_begin + a.split_len);
+  if (HAS_NEW && dup.general && !bad) {
+    kv_general_row<T, SQ, kWaves>(a, app, b, h, slot, cs, t0, nq, SQ, split, n_split_b, k_begin, k_end, sm_acc,
+                                  sm_m, sm_l);
+    return;
+  }
 
   // Queries. 16-bit types keep the raw packed pairs for v_dot2 (the scale is applied to the
   // reduced score); fp32 keeps floats pre-scaled into the log2 domain.
@@ -303,8 +335,9 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
   const int safe_slot = bad ? 0 : slot;
   const char* kc_row = a.kc + safe_slot * a.kcs[0] + h * a.kcs[2] + r * 16;
   const char* vc_row = a.vc + safe_slot * a.vcs[0] + h * a.vcs[2] + r * 16;
-  const char* kn_row = HAS_NEW ? a.kn + b * a.kns[0] + h * a.kns[2] + r * 16 : nullptr;
-  const char* vn_row = HAS_NEW ? a.vn + b * a.vns[0] + h * a.vns[2] + r * 16 : nullptr;
+  // the appended rows: those of the last row appending this same region (this row when alone)
+  const char* kn_row = HAS_NEW ? a.kn + dup.src * a.kns[0] + h * a.kns[2] + r * 16 : nullptr;
+  const char* vn_row = HAS_NEW ? a.vn + dup.src * a.vns[0] + h * a.vns[2] + r * 16 : nullptr;
 
   // Batches of kUnroll keys per lane group. Loads past the row's end re-read its last key.
   auto load_batch = [&](int base, u32x4 (&kr)[kUnroll], u32x4 (&vr)[kUnroll]) __attribute__((always_inline)) {
@@ -313,17 +346,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
       const int kk = min(base + u * G, k_end - 1);
       const char* kp;
       const char* vp;
-      if (HAS_NEW && kv_dup_in_window(dup, kk)) {  // another row naming this slot appends here
-        int cw = 0;
-        const int w = kv_dup_winner(a, dup, safe_slot, kk, cw);
-        if (w >= 0) {
-          kp = a.kn + w * a.kns[0] + h * a.kns[2] + r * 16 + (int64_t)(kk - cw) * a.kns[1];
-          vp = a.vn + w * a.vns[0] + h * a.vns[2] + r * 16 + (int64_t)(kk - cw) * a.vns[1];
-        } else {
-          kp = kc_row + (int64_t)kk * a.kcs[1];
-          vp = vc_row + (int64_t)kk * a.vcs[1];
-        }
-      } else if (HAS_NEW && kk >= cs) {
+      if (HAS_NEW && kk >= cs) {
         kp = kn_row + (int64_t)(kk - cs) * a.kns[1];
         vp = vn_row + (int64_t)(kk - cs) * a.vns[1];
       } else {
@@ -444,7 +467,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64) void kv_attn_kernel(KvArgs a) {
     }
   }
 
-  if (HAS_NEW && !bad) kv_append_store(a, app, t0, h, split, b, slot, cs, dup);
+  if (HAS_NEW && !bad) kv_append_store(a, app, t0, h, split, slot, cs, dup.src == b);
 
   // Merge lane groups inside the wavefront (groups differ in lane bits >= log2(LPK)).
 #pragma unroll
@@ -563,7 +586,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
 
   const int slot = a.bidx ? a.bidx[b] : b;
   const int cs = HAS_NEW ? a.seqlens[b] : 0;
-  const KvDup dup = HAS_NEW ? kv_dup_scan(a, b, slot) : KvDup{INT_MAX, INT_MIN, 0ull, 0};
+  const KvDup dup = HAS_NEW ? kv_dup_classify(a, b, slot, cs) : KvDup{b, false};
   static_assert(SQ * 2 * (kHeadDim * 2 / 16) <= kWaves * 64, "one append piece per thread");
   const AppendPiece app = HAS_NEW ? kv_append_load<T>(a, b, t0, nq, h) : AppendPiece{};
   const bool bad = slot < 0 || slot >= a.n_slots || cs < 0 || (HAS_NEW && cs + a.sq > a.Lk);
@@ -572,6 +595,11 @@ __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
   if (split >= n_split_b) return;
   const int k_begin = split * a.split_len;
   const int k_end = bad ? k_begin : min(key_lim, k_begin + a.split_len);
+  if (HAS_NEW && dup.general && !bad) {
+    kv_general_row<T, SQ, kWaves>(a, app, b, h, slot, cs, t0, nq, a.n_qblocks > 1 ? SQ : nq, split, n_split_b,
+                                  k_begin, k_end, sm_acc, sm_m, sm_l);
+    return;
+  }
   // last key this lane's query may see (slots >= nq see none)
   int lim = k_end - 1;
   if (HAS_NEW) lim = min(lim, cs + t0 + qi);
@@ -588,20 +616,12 @@ __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
   const int safe_slot = bad ? 0 : slot;
   const char* kc_row = a.kc + safe_slot * a.kcs[0] + h * a.kcs[2];
   const char* vc_row = a.vc + safe_slot * a.vcs[0] + h * a.vcs[2];
-  const char* kn_row = HAS_NEW ? a.kn + b * a.kns[0] + h * a.kns[2] : nullptr;
-  const char* vn_row = HAS_NEW ? a.vn + b * a.vns[0] + h * a.vns[2] : nullptr;
-  // key rows another row naming this slot appends come from that row's k_new / v_new (kv_dup.h)
-  auto dup_ptr = [&](int key, const char* nb, const int64_t (&ns)[3], const char* crow, int64_t cstr) -> const char* {
-    int cw = 0;
-    const int w = kv_dup_winner(a, dup, safe_slot, key, cw);
-    return w >= 0 ? nb + w * ns[0] + h * ns[2] + (int64_t)(key - cw) * ns[1] : crow + (int64_t)key * cstr;
-  };
+  const char* kn_row = HAS_NEW ? a.kn + dup.src * a.kns[0] + h * a.kns[2] : nullptr;  // see kv_attn_kernel
+  const char* vn_row = HAS_NEW ? a.vn + dup.src * a.vns[0] + h * a.vns[2] : nullptr;
   auto k_ptr = [&](int key) __attribute__((always_inline)) {
-    if (HAS_NEW && kv_dup_in_window(dup, key)) return dup_ptr(key, a.kn, a.kns, kc_row, a.kcs[1]);
     return (HAS_NEW && key >= cs) ? kn_row + (int64_t)(key - cs) * a.kns[1] : kc_row + (int64_t)key * a.kcs[1];
   };
   auto v_ptr = [&](int key) __attribute__((always_inline)) {
-    if (HAS_NEW && kv_dup_in_window(dup, key)) return dup_ptr(key, a.vn, a.vns, vc_row, a.vcs[1]);
     return (HAS_NEW && key >= cs) ? vn_row + (int64_t)(key - cs) * a.vns[1] : vc_row + (int64_t)key * a.vcs[1];
   };
 
@@ -691,7 +711,7 @@ __global__ __launch_bounds__(kWavesPerWg * 64, 4) void kv_mq_kernel(KvArgs a) {
     for (int db = 0; db < 4; ++db) o[db] = Mfma16<T>::run(vop[db], pop, o[db]);
   }
 
-  if (HAS_NEW && !bad) kv_append_store(a, app, t0, h, split, b, slot, cs, dup);
+  if (HAS_NEW && !bad) kv_append_store(a, app, t0, h, split, slot, cs, dup.src == b);
 
   // row sums: the four lane groups hold different keys of the same query
   l += __shfl_xor(l, 16);
