@@ -163,3 +163,82 @@ def test_qkv_attention_helper(cuda):
     )
     ref = ref.transpose(0, 2, 1, 3).reshape(B, T, H * D)
     assert_close(out, ref, torch.float32, "qkv_attention")
+
+
+PIPE_SHAPES = [
+    # (B, H, Lq, Lk): grids of >= 256 workgroups of 384 queries route to dense_pipe_kernel;
+    # Lk covers an even / odd number of full 32-key steps, with and without a partial last step,
+    # and the loop's minimum of two tiles
+    (4, 64, 100, 64),
+    (4, 64, 100, 96),
+    (4, 64, 100, 100),
+    (4, 64, 100, 127),
+    (4, 64, 100, 160),
+    (2, 64, 400, 333),
+    (1, 128, 800, 1500),
+    (2, 128, 300, 2001),
+]
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,H,Lq,Lk", PIPE_SHAPES)
+def test_pipe_kernel_shapes(cuda, dtype, B, H, Lq, Lk):
+    """The hand-scheduled 384-query kernel on every head against a float64 evaluation on the
+    device, and a few heads against the float64 numpy oracle; 2e-2 max-abs."""
+    print(f"pipe dtype={dtype} B={B} H={H} Lq={Lq} Lk={Lk}", flush=True)
+    from whisperdrz_amd import scaled_dot_product_attention
+
+    D = 64
+    q = randn((B, Lq, H, D), 31 + Lk, dtype).to(cuda)
+    k = randn((B, Lk, H, D), 32 + Lk, dtype).to(cuda)
+    v = randn((B, Lk, H, D), 33 + Lk, dtype).to(cuda)
+    out = scaled_dot_product_attention(q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3),
+                                       scale=0.125)
+    torch.cuda.synchronize()
+    for b in range(B):
+        qb, kb, vb = (x[b].permute(1, 0, 2).double() for x in (q, k, v))
+        ref = torch.softmax(qb @ kb.transpose(1, 2) * 0.125, dim=-1) @ vb
+        err = (out[b].double() - ref).abs().max().item()
+        assert err <= 2e-2, f"b={b}: max|diff|={err:.3e}"
+    for b, h in ((0, 0), (B - 1, H - 1), (B // 2, H // 3)):
+        ref = sdpa_ref(to_np(q[b : b + 1, :, h : h + 1].permute(0, 2, 1, 3)),
+                       to_np(k[b : b + 1, :, h : h + 1].permute(0, 2, 1, 3)),
+                       to_np(v[b : b + 1, :, h : h + 1].permute(0, 2, 1, 3)), scale=0.125)
+        assert_close(out[b : b + 1, h : h + 1], ref, dtype, f"pipe b={b} h={h}")
+
+
+@pytest.mark.parametrize("case", ["growing", "shrinking", "bump", "flat_x6", "negative"])
+def test_pipe_kernel_large_scores(cuda, case):
+    """Scores far above the running max of earlier keys, so that the rare rescale runs in every
+    block and many steps (growing key norms, a bump of large keys, flat large scores), scores
+    whose first step holds the max (shrinking), and rows whose scores are all very negative (the
+    first step's max far below zero). The kernels pre-scale Q by scale*log2(e) in the input's
+    16-bit type; at these score magnitudes that rounding alone moves the output by more than the
+    N(0,1) tolerance, so the float64 reference here uses the same rounded Q: what is checked is
+    the online softmax, the rescaling and the merge. The remaining error is the 16-bit rounding of
+    P in peaked rows (the previous kernel gives the same outputs bit for bit); bound 3e-2."""
+    from whisperdrz_amd import scaled_dot_product_attention
+
+    B, H, Lq, Lk, D = 2, 128, 384, 700, 64
+    print(f"pipe large scores: {case}", flush=True)
+    q = randn((B, Lq, H, D), 5, torch.bfloat16).to(cuda)
+    k = randn((B, Lk, H, D), 6, torch.bfloat16).to(cuda)
+    v = randn((B, Lk, H, D), 7, torch.bfloat16).to(cuda)
+    ramp = {"growing": torch.linspace(0.2, 6.0, Lk), "shrinking": torch.linspace(6.0, 0.2, Lk),
+            "flat_x6": torch.full((Lk,), 6.0), "negative": torch.ones(Lk),
+            "bump": torch.where(torch.arange(Lk) % 97 == 50, 8.0, 1.0)}[case].to(cuda)
+    k = (k.float() * ramp[None, :, None, None]).to(torch.bfloat16)
+    if case == "negative":
+        q[:, :, ::7] = (q[:, :, ::7].float() * -40.0).to(torch.bfloat16)
+    out = scaled_dot_product_attention(q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3),
+                                       scale=0.125)
+    torch.cuda.synchronize()
+    c = 0.125 * 1.4426950408889634
+    q_eff = (q.float() * c).to(torch.bfloat16).double() / c  # Q as the kernel holds it
+    for b in range(B):
+        qb = q_eff[b].permute(1, 0, 2)
+        kb, vb = (x[b].permute(1, 0, 2).double() for x in (k, v))
+        ref = torch.softmax(qb @ kb.transpose(1, 2) * 0.125, dim=-1) @ vb
+        assert torch.isfinite(out[b]).all()
+        err = (out[b].double() - ref).abs().max().item()
+        assert err <= 3e-2, f"b={b}: max|diff|={err:.3e}"

@@ -33,7 +33,7 @@ def source_hash() -> str:
     header and this build script (flags). Stamped into the library (wdrz_build_id) so that a
     library built from other sources is refused at load time."""
     h = hashlib.sha256()
-    files = sorted(p for p in CSRC.iterdir() if p.suffix in (".hip", ".cpp", ".h"))
+    files = sorted(p for p in CSRC.iterdir() if p.suffix in (".hip", ".cpp", ".h", ".inc", ".py"))
     files += sorted((PKG_DIR.parent / "include").glob("*.h"))
     files.append(Path(__file__).resolve())
     for f in files:
@@ -55,6 +55,10 @@ def build_library(debug: bool = False, verbose: bool = False) -> Path:
     """Compile every source for gfx950 and link libwdrz_attn.so next to this file."""
     out_dir = PKG_DIR / "_build"
     out_dir.mkdir(exist_ok=True)
+    # the encoder kernel's hand-scheduled loop is generated (rewritten only when it changes)
+    gen = subprocess.run([sys.executable, str(CSRC / "gen_dense_loop.py")], capture_output=True, text=True)
+    if gen.returncode != 0:
+        raise RuntimeError(f"gen_dense_loop.py failed:\n{gen.stderr}")
     opt = ["-O1", "-g"] if debug else ["-O3"]
     common = [
         f"--offload-arch={ARCH}",

@@ -47,6 +47,7 @@
 #include "kv_dup.h"
 #include "wdrz_common.h"
 #include "wdrz_launch.h"
+#include "dense_loop.inc"
 
 #include <type_traits>
 
@@ -945,6 +946,356 @@ __global__ __launch_bounds__(kFThreads, 1) void dense_fwd_kernel(DenseArgs a) {
 }
 
 // ============================================================================================
+// Non-causal kernel with a hand-scheduled main loop (the encoder shape): 256-thread workgroups,
+// one wavefront per SIMD, 96 queries per wavefront (three 32-query blocks), 384 queries per
+// workgroup. With two wavefronts per SIMD (dense_fwd_kernel above) the softmax VALU work and the
+// MFMAs of the two largely serialise; here a single instruction stream per SIMD interleaves them
+// explicitly: while the VALU runs block b's softmax the matrix pipe runs the MFMAs of the block
+// before it, whose inputs are all a phase old (gen_dense_loop.py, which emits the loop, gives
+// the schedule and the register map). 384-query blocks also make the encoder launch whole rounds
+// (B=16: 320 heads x 4 blocks = 5 x 256 workgroups).
+//
+// The C++ around the loop stages Q (pre-scaled by scale*log2(e)) into its operand registers,
+// the first two K/V tiles into LDS and the third into the staging registers, and after the loop
+// finishes the last (partial) steps, normalises and stores O through LDS as whole rows.
+// ============================================================================================
+constexpr int kPWaves = 4;
+constexpr int kPThreads = kPWaves * 64;
+constexpr int kPBM = 96 * kPWaves;  // queries per workgroup
+constexpr int kPTile = kBN * kPitchK;  // elements of one 64-key tile buffer
+constexpr int kPMinKeys = 64;         // the loop needs two tiles up front
+
+typedef float f32x32 __attribute__((ext_vector_type(32)));
+typedef uint32_t u32x32 __attribute__((ext_vector_type(32)));
+typedef uint32_t u32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+
+// A raw buffer resource over [base, base + bytes): loads past the end return zero.
+__device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)(uintptr_t)base;
+  i32x4 r;
+  r[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+  r[1] = __builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32) & 0xffff);  // stride 0
+  r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+  r[3] = 0x00020000;  // 32-bit data format, no swizzle
+  return r;
+}
+
+template <typename T>
+__global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void dense_pipe_kernel(DenseArgs a) {
+  typedef typename Mfma<T>::op_t op_t;
+  typedef uint16_t e_t;
+  // four K tile buffers, then four V tile buffers, row-major [key][dim] with a 16-byte row pad;
+  // Q and O are staged through the same memory at the start and the end
+  __shared__ __attribute__((aligned(16))) e_t smem[8 * kPTile];
+  static_assert(kPBM * kPitchK <= 8 * kPTile, "Q/O staging must fit the tile buffers");
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int hl = lane >> 5;
+  const int l32 = lane & 31;
+
+  const int n_qblk = (a.Lq + kPBM - 1) / kPBM;
+  const int tile_id = remap_xcd(blockIdx.x, gridDim.x);
+  const int qblk = tile_id % n_qblk;
+  const int bh = tile_id / n_qblk;
+  const int b = bh / a.H, h = bh % a.H;
+  const e_t* Q = reinterpret_cast<const e_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
+  const e_t* K = reinterpret_cast<const e_t*>(a.k) + b * a.ks[0] + h * a.ks[1];
+  const e_t* V = reinterpret_cast<const e_t*>(a.v) + b * a.vs[0] + h * a.vs[1];
+  e_t* O = reinterpret_cast<e_t*>(a.o) + b * a.os[0] + h * a.os[1];
+  const int q_blk0 = qblk * kPBM;
+  const float c = a.c;
+
+  // Row-contiguous transfers: thread tid moves 16-byte chunk (tid & 7) of rows tid/8 + 32*i.
+  const int crow = tid >> 3, cd0 = (tid & 7) * 8;
+  const int rs_k = (int)a.ks[2] * 2, rs_v = (int)a.vs[2] * 2;  // row strides in bytes
+  const i32x4 srd_k = buffer_rsrc(K, (uint32_t)((a.Lk - 1) * rs_k + 128));
+  const i32x4 srd_v = buffer_rsrc(V, (uint32_t)((a.Lk - 1) * rs_v + 128));
+  auto tile_load = [&](int kt, u32x4 (&st)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int r = kt * kBN + crow + 32 * i;
+      const bool in = r < a.Lk;
+      const int rc = in ? r : a.Lk - 1;
+      st[i] = load16(K + (int64_t)rc * a.ks[2] + cd0);
+      st[2 + i] = load16(V + (int64_t)rc * a.vs[2] + cd0);
+      if (!in) st[i] = st[2 + i] = u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  const int st_off = crow * kPitchK + cd0;  // elements
+  auto tile_store = [&](int buf, const u32x4 (&st)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      *reinterpret_cast<u32x4*>(&smem[buf * kPTile + st_off + 32 * i * kPitchK]) = st[i];
+      *reinterpret_cast<u32x4*>(&smem[(4 + buf) * kPTile + st_off + 32 * i * kPitchK]) = st[2 + i];
+    }
+  };
+
+  // ---- Q: whole rows into LDS, then each wavefront's operand registers, pre-scaled by c ----
+  u32x4 t0[4], t1[4], stage[4];
+  {
+    u32x4 qc[kPBM / 32];
+#pragma unroll
+    for (int i = 0; i < kPBM / 32; ++i) qc[i] = load16(Q + min(q_blk0 + crow + 32 * i, a.Lq - 1) * a.qs[2] + cd0);
+    tile_load(0, t0);
+    tile_load(1, t1);
+#pragma unroll
+    for (int i = 0; i < kPBM / 32; ++i) *reinterpret_cast<u32x4*>(&smem[(crow + 32 * i) * kPitchK + cd0]) = qc[i];
+  }
+  __syncthreads();
+  u32x16 q0, q1, q2;
+#pragma unroll
+  for (int qb = 0; qb < 3; ++qb)
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      const u32x4 raw =
+          *reinterpret_cast<const u32x4*>(&smem[(wave * 96 + qb * 32 + l32) * kPitchK + ks * 16 + hl * 8]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t w = Mfma<T>::pack(Mfma<T>::widen_lo(raw[e]) * c, Mfma<T>::widen_hi(raw[e]) * c);
+        (qb == 0 ? q0 : qb == 1 ? q1 : q2)[ks * 4 + e] = w;
+      }
+    }
+  __syncthreads();
+  tile_store(0, t0);
+  tile_store(1, t1);
+  tile_load(2, stage);
+  __syncthreads();
+
+  // ---- the hand-scheduled loop over pairs of 32-key steps (full tiles only) ----
+  const int n_sub = (a.Lk + kBS - 1) / kBS;
+  const int n_iter = (a.Lk / kBS) / 2;
+  const int s_end = 2 * n_iter;
+  // LDS byte offsets of this lane's operand reads (the permuted K rows; V^T through the
+  // transposing read), and of its tile stores
+  const int pm = l32;
+  const int pi_row = 16 * ((pm >> 3) >> 1) + 8 * ((pm >> 2) & 1) + 4 * ((pm >> 3) & 1) + (pm & 3);
+  const int g16 = lane >> 4, j16 = lane & 15;
+  const uint32_t klane = (uint32_t)(pi_row * kPitchK + hl * 8) * 2;
+  const uint32_t vlane = (uint32_t)((8 * (g16 >> 1) + (j16 >> 2)) * kPitchK + 16 * (g16 & 1) + 4 * (j16 & 3)) * 2;
+  const uint32_t stlane = (uint32_t)st_off * 2;
+  // global byte offsets of this thread's rows in tile 3 (the first the loop requests)
+  u32x4 voff;
+  voff[0] = (3 * kBN + crow) * rs_k + cd0 * 2;
+  voff[1] = voff[0] + 32 * rs_k;
+  voff[2] = (3 * kBN + crow) * rs_v + cd0 * 2;
+  voff[3] = voff[2] + 32 * rs_v;
+  const int tsk = kBN * rs_k, tsv = kBN * rs_v;
+  u32x16 stg;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) stg[4 * i + e] = stage[i][e];
+
+  f32x16 o00, o01, o10, o11, o20, o21;
+  op_t kop[4], vop[2][2], vpr[2][2];  // K(s_end), V(s_end), V(s_end - 1) operands after the loop
+  typedef float f32x6 __attribute__((ext_vector_type(6)));
+  typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
+  f32x6 ml;  // m_run[3], l_run[3]
+  const u32x3 lanes = {klane, vlane, stlane};
+  f32x32 s01;
+  f32x16 s2;
+  f32x32 ci01;
+  f32x16 ci2;
+  u32x16 p01;
+  u32x8 p2;
+  __builtin_amdgcn_sched_barrier(0);
+  if constexpr (__is_same(T, Bf16)) {
+    asm volatile(WDRZ_DENSE_LOOP_BF16
+                 : "={a[0:15]}"(o00), "={a[16:31]}"(o01), "={a[32:47]}"(o10), "={a[48:63]}"(o11), "={a[64:79]}"(o20),
+                   "={a[80:95]}"(o21), "={a[144:147]}"(kop[0]), "={a[148:151]}"(kop[1]), "={a[152:155]}"(kop[2]),
+                   "={a[156:159]}"(kop[3]), "={a[176:179]}"(vop[0][0]), "={a[180:183]}"(vop[0][1]),
+                   "={a[184:187]}"(vop[1][0]), "={a[188:191]}"(vop[1][1]), "={a[192:195]}"(vpr[0][0]),
+                   "={a[196:199]}"(vpr[0][1]), "={a[200:203]}"(vpr[1][0]), "={a[204:207]}"(vpr[1][1]),
+                   "={v[0:31]}"(s01), "={v[32:47]}"(s2), "={v[48:79]}"(ci01), "={v[80:95]}"(ci2), "={v[96:111]}"(p01),
+                   "={v[112:119]}"(p2), "+{v[136:151]}"(stg), "={v[152:157]}"(ml), "+{v[162:165]}"(voff)
+                 : "{a[96:111]}"(q0), "{a[112:127]}"(q1), "{a[128:143]}"(q2), "{v[158:160]}"(lanes),
+                   "{s[80:83]}"(srd_k), "{s[84:87]}"(srd_v), [n] "s"(n_iter), [tsk] "s"(tsk), [tsv] "s"(tsv)
+                 : "a160", "a161", "a162", "a163", "a164", "a165", "a166", "a167", "a168", "a169", "a170", "a171", "a172",
+                   "a173", "a174", "a175", "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127", "v128",
+                   "v129", "v130", "v131",
+                   "v132", "v133", "v134", "v135", "v161", "v166", "v167", "v168", "v169", "v170", "v171", "v172",
+                   "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180", "v181", "v184", "v185", "v186",
+                   "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195", "v196", "v197", "v198",
+                   "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "s70",
+                   "s71", "s72", "s73", "s74", "s75", "s76", "s77", "s78", "s79", "vcc", "scc", "memory");
+  } else {
+    asm volatile(WDRZ_DENSE_LOOP_F16
+                 : "={a[0:15]}"(o00), "={a[16:31]}"(o01), "={a[32:47]}"(o10), "={a[48:63]}"(o11), "={a[64:79]}"(o20),
+                   "={a[80:95]}"(o21), "={a[144:147]}"(kop[0]), "={a[148:151]}"(kop[1]), "={a[152:155]}"(kop[2]),
+                   "={a[156:159]}"(kop[3]), "={a[176:179]}"(vop[0][0]), "={a[180:183]}"(vop[0][1]),
+                   "={a[184:187]}"(vop[1][0]), "={a[188:191]}"(vop[1][1]), "={a[192:195]}"(vpr[0][0]),
+                   "={a[196:199]}"(vpr[0][1]), "={a[200:203]}"(vpr[1][0]), "={a[204:207]}"(vpr[1][1]),
+                   "={v[0:31]}"(s01), "={v[32:47]}"(s2), "={v[48:79]}"(ci01), "={v[80:95]}"(ci2), "={v[96:111]}"(p01),
+                   "={v[112:119]}"(p2), "+{v[136:151]}"(stg), "={v[152:157]}"(ml), "+{v[162:165]}"(voff)
+                 : "{a[96:111]}"(q0), "{a[112:127]}"(q1), "{a[128:143]}"(q2), "{v[158:160]}"(lanes),
+                   "{s[80:83]}"(srd_k), "{s[84:87]}"(srd_v), [n] "s"(n_iter), [tsk] "s"(tsk), [tsv] "s"(tsv)
+                 : "a160", "a161", "a162", "a163", "a164", "a165", "a166", "a167", "a168", "a169", "a170", "a171", "a172",
+                   "a173", "a174", "a175", "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127", "v128",
+                   "v129", "v130", "v131",
+                   "v132", "v133", "v134", "v135", "v161", "v166", "v167", "v168", "v169", "v170", "v171", "v172",
+                   "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180", "v181", "v184", "v185", "v186",
+                   "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195", "v196", "v197", "v198",
+                   "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "s70",
+                   "s71", "s72", "s73", "s74", "s75", "s76", "s77", "s78", "s79", "vcc", "scc", "memory");
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- the remaining steps (the partial last one, and a full one when the full steps are odd).
+  // State after the loop: S(s_end) of blocks 0, 1; P(s_end - 1) of block 2, whose P V and whose
+  // scores S(s_end) the loop leaves to the next step; K(s_end) in K buffer 0, V(s_end) in V buffer
+  // 0 and V(s_end - 1) in V buffer 1.
+  f32x16 acc_o[3][2], sacc[3], cinit[3];
+  op_t qop[3][4], pcur[3][2];
+  float m_run[3] = {ml[0], ml[1], ml[2]}, l_run[3] = {ml[3], ml[4], ml[5]};
+  acc_o[0][0] = o00;
+  acc_o[0][1] = o01;
+  acc_o[1][0] = o10;
+  acc_o[1][1] = o11;
+  acc_o[2][0] = o20;
+  acc_o[2][1] = o21;
+#pragma unroll
+  for (int x = 0; x < 16; ++x) {
+    sacc[0][x] = s01[x];
+    sacc[1][x] = s01[16 + x];
+    sacc[2][x] = s2[x];
+    cinit[0][x] = ci01[x];
+    cinit[1][x] = ci01[16 + x];
+    cinit[2][x] = ci2[x];
+  }
+  auto op4 = [](uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) { return __builtin_bit_cast(op_t, u32x4{w0, w1, w2, w3}); };
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    qop[0][ks] = op4(q0[4 * ks], q0[4 * ks + 1], q0[4 * ks + 2], q0[4 * ks + 3]);
+    qop[1][ks] = op4(q1[4 * ks], q1[4 * ks + 1], q1[4 * ks + 2], q1[4 * ks + 3]);
+    qop[2][ks] = op4(q2[4 * ks], q2[4 * ks + 1], q2[4 * ks + 2], q2[4 * ks + 3]);
+  }
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch) {
+    pcur[0][ch] = op4(p01[4 * ch], p01[4 * ch + 1], p01[4 * ch + 2], p01[4 * ch + 3]);
+    pcur[1][ch] = op4(p01[8 + 4 * ch], p01[9 + 4 * ch], p01[10 + 4 * ch], p01[11 + 4 * ch]);
+    pcur[2][ch] = op4(p2[4 * ch], p2[4 * ch + 1], p2[4 * ch + 2], p2[4 * ch + 3]);
+  }
+  // P(s_end - 1) V(s_end - 1) of block 2
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+    for (int db = 0; db < 2; ++db) {
+      acc_o[2][db] = Mfma<T>::run(vpr[ch][db], pcur[2][ch], acc_o[2][db]);
+    }
+  auto mfma_s = [&](int qb) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) sacc[qb] = Mfma<T>::run(kop[ks], qop[qb][ks], ks == 0 ? cinit[qb] : sacc[qb]);
+  };
+  if (s_end < n_sub) mfma_s(2);
+  auto read_k = [&](int s) __attribute__((always_inline)) {
+    const e_t* kb = &smem[((s >> 1) & 3) * kPTile + (s & 1) * 32 * kPitchK] + klane / 2;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) kop[ks] = __builtin_bit_cast(op_t, *reinterpret_cast<const u32x4*>(kb + ks * 16));
+  };
+  auto read_v = [&](int s) __attribute__((always_inline)) {
+    const e_t* vb = &smem[(4 + ((s >> 1) & 3)) * kPTile + (s & 1) * 32 * kPitchK] + vlane / 2;
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+      for (int db = 0; db < 2; ++db) {
+        const e_t* p = vb + ch * 16 * kPitchK + db * 32;
+        const u32x2 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 4 * kPitchK);
+        vop[ch][db] = __builtin_bit_cast(op_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
+      }
+  };
+  // online softmax of step s for block qb, as in dense_fwd_kernel (keys past Lk masked; the
+  // first step takes the true max)
+  auto exp_sum = [&](int qb) __attribute__((always_inline)) {
+    float t[4];
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      u32x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float p0 = fast_exp2(sacc[qb][ch * 8 + 2 * e]);
+        const float p1 = fast_exp2(sacc[qb][ch * 8 + 2 * e + 1]);
+        w[e] = Mfma<T>::pack(p0, p1);
+        t[e] = ch == 0 ? p0 + p1 : t[e] + p0 + p1;
+      }
+      pcur[qb][ch] = __builtin_bit_cast(op_t, w);
+    }
+    return (t[0] + t[1]) + (t[2] + t[3]);
+  };
+  for (int s = s_end; s < n_sub; ++s) {
+    if (s > s_end) read_v(s);
+    const bool more = s + 1 < n_sub;
+    if (more) read_k(s + 1);
+    const int k0 = s * kBS;
+#pragma unroll
+    for (int qb = 0; qb < 3; ++qb) {
+      if (k0 + kBS > a.Lk) {
+#pragma unroll
+        for (int x = 0; x < 16; ++x)
+          if (k0 + 16 * (x >> 3) + 8 * hl + (x & 7) >= a.Lk) sacc[qb][x] = -INFINITY;
+      }
+      float st = s == 0 ? INFINITY : exp_sum(qb);
+      if (__any(!(st <= kSumLimit))) {
+        const f32x16& v = sacc[qb];
+        float mx = v[0];
+#pragma unroll
+        for (int x = 1; x < 16; ++x) mx = fmaxf(mx, v[x]);
+        mx = half_swap_max(mx);
+        const float delta = s == 0 ? mx : fmaxf(mx, 0.f);
+        m_run[qb] += delta;
+        if (s != 0) {  // (the first step has nothing to rescale; exp2(-delta) may be inf there)
+          const float alpha = fast_exp2(-delta);
+          l_run[qb] *= alpha;
+#pragma unroll
+          for (int db = 0; db < 2; ++db)
+#pragma unroll
+            for (int x = 0; x < 16; ++x) acc_o[qb][db][x] *= alpha;
+        }
+#pragma unroll
+        for (int x = 0; x < 16; ++x) {
+          sacc[qb][x] -= delta;
+          cinit[qb][x] = -m_run[qb];
+        }
+        st = exp_sum(qb);
+      }
+      l_run[qb] += st;
+#pragma unroll
+      for (int ch = 0; ch < 2; ++ch)
+#pragma unroll
+        for (int db = 0; db < 2; ++db) acc_o[qb][db] = Mfma<T>::run(vop[ch][db], pcur[qb][ch], acc_o[qb][db]);
+      if (more) mfma_s(qb);
+    }
+  }
+
+  // ---- normalise, stage O^T through LDS as [query][dim] rows, store whole rows ----
+  __syncthreads();  // every wavefront is done with the tiles
+#pragma unroll
+  for (int qb = 0; qb < 3; ++qb) {
+    const float inv = 1.f / (l_run[qb] + __shfl_xor(l_run[qb], 32));
+    e_t* orow = &smem[(wave * 96 + qb * 32 + l32) * kPitchK];
+#pragma unroll
+    for (int db = 0; db < 2; ++db)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        u32x2 w;
+        w[0] = Mfma<T>::pack(acc_o[qb][db][i * 4 + 0] * inv, acc_o[qb][db][i * 4 + 1] * inv);
+        w[1] = Mfma<T>::pack(acc_o[qb][db][i * 4 + 2] * inv, acc_o[qb][db][i * 4 + 3] * inv);
+        *reinterpret_cast<u32x2*>(orow + db * 32 + i * 8 + hl * 4) = w;
+      }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < kPBM / 32; ++i) {
+    const int qi = q_blk0 + crow + 32 * i;
+    if (qi < a.Lq)
+      store16(O + qi * a.os[2] + cd0, *reinterpret_cast<const u32x4*>(&smem[(crow + 32 * i) * kPitchK + cd0]));
+  }
+}
+
+// ============================================================================================
 // Key-split kernel (non-causal, small grids): a workgroup holds four query groups of 32*QB
 // queries; each group is served by two wavefronts on the same SIMD (waves g and g+4), one per
 // 32-key half of every 64-key tile, which merge their (m, l, O) through LDS at the end. Per query
@@ -1450,6 +1801,12 @@ hipError_t launch_typed(const DenseArgs& a, hipStream_t stream) {
     };
     if (bh * q2 <= kNumCus) {
       split(a, bh);
+      return hipGetLastError();
+    }
+    // the hand-scheduled 384-query kernel when its grid fills the chip
+    const int64_t np = bh * ((a.Lq + kPBM - 1) / kPBM);
+    if (a.Lk >= kPMinKeys && np >= kNumCus && np <= 0x7fffffff) {
+      hipLaunchKernelGGL((dense_pipe_kernel<T>), dim3((unsigned)np), dim3(kPThreads), 0, stream, a);
       return hipGetLastError();
     }
     const int64_t bh_main = (n / kNumCus) * kNumCus / qf;  // heads filling whole rounds

@@ -1,0 +1,328 @@
+"""Generates dense_loop.inc: the hand-scheduled main loop of dense_pipe_kernel (attn_dense.hip).
+
+Usage: python gen_dense_loop.py [out_path]   (whisperdrz_amd/build.py runs it before compiling)
+
+The loop is one inline-asm statement per element type (bf16 / fp16) over physical registers that
+the kernel binds with register constraints. Design (one wavefront per SIMD, 96 queries per
+wavefront as three 32-query blocks b = 0, 1, 2; 32 keys per step, 64-key LDS tiles):
+
+  * Each step s runs three phases. Phase b runs the online softmax of block b's scores S(s)[b]
+    on the VALU (exp2, bf16/fp16 packs of P, row sums, the rescale check) while the matrix pipe
+    runs the MFMAs of the previous block: in phase 1 and 2 those of blocks 0 and 1 (P(s)V(s) and
+    the next step's scores S(s+1) = K(s+1) Q^T), in phase 0 those of block 2 of the previous step
+    (P(s-1)V(s-1) and S(s)[2]). Every MFMA input was produced at least one phase earlier and every
+    VALU input at least one phase earlier, so no instruction waits on the one just issued: the
+    in-order instruction stream keeps the matrix pipe and the VALU busy side by side (8 MFMAs and
+    ~45 VALU instructions per phase, ~5 VALU instructions between MFMAs).
+  * The running max is subtracted inside the MFMA: every score chain starts from cinit[b] =
+    -m_run[b]. The rescale check runs on the step's row sum (a lane's 16 P values summing above
+    1024 means a score exceeded the max by more than 6 in log2 units); the rare rescale takes
+    the true max, rescales O (AGPRs), l and cinit, and redoes the block's softmax. The first
+    step always takes it (its limit register is -1), which establishes the max. The compare is
+    placed a few instructions before the phase's branch (a branch on a VCC the VALU has only just
+    written stalls the in-order wavefront).
+  * K and V operands for the MFMAs come from LDS one step ahead into double-buffered AGPRs
+    (K through ds_read_b128 in the permuted key order that makes P^T the B operand without
+    shuffles; V^T through ds_read_b64_tr_b16). Tiles of 64 keys are staged global -> VGPR ->
+    LDS through four LDS buffers: tile t+2 is written and tile t+3 requested during tile t,
+    one workgroup barrier per tile. Global loads are buffer loads bounded by the tensor's extent
+    (rows past the last key read as zero; those keys are never used unmasked).
+
+Register map (the kernel passes these through "{v[..]}" / "{a[..]}" constraints):
+  v0-47 S[b] (16 each)   v48-95 cinit[b]   v96-119 P[b] (8 each: two 16-key chunks)
+  v120-135 exp temps     v136-151 tile staging (K rows r, r+32, V rows r, r+32)
+  v152-154 m_run[b]      v155-157 l_run[b] (this lane's half of the row sum)
+  v158 K read lane base  v159 V read lane base  v160 tile store lane base
+  v162-165 global row offsets (K r, K r+32, V r, V r+32)   v166-181 addresses, temporaries
+  v184-207 row-sum temporaries (8 per block)
+  a0-95 O[b][db] (16 each)   a96-143 Q[b][ks] (4 each)   a144-175 K buffers (2 x 16)
+  a176-207 V buffers (2 x 16: [ch][db] operands of 4)
+  s70-s79 loop state (clobbered: iteration, tile offsets, sum limit, rescale floor); the kernel passes the buffer resources in s[80:83], s[84:87].
+"""
+import sys
+from pathlib import Path
+
+# ---- register map --------------------------------------------------------------------------
+def S(b): return 16 * b
+def CINIT(b): return 48 + 16 * b
+def P(b, ch=0): return 96 + 8 * b + 4 * ch
+T0 = 120
+STAGE = 136
+def U(b): return 184 + 8 * b  # row-sum temporaries of block b (184..207)
+def MRUN(b): return 152 + b
+def LRUN(b): return 155 + b
+KLANE, VLANE, STLANE = 158, 159, 160
+VOFF = 162  # 162..165 (a 4-register tuple: even-aligned)
+KADDR, VADDRA, VADDRB, STADDR = 166, 167, 168, 169
+RT = 170  # rare-path temporaries 170..181
+def O(b, db): return 32 * b + 16 * db
+def Q(b, ks): return 96 + 16 * b + 4 * ks
+def KB(p, ks): return 144 + 16 * p + 4 * ks
+def VB(p, ch, db): return 176 + 16 * p + 8 * ch + 4 * db
+
+S_N = None  # the iteration count comes in through an operand: %[n]
+S_IT, S_BUFA, S_BUFB, S_BUFC, S_TMP = "s70", "s71", "s72", "s73", "s74"
+S_LIMIT, S_FLOOR = "s76", "s78"
+SRD_K, SRD_V = "s[80:83]", "s[84:87]"
+
+TILE_BYTES = 64 * 72 * 2   # one 64-key tile of K (or V): 64 rows x 72 elements (16-byte pad)
+HALF_BYTES = 32 * 72 * 2   # 32 key rows
+V_BASE = 4 * TILE_BYTES    # the V tiles follow the four K tiles
+SUM_LIMIT = "0x44800000"   # 1024.0f
+
+
+def vr(lo, n=1):
+    return f"v{lo}" if n == 1 else f"v[{lo}:{lo + n - 1}]"
+
+
+def ar(lo, n=1):
+    return f"a{lo}" if n == 1 else f"a[{lo}:{lo + n - 1}]"
+
+
+class Gen:
+    def __init__(self, dtype):
+        self.mfma = "v_mfma_f32_32x32x16_bf16" if dtype == "bf16" else "v_mfma_f32_32x32x16_f16"
+        self.cvt = "v_cvt_pk_bf16_f32" if dtype == "bf16" else "v_cvt_pk_f16_f32"
+        self.out = []
+        self.rare = []
+
+    def emit(self, s, into=None):
+        (self.out if into is None else into).append(s)
+
+    # ---- building blocks ---------------------------------------------------------------------
+    def mfma_s(self, b, ks, kbuf):
+        c = vr(CINIT(b), 16) if ks == 0 else vr(S(b), 16)
+        return f"{self.mfma} {vr(S(b), 16)}, {ar(KB(kbuf, ks), 4)}, {ar(Q(b, ks), 4)}, {c}"
+
+    def mfma_pv(self, b, ch, db, vbuf):
+        return f"{self.mfma} {ar(O(b, db), 16)}, {ar(VB(vbuf, ch, db), 4)}, {vr(P(b, ch), 4)}, {ar(O(b, db), 16)}"
+
+    def softmax_valu(self, b, check=True):
+        """exp2 of the 16 scores, the row sum into T0 (pairs, then a tree), the rescale check into
+        vcc, then the packs of P. The compare comes two MFMA slots before the phase's branch: a
+        branch on a VCC that the VALU has only just written stalls the wavefront."""
+        v = []
+        for i in range(16):
+            v.append(f"v_exp_f32 {vr(T0 + i)}, {vr(S(b) + i)}")
+        for j in range(8):
+            v.append(f"v_add_f32 {vr(U(b) + j)}, {vr(T0 + 2 * j)}, {vr(T0 + 2 * j + 1)}")
+        for k in range(4):
+            v.append(f"v_add_f32 {vr(U(b) + 2 * k)}, {vr(U(b) + 2 * k)}, {vr(U(b) + 2 * k + 1)}")
+        v.append(f"v_add_f32 {vr(U(b))}, {vr(U(b))}, {vr(U(b) + 2)}")
+        v.append(f"v_add_f32 {vr(U(b) + 4)}, {vr(U(b) + 4)}, {vr(U(b) + 6)}")
+        v.append(f"v_add_f32 {vr(U(b))}, {vr(U(b))}, {vr(U(b) + 4)}")
+        if check:
+            # sum > limit in any lane -> rescale; the limit register is -1 in the first step, so
+            # that step always takes the true max
+            v.append(f"v_cmp_lt_f32 vcc, {S_LIMIT}, {vr(U(b))}")
+        for j in range(8):
+            v.append(f"{self.cvt} {vr(P(b) + j)}, {vr(T0 + 2 * j)}, {vr(T0 + 2 * j + 1)}")
+        return v
+
+    def rare_block(self, b, label, back):
+        """Rescale of block b (rare): true max, O / l / cinit rescaled, softmax redone."""
+        r = self.rare
+        r.append(f"{label}:")
+        r.append("s_nop 7")
+        r.append("s_nop 7")
+        mx, mx2, dl, al = RT, RT + 1, RT + 2, RT + 3
+        s0 = S(b)
+        r.append(f"v_max3_f32 {vr(mx)}, {vr(s0)}, {vr(s0 + 1)}, {vr(s0 + 2)}")
+        for i in range(3, 15, 2):
+            r.append(f"v_max3_f32 {vr(mx)}, {vr(mx)}, {vr(s0 + i)}, {vr(s0 + i + 1)}")
+        r.append(f"v_max_f32 {vr(mx)}, {vr(mx)}, {vr(s0 + 15)}")
+        r.append(f"v_mov_b32 {vr(mx2)}, {vr(mx)}")
+        r.append("s_nop 1")
+        r.append(f"v_permlane32_swap_b32 {vr(mx)}, {vr(mx2)}")
+        r.append(f"v_max3_f32 {vr(dl)}, {vr(mx)}, {vr(mx2)}, {S_FLOOR}")  # delta (>= 0 except forced)
+        r.append(f"v_add_f32 {vr(MRUN(b))}, {vr(MRUN(b))}, {vr(dl)}")
+        r.append(f"v_exp_f32_e64 {vr(al)}, -{vr(dl)}")
+        r.append("s_nop 1")  # a transcendental's result is not forwarded to the next VALU instruction
+        # alpha <= 1: in the forced first step delta may be any negative number, but O and l are
+        # still zero there, and exp2(-delta) = inf would turn them into NaN
+        r.append(f"v_min_f32 {vr(al)}, 1.0, {vr(al)}")
+        r.append(f"v_mul_f32 {vr(LRUN(b))}, {vr(LRUN(b))}, {vr(al)}")
+        tmp = [RT + 4 + i for i in range(8)]
+        for i0 in range(0, 32, 8):
+            for i in range(8):
+                r.append(f"v_accvgpr_read_b32 {vr(tmp[i])}, {ar(O(b, 0) + i0 + i)}")
+            for i in range(8):
+                r.append(f"v_mul_f32 {vr(tmp[i])}, {vr(al)}, {vr(tmp[i])}")
+            for i in range(8):
+                r.append(f"v_accvgpr_write_b32 {ar(O(b, 0) + i0 + i)}, {vr(tmp[i])}")
+        for i in range(16):
+            r.append(f"v_sub_f32 {vr(CINIT(b) + i)}, 0, {vr(MRUN(b))}")
+        for i in range(16):
+            r.append(f"v_sub_f32 {vr(S(b) + i)}, {vr(S(b) + i)}, {vr(dl)}")
+        r.extend(self.softmax_valu(b, check=False))
+        r.append("s_nop 4")
+        r.append(f"s_branch {back}")
+
+    def phase(self, p, ph, pre=(), slots=None):
+        """One phase of a step of parity p. slots: {mfma index: [extra instructions after it]}."""
+        slots = slots or {}
+        if ph == 0:
+            mb, kbuf, vbuf = 2, p, 1 - p
+        else:
+            mb, kbuf, vbuf = ph - 1, 1 - p, p
+        mf = []
+        for ks in range(4):
+            mf.append(self.mfma_s(mb, ks, kbuf))
+            ch, db = divmod(ks, 2)
+            mf.append(self.mfma_pv(mb, ch, db, vbuf))
+        valu = self.softmax_valu(ph)
+        for s in pre:
+            self.emit(s)
+        # spread the VALU list over the 8 MFMA slots
+        n = len(valu)
+        k = 0
+        for i in range(8):
+            self.emit(mf[i])
+            for s in slots.get(i, []):
+                self.emit(s)
+            hi = (n * (i + 1)) // 8
+            while k < hi:
+                self.emit(valu[k])
+                k += 1
+        # check: sum > limit in any lane, or the forced first step -> rescale
+        label = f"R{ph}P{p}_%="
+        back = f"B{ph}P{p}_%="
+        self.emit(f"s_cbranch_vccnz {label}")
+        self.emit(f"{back}:")
+        self.emit(f"v_add_f32 {vr(LRUN(ph))}, {vr(LRUN(ph))}, {vr(U(ph))}")
+        self.rare_block(ph, label, back)
+
+    def k_reads(self, p):
+        """K(s+2) -> K buffer p: tile t+1, half p (base KADDR)."""
+        return [f"ds_read_b128 {ar(KB(p, ks), 4)}, {vr(KADDR)} offset:{p * HALF_BYTES + ks * 32}" for ks in range(4)]
+
+    def v_reads(self, p):
+        """V(s+1) -> V buffer 1-p: step 2t: tile t half 1 (VADDRA); step 2t+1: tile t+1 half 0 (VADDRB)."""
+        base, half = (VADDRA, 1) if p == 0 else (VADDRB, 0)
+        out = []
+        for ch in range(2):
+            for db in range(2):
+                off = V_BASE + half * HALF_BYTES + ch * 16 * 144 + db * 64
+                dst = VB(1 - p, ch, db)
+                out.append(f"ds_read_b64_tr_b16 {ar(dst, 2)}, {vr(base)} offset:{off}")
+                out.append(f"ds_read_b64_tr_b16 {ar(dst + 2, 2)}, {vr(base)} offset:{off + 4 * 144}")
+        return out
+
+    def staging(self):
+        """Tile t+2 from the staging registers into LDS; tile t+3 requested into them."""
+        w = [
+            "s_waitcnt vmcnt(0)",
+            f"ds_write_b128 {vr(STADDR)}, {vr(STAGE, 4)}",
+            f"ds_write_b128 {vr(STADDR)}, {vr(STAGE + 4, 4)} offset:{HALF_BYTES}",
+            f"ds_write_b128 {vr(STADDR)}, {vr(STAGE + 8, 4)} offset:{V_BASE}",
+            f"ds_write_b128 {vr(STADDR)}, {vr(STAGE + 12, 4)} offset:{V_BASE + HALF_BYTES}",
+        ]
+        ld = [
+            f"buffer_load_dwordx4 {vr(STAGE, 4)}, {vr(VOFF)}, {SRD_K}, 0 offen",
+            f"buffer_load_dwordx4 {vr(STAGE + 4, 4)}, {vr(VOFF + 1)}, {SRD_K}, 0 offen",
+            f"buffer_load_dwordx4 {vr(STAGE + 8, 4)}, {vr(VOFF + 2)}, {SRD_V}, 0 offen",
+            f"buffer_load_dwordx4 {vr(STAGE + 12, 4)}, {vr(VOFF + 3)}, {SRD_V}, 0 offen",
+        ]
+        adv = [
+            f"v_add_u32 {vr(VOFF)}, %[tsk], {vr(VOFF)}",
+            f"v_add_u32 {vr(VOFF + 1)}, %[tsk], {vr(VOFF + 1)}",
+            f"v_add_u32 {vr(VOFF + 2)}, %[tsv], {vr(VOFF + 2)}",
+            f"v_add_u32 {vr(VOFF + 3)}, %[tsv], {vr(VOFF + 3)}",
+        ]
+        return w, ld, adv
+
+    def build(self):
+        e = self.emit
+        # ---- prologue: first operands, zero state, scores of step 0 for blocks 0 and 1 ----
+        for ks in range(4):
+            e(f"ds_read_b128 {ar(KB(0, ks), 4)}, {vr(KLANE)} offset:{ks * 32}")
+            e(f"ds_read_b128 {ar(KB(1, ks), 4)}, {vr(KLANE)} offset:{HALF_BYTES + ks * 32}")
+        for ch in range(2):
+            for db in range(2):
+                off = V_BASE + ch * 16 * 144 + db * 64
+                e(f"ds_read_b64_tr_b16 {ar(VB(0, ch, db), 2)}, {vr(VLANE)} offset:{off}")
+                e(f"ds_read_b64_tr_b16 {ar(VB(0, ch, db) + 2, 2)}, {vr(VLANE)} offset:{off + 4 * 144}")
+        for i in range(16):
+            e(f"v_accvgpr_write_b32 {ar(VB(1, 0, 0) + i)}, 0")
+        for i in range(8):
+            e(f"v_mov_b32 {vr(P(2) + i)}, 0")
+        for i in range(48):
+            e(f"v_mov_b32 {vr(CINIT(0) + i)}, 0")
+        for i in range(96):
+            e(f"v_accvgpr_write_b32 {ar(i)}, 0")
+        for b in range(3):
+            e(f"v_mov_b32 {vr(MRUN(b))}, 0")
+            e(f"v_mov_b32 {vr(LRUN(b))}, 0")
+        e("s_waitcnt lgkmcnt(0)")
+        for b in range(2):
+            for ks in range(4):
+                c = "0" if ks == 0 else vr(S(b), 16)
+                e(f"{self.mfma} {vr(S(b), 16)}, {ar(KB(0, ks), 4)}, {ar(Q(b, ks), 4)}, {c}")
+        e(f"s_mov_b32 {S_LIMIT}, -1.0")
+        e(f"s_mov_b32 {S_FLOOR}, 0xff800000")
+        e(f"s_mov_b32 {S_IT}, 0")
+        e("s_cmp_eq_u32 %[n], 0")
+        e("s_cbranch_scc1 LEND_%=")
+        # ---- loop over tiles ----
+        e("LLOOP_%=:")
+        e(f"s_and_b32 {S_TMP}, {S_IT}, 3")
+        e(f"s_mul_i32 {S_BUFA}, {S_TMP}, {TILE_BYTES}")
+        e(f"s_add_u32 {S_TMP}, {S_IT}, 1")
+        e(f"s_and_b32 {S_TMP}, {S_TMP}, 3")
+        e(f"s_mul_i32 {S_BUFB}, {S_TMP}, {TILE_BYTES}")
+        e(f"s_add_u32 {S_TMP}, {S_IT}, 2")
+        e(f"s_and_b32 {S_TMP}, {S_TMP}, 3")
+        e(f"s_mul_i32 {S_BUFC}, {S_TMP}, {TILE_BYTES}")
+        e(f"v_add_u32 {vr(KADDR)}, {S_BUFB}, {vr(KLANE)}")
+        e(f"v_add_u32 {vr(VADDRA)}, {S_BUFA}, {vr(VLANE)}")
+        e(f"v_add_u32 {vr(VADDRB)}, {S_BUFB}, {vr(VLANE)}")
+        e(f"v_add_u32 {vr(STADDR)}, {S_BUFC}, {vr(STLANE)}")
+        w, ld, adv = self.staging()
+        kr0, vr0 = self.k_reads(0), self.v_reads(0)
+        kr1, vr1 = self.k_reads(1), self.v_reads(1)
+        # step 2t (parity 0)
+        self.phase(0, 0)
+        self.phase(0, 1, pre=["s_waitcnt lgkmcnt(0)"], slots={3: kr0[:2], 4: kr0[2:]})
+        self.phase(0, 2, slots={1: vr0[0:2], 2: vr0[2:4], 3: vr0[4:6], 4: vr0[6:8]})
+        # step 2t+1 (parity 1): the forced first-step rescale is over
+        e(f"s_mov_b32 {S_LIMIT}, {SUM_LIMIT}")
+        e(f"s_mov_b32 {S_FLOOR}, 0")
+        self.phase(1, 0, pre=[w[0]], slots={0: w[1:], 1: ld, 2: adv})
+        self.phase(1, 1, pre=["s_waitcnt lgkmcnt(0)"], slots={3: kr1[:2], 4: kr1[2:]})
+        self.phase(1, 2, slots={1: vr1[0:2], 2: vr1[2:4], 3: vr1[4:6], 4: vr1[6:8]})
+        e("s_waitcnt lgkmcnt(0)")
+        e("s_barrier")
+        e(f"s_add_u32 {S_IT}, {S_IT}, 1")
+        e(f"s_cmp_lt_u32 {S_IT}, %[n]")
+        e("s_cbranch_scc1 LLOOP_%=")
+        e("LEND_%=:")
+        e("s_waitcnt vmcnt(0) lgkmcnt(0)")
+        e("s_branch LDONE_%=")
+        self.out.extend(self.rare)
+        e("LDONE_%=:")
+        e("s_nop 4")
+        return self.out
+
+
+def render() -> str:
+    lines = [
+        "// Generated by gen_dense_loop.py -- do not edit; edit the generator and rebuild.",
+        "// The main loop of dense_pipe_kernel (attn_dense.hip); see the generator for the design.",
+        "#pragma once",
+        "",
+    ]
+    for dtype in ("bf16", "f16"):
+        body = Gen(dtype).build()
+        lines.append(f"#define WDRZ_DENSE_LOOP_{dtype.upper()} \\")
+        for s in body:
+            lines.append(f'  "{s}\\n" \\')
+        lines.append('  ""')
+        lines.append("")
+    return "\n".join(lines) + "\n"
+
+
+if __name__ == "__main__":
+    out = Path(sys.argv[1]) if len(sys.argv) > 1 else Path(__file__).with_name("dense_loop.inc")
+    text = render()
+    if not out.exists() or out.read_text() != text:
+        out.write_text(text)
