@@ -982,6 +982,28 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
   return r;
 }
 
+// Registers the generated loop uses beyond its operands (gen_dense_loop.py has the map).
+#define WDRZ_PIPE_CLOBBERS \
+  "v0", "v1", "v2", "v3", "v4", "v5", "v6", "v7", "v8", "v9", "v10", "v11", "v12", "v13", "v14", "v15", \
+  "v16", "v17", "v18", "v19", "v20", "v21", "v22", "v23", "v24", "v25", "v26", "v27", "v28", "v29", "v30", \
+  "v31", "v32", "v33", "v34", "v35", "v36", "v37", "v38", "v39", "v40", "v41", "v42", "v43", "v44", "v45", \
+  "v46", "v47", "v48", "v49", "v50", "v51", "v52", "v53", "v54", "v55", "v56", "v57", "v58", "v59", "v60", \
+  "v61", "v62", "v63", "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71", "v72", "v73", "v74", "v75", \
+  "v76", "v77", "v78", "v79", "v80", "v81", "v82", "v83", "v84", "v85", "v86", "v87", "v88", "v89", "v90", \
+  "v91", "v92", "v93", "v94", "v95", "v96", "v97", "v98", "v99", "v100", "v101", "v102", "v103", "v104", \
+  "v105", "v106", "v107", "v108", "v109", "v110", "v111", "v112", "v113", "v114", "v115", "v116", "v117", \
+  "v118", "v119", "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127", "v128", "v129", "v130", \
+  "v131", "v132", "v133", "v134", "v135", "v152", "v153", "v154", "v155", "v159", "v168", "v169", "v170", \
+  "v171", "v172", "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180", "v181", "v182", "v183", \
+  "v184", "v185", "v186", "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195", "v196", \
+  "v197", "v198", "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "a144", "a145", \
+  "a146", "a147", "a148", "a149", "a150", "a151", "a152", "a153", "a154", "a155", "a156", "a157", "a158", \
+  "a159", "a160", "a161", "a162", "a163", "a164", "a165", "a166", "a167", "a168", "a169", "a170", "a171", \
+  "a172", "a173", "a174", "a175", "a176", "a177", "a178", "a179", "a180", "a181", "a182", "a183", "a184", \
+  "a185", "a186", "a187", "a188", "a189", "a190", "a191", "a192", "a193", "a194", "a195", "a196", "a197", \
+  "a198", "a199", "a200", "a201", "a202", "a203", "a204", "a205", "a206", "a207", "s70", "s71", "s72", "s73", \
+  "s74", "s75", "s76", "s77", "s78", "s79", "vcc", "scc", "memory"
+
 template <typename T>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void dense_pipe_kernel(DenseArgs a) {
   typedef typename Mfma<T>::op_t op_t;
@@ -1065,18 +1087,22 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
   tile_load(2, stage);
   __syncthreads();
 
-  // ---- the hand-scheduled loop over pairs of 32-key steps (full tiles only) ----
+  // ---- the hand-scheduled loop over pairs of 32-key steps (full tiles), then the remaining
+  // steps (the last one masked at Lk) and the last block's P V, all in the generated code ----
   const int n_sub = (a.Lk + kBS - 1) / kBS;
   const int n_iter = (a.Lk / kBS) / 2;
-  const int s_end = 2 * n_iter;
+  const int n_rest = n_sub - 2 * n_iter;       // 0, 1 or 2
+  const int rem = a.Lk - kBS * (n_sub - 1);    // valid keys of the last step
   // LDS byte offsets of this lane's operand reads (the permuted K rows; V^T through the
   // transposing read), and of its tile stores
   const int pm = l32;
   const int pi_row = 16 * ((pm >> 3) >> 1) + 8 * ((pm >> 2) & 1) + 4 * ((pm >> 3) & 1) + (pm & 3);
   const int g16 = lane >> 4, j16 = lane & 15;
-  const uint32_t klane = (uint32_t)(pi_row * kPitchK + hl * 8) * 2;
-  const uint32_t vlane = (uint32_t)((8 * (g16 >> 1) + (j16 >> 2)) * kPitchK + 16 * (g16 & 1) + 4 * (j16 & 3)) * 2;
-  const uint32_t stlane = (uint32_t)st_off * 2;
+  u32x4 lanes;
+  lanes[0] = (uint32_t)(pi_row * kPitchK + hl * 8) * 2;  // K reads
+  lanes[1] = (uint32_t)((8 * (g16 >> 1) + (j16 >> 2)) * kPitchK + 16 * (g16 & 1) + 4 * (j16 & 3)) * 2;  // V^T reads
+  lanes[2] = (uint32_t)st_off * 2;  // tile stores
+  lanes[3] = 8 * hl;                // key offset of this lane half (masking)
   // global byte offsets of this thread's rows in tile 3 (the first the loop requests)
   u32x4 voff;
   voff[0] = (3 * kBN + crow) * rs_k + cd0 * 2;
@@ -1090,185 +1116,24 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
 #pragma unroll
     for (int e = 0; e < 4; ++e) stg[4 * i + e] = stage[i][e];
 
-  f32x16 o00, o01, o10, o11, o20, o21;
-  op_t kop[4], vop[2][2], vpr[2][2];  // K(s_end), V(s_end), V(s_end - 1) operands after the loop
-  typedef float f32x6 __attribute__((ext_vector_type(6)));
-  typedef uint32_t u32x3 __attribute__((ext_vector_type(3)));
-  f32x6 ml;  // m_run[3], l_run[3]
-  const u32x3 lanes = {klane, vlane, stlane};
-  f32x32 s01;
-  f32x16 s2;
-  f32x32 ci01;
-  f32x16 ci2;
-  u32x16 p01;
-  u32x8 p2;
+  f32x16 acc_o[3][2];
+  typedef float f32x3 __attribute__((ext_vector_type(3)));
+  f32x3 lr;  // this lane's half of each block's row sum
+#define WDRZ_PIPE_OPERANDS                                                                                    \
+  : "={a[0:15]}"(acc_o[0][0]), "={a[16:31]}"(acc_o[0][1]), "={a[32:47]}"(acc_o[1][0]), "={a[48:63]}"(acc_o[1][1]), \
+    "={a[64:79]}"(acc_o[2][0]), "={a[80:95]}"(acc_o[2][1]), "={v[156:158]}"(lr), "+{v[136:151]}"(stg),              \
+    "+{v[164:167]}"(voff)                                                                                         \
+  : "{a[96:111]}"(q0), "{a[112:127]}"(q1), "{a[128:143]}"(q2), "{v[160:163]}"(lanes), "{s[80:83]}"(srd_k),        \
+    "{s[84:87]}"(srd_v), [n] "s"(n_iter), [r] "s"(n_rest), [rem] "s"(rem), [tsk] "s"(tsk), [tsv] "s"(tsv)           \
+  : WDRZ_PIPE_CLOBBERS
   __builtin_amdgcn_sched_barrier(0);
-  if constexpr (__is_same(T, Bf16)) {
-    asm volatile(WDRZ_DENSE_LOOP_BF16
-                 : "={a[0:15]}"(o00), "={a[16:31]}"(o01), "={a[32:47]}"(o10), "={a[48:63]}"(o11), "={a[64:79]}"(o20),
-                   "={a[80:95]}"(o21), "={a[144:147]}"(kop[0]), "={a[148:151]}"(kop[1]), "={a[152:155]}"(kop[2]),
-                   "={a[156:159]}"(kop[3]), "={a[176:179]}"(vop[0][0]), "={a[180:183]}"(vop[0][1]),
-                   "={a[184:187]}"(vop[1][0]), "={a[188:191]}"(vop[1][1]), "={a[192:195]}"(vpr[0][0]),
-                   "={a[196:199]}"(vpr[0][1]), "={a[200:203]}"(vpr[1][0]), "={a[204:207]}"(vpr[1][1]),
-                   "={v[0:31]}"(s01), "={v[32:47]}"(s2), "={v[48:79]}"(ci01), "={v[80:95]}"(ci2), "={v[96:111]}"(p01),
-                   "={v[112:119]}"(p2), "+{v[136:151]}"(stg), "={v[152:157]}"(ml), "+{v[162:165]}"(voff)
-                 : "{a[96:111]}"(q0), "{a[112:127]}"(q1), "{a[128:143]}"(q2), "{v[158:160]}"(lanes),
-                   "{s[80:83]}"(srd_k), "{s[84:87]}"(srd_v), [n] "s"(n_iter), [tsk] "s"(tsk), [tsv] "s"(tsv)
-                 : "a160", "a161", "a162", "a163", "a164", "a165", "a166", "a167", "a168", "a169", "a170", "a171", "a172",
-                   "a173", "a174", "a175", "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127", "v128",
-                   "v129", "v130", "v131",
-                   "v132", "v133", "v134", "v135", "v161", "v166", "v167", "v168", "v169", "v170", "v171", "v172",
-                   "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180", "v181", "v184", "v185", "v186",
-                   "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195", "v196", "v197", "v198",
-                   "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "s70",
-                   "s71", "s72", "s73", "s74", "s75", "s76", "s77", "s78", "s79", "vcc", "scc", "memory");
-  } else {
-    asm volatile(WDRZ_DENSE_LOOP_F16
-                 : "={a[0:15]}"(o00), "={a[16:31]}"(o01), "={a[32:47]}"(o10), "={a[48:63]}"(o11), "={a[64:79]}"(o20),
-                   "={a[80:95]}"(o21), "={a[144:147]}"(kop[0]), "={a[148:151]}"(kop[1]), "={a[152:155]}"(kop[2]),
-                   "={a[156:159]}"(kop[3]), "={a[176:179]}"(vop[0][0]), "={a[180:183]}"(vop[0][1]),
-                   "={a[184:187]}"(vop[1][0]), "={a[188:191]}"(vop[1][1]), "={a[192:195]}"(vpr[0][0]),
-                   "={a[196:199]}"(vpr[0][1]), "={a[200:203]}"(vpr[1][0]), "={a[204:207]}"(vpr[1][1]),
-                   "={v[0:31]}"(s01), "={v[32:47]}"(s2), "={v[48:79]}"(ci01), "={v[80:95]}"(ci2), "={v[96:111]}"(p01),
-                   "={v[112:119]}"(p2), "+{v[136:151]}"(stg), "={v[152:157]}"(ml), "+{v[162:165]}"(voff)
-                 : "{a[96:111]}"(q0), "{a[112:127]}"(q1), "{a[128:143]}"(q2), "{v[158:160]}"(lanes),
-                   "{s[80:83]}"(srd_k), "{s[84:87]}"(srd_v), [n] "s"(n_iter), [tsk] "s"(tsk), [tsv] "s"(tsv)
-                 : "a160", "a161", "a162", "a163", "a164", "a165", "a166", "a167", "a168", "a169", "a170", "a171", "a172",
-                   "a173", "a174", "a175", "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127", "v128",
-                   "v129", "v130", "v131",
-                   "v132", "v133", "v134", "v135", "v161", "v166", "v167", "v168", "v169", "v170", "v171", "v172",
-                   "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180", "v181", "v184", "v185", "v186",
-                   "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195", "v196", "v197", "v198",
-                   "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "s70",
-                   "s71", "s72", "s73", "s74", "s75", "s76", "s77", "s78", "s79", "vcc", "scc", "memory");
-  }
+  if constexpr (__is_same(T, Bf16))
+    asm volatile(WDRZ_DENSE_LOOP_BF16 WDRZ_PIPE_OPERANDS);
+  else
+    asm volatile(WDRZ_DENSE_LOOP_F16 WDRZ_PIPE_OPERANDS);
   __builtin_amdgcn_sched_barrier(0);
-
-  // ---- the remaining steps (the partial last one, and a full one when the full steps are odd).
-  // State after the loop: S(s_end) of blocks 0, 1; P(s_end - 1) of block 2, whose P V and whose
-  // scores S(s_end) the loop leaves to the next step; K(s_end) in K buffer 0, V(s_end) in V buffer
-  // 0 and V(s_end - 1) in V buffer 1.
-  f32x16 acc_o[3][2], sacc[3], cinit[3];
-  op_t qop[3][4], pcur[3][2];
-  float m_run[3] = {ml[0], ml[1], ml[2]}, l_run[3] = {ml[3], ml[4], ml[5]};
-  acc_o[0][0] = o00;
-  acc_o[0][1] = o01;
-  acc_o[1][0] = o10;
-  acc_o[1][1] = o11;
-  acc_o[2][0] = o20;
-  acc_o[2][1] = o21;
-#pragma unroll
-  for (int x = 0; x < 16; ++x) {
-    sacc[0][x] = s01[x];
-    sacc[1][x] = s01[16 + x];
-    sacc[2][x] = s2[x];
-    cinit[0][x] = ci01[x];
-    cinit[1][x] = ci01[16 + x];
-    cinit[2][x] = ci2[x];
-  }
-  auto op4 = [](uint32_t w0, uint32_t w1, uint32_t w2, uint32_t w3) { return __builtin_bit_cast(op_t, u32x4{w0, w1, w2, w3}); };
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    qop[0][ks] = op4(q0[4 * ks], q0[4 * ks + 1], q0[4 * ks + 2], q0[4 * ks + 3]);
-    qop[1][ks] = op4(q1[4 * ks], q1[4 * ks + 1], q1[4 * ks + 2], q1[4 * ks + 3]);
-    qop[2][ks] = op4(q2[4 * ks], q2[4 * ks + 1], q2[4 * ks + 2], q2[4 * ks + 3]);
-  }
-#pragma unroll
-  for (int ch = 0; ch < 2; ++ch) {
-    pcur[0][ch] = op4(p01[4 * ch], p01[4 * ch + 1], p01[4 * ch + 2], p01[4 * ch + 3]);
-    pcur[1][ch] = op4(p01[8 + 4 * ch], p01[9 + 4 * ch], p01[10 + 4 * ch], p01[11 + 4 * ch]);
-    pcur[2][ch] = op4(p2[4 * ch], p2[4 * ch + 1], p2[4 * ch + 2], p2[4 * ch + 3]);
-  }
-  // P(s_end - 1) V(s_end - 1) of block 2
-#pragma unroll
-  for (int ch = 0; ch < 2; ++ch)
-#pragma unroll
-    for (int db = 0; db < 2; ++db) {
-      acc_o[2][db] = Mfma<T>::run(vpr[ch][db], pcur[2][ch], acc_o[2][db]);
-    }
-  auto mfma_s = [&](int qb) __attribute__((always_inline)) {
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) sacc[qb] = Mfma<T>::run(kop[ks], qop[qb][ks], ks == 0 ? cinit[qb] : sacc[qb]);
-  };
-  if (s_end < n_sub) mfma_s(2);
-  auto read_k = [&](int s) __attribute__((always_inline)) {
-    const e_t* kb = &smem[((s >> 1) & 3) * kPTile + (s & 1) * 32 * kPitchK] + klane / 2;
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) kop[ks] = __builtin_bit_cast(op_t, *reinterpret_cast<const u32x4*>(kb + ks * 16));
-  };
-  auto read_v = [&](int s) __attribute__((always_inline)) {
-    const e_t* vb = &smem[(4 + ((s >> 1) & 3)) * kPTile + (s & 1) * 32 * kPitchK] + vlane / 2;
-#pragma unroll
-    for (int ch = 0; ch < 2; ++ch)
-#pragma unroll
-      for (int db = 0; db < 2; ++db) {
-        const e_t* p = vb + ch * 16 * kPitchK + db * 32;
-        const u32x2 lo = lds_read_tr16(p), hi = lds_read_tr16(p + 4 * kPitchK);
-        vop[ch][db] = __builtin_bit_cast(op_t, u32x4{lo[0], lo[1], hi[0], hi[1]});
-      }
-  };
-  // online softmax of step s for block qb, as in dense_fwd_kernel (keys past Lk masked; the
-  // first step takes the true max)
-  auto exp_sum = [&](int qb) __attribute__((always_inline)) {
-    float t[4];
-#pragma unroll
-    for (int ch = 0; ch < 2; ++ch) {
-      u32x4 w;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float p0 = fast_exp2(sacc[qb][ch * 8 + 2 * e]);
-        const float p1 = fast_exp2(sacc[qb][ch * 8 + 2 * e + 1]);
-        w[e] = Mfma<T>::pack(p0, p1);
-        t[e] = ch == 0 ? p0 + p1 : t[e] + p0 + p1;
-      }
-      pcur[qb][ch] = __builtin_bit_cast(op_t, w);
-    }
-    return (t[0] + t[1]) + (t[2] + t[3]);
-  };
-  for (int s = s_end; s < n_sub; ++s) {
-    if (s > s_end) read_v(s);
-    const bool more = s + 1 < n_sub;
-    if (more) read_k(s + 1);
-    const int k0 = s * kBS;
-#pragma unroll
-    for (int qb = 0; qb < 3; ++qb) {
-      if (k0 + kBS > a.Lk) {
-#pragma unroll
-        for (int x = 0; x < 16; ++x)
-          if (k0 + 16 * (x >> 3) + 8 * hl + (x & 7) >= a.Lk) sacc[qb][x] = -INFINITY;
-      }
-      float st = s == 0 ? INFINITY : exp_sum(qb);
-      if (__any(!(st <= kSumLimit))) {
-        const f32x16& v = sacc[qb];
-        float mx = v[0];
-#pragma unroll
-        for (int x = 1; x < 16; ++x) mx = fmaxf(mx, v[x]);
-        mx = half_swap_max(mx);
-        const float delta = s == 0 ? mx : fmaxf(mx, 0.f);
-        m_run[qb] += delta;
-        if (s != 0) {  // (the first step has nothing to rescale; exp2(-delta) may be inf there)
-          const float alpha = fast_exp2(-delta);
-          l_run[qb] *= alpha;
-#pragma unroll
-          for (int db = 0; db < 2; ++db)
-#pragma unroll
-            for (int x = 0; x < 16; ++x) acc_o[qb][db][x] *= alpha;
-        }
-#pragma unroll
-        for (int x = 0; x < 16; ++x) {
-          sacc[qb][x] -= delta;
-          cinit[qb][x] = -m_run[qb];
-        }
-        st = exp_sum(qb);
-      }
-      l_run[qb] += st;
-#pragma unroll
-      for (int ch = 0; ch < 2; ++ch)
-#pragma unroll
-        for (int db = 0; db < 2; ++db) acc_o[qb][db] = Mfma<T>::run(vop[ch][db], pcur[qb][ch], acc_o[qb][db]);
-      if (more) mfma_s(qb);
-    }
-  }
+#undef WDRZ_PIPE_OPERANDS
+  const float l_run[3] = {lr[0], lr[1], lr[2]};
 
   // ---- normalise, stage O^T through LDS as [query][dim] rows, store whole rows ----
   __syncthreads();  // every wavefront is done with the tiles

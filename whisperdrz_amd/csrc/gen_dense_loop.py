@@ -31,13 +31,15 @@ wavefront as three 32-query blocks b = 0, 1, 2; 32 keys per step, 64-key LDS til
 Register map (the kernel passes these through "{v[..]}" / "{a[..]}" constraints):
   v0-47 S[b] (16 each)   v48-95 cinit[b]   v96-119 P[b] (8 each: two 16-key chunks)
   v120-135 exp temps     v136-151 tile staging (K rows r, r+32, V rows r, r+32)
-  v152-154 m_run[b]      v155-157 l_run[b] (this lane's half of the row sum)
-  v158 K read lane base  v159 V read lane base  v160 tile store lane base
-  v162-165 global row offsets (K r, K r+32, V r, V r+32)   v166-181 addresses, temporaries
-  v184-207 row-sum temporaries (8 per block)
+  v152-154 m_run[b]      v155 tail V address   v156-158 l_run[b] (this lane's half of the row sum)
+  v159 -inf
+  v160-163 lane bases: K read, V read, tile store, 8 * (lane >> 5)
+  v164-167 global row offsets (K r, K r+32, V r, V r+32)   v168-171 per-tile addresses
+  v172-183 rare-path temporaries   v184-207 row-sum temporaries (8 per block)
   a0-95 O[b][db] (16 each)   a96-143 Q[b][ks] (4 each)   a144-175 K buffers (2 x 16)
   a176-207 V buffers (2 x 16: [ch][db] operands of 4)
-  s70-s79 loop state (clobbered: iteration, tile offsets, sum limit, rescale floor); the kernel passes the buffer resources in s[80:83], s[84:87].
+  s70-s79 loop state (clobbered: iteration, tile offsets, sum limit, rescale floor); the kernel
+  passes the buffer resources in s[80:83], s[84:87].
 """
 import sys
 from pathlib import Path
@@ -50,11 +52,13 @@ T0 = 120
 STAGE = 136
 def U(b): return 184 + 8 * b  # row-sum temporaries of block b (184..207)
 def MRUN(b): return 152 + b
-def LRUN(b): return 155 + b
-KLANE, VLANE, STLANE = 158, 159, 160
-VOFF = 162  # 162..165 (a 4-register tuple: even-aligned)
-KADDR, VADDRA, VADDRB, STADDR = 166, 167, 168, 169
-RT = 170  # rare-path temporaries 170..181
+def LRUN(b): return 156 + b  # a 3-register tuple (even-aligned), an output of the loop
+KLANE, VLANE, STLANE, HL8 = 160, 161, 162, 163  # HL8: 8 * (lane >> 5), the masking's key offset
+VOFF = 164  # 164..167 (a 4-register tuple: even-aligned)
+KADDR, VADDRA, VADDRB, STADDR = 168, 169, 170, 171
+RT = 172  # rare-path temporaries 172..183
+VADDRT = 155  # the tail's V read address
+NEGINF = 159  # -inf (the masked score)
 def O(b, db): return 32 * b + 16 * db
 def Q(b, ks): return 96 + 16 * b + 4 * ks
 def KB(p, ks): return 144 + 16 * p + 4 * ks
@@ -158,8 +162,21 @@ class Gen:
         r.append("s_nop 4")
         r.append(f"s_branch {back}")
 
-    def phase(self, p, ph, pre=(), slots=None):
-        """One phase of a step of parity p. slots: {mfma index: [extra instructions after it]}."""
+    def mask_valu(self, b):
+        """Keys past Lk (last step only): score -> -inf. Key of accumulator i of lane half hl:
+        k0 + 8 hl + 16 (i >> 3) + (i & 7); valid iff 8 hl < rem - 16 (i >> 3) - (i & 7), rem = Lk - k0."""
+        v = []
+        for i in range(16):
+            c = 16 * (i >> 3) + (i & 7)
+            v.append(f"s_sub_i32 {S_TMP}, %[rem], {c}")
+            v.append(f"v_cmp_gt_i32 vcc, {S_TMP}, {vr(HL8)}")
+            v.append(f"v_cndmask_b32 {vr(S(b) + i)}, {vr(NEGINF)}, {vr(S(b) + i)}, vcc")
+        return v
+
+    def phase(self, p, ph, tag, pre=(), slots=None, do_s=True, mask=False):
+        """One phase of a step of parity p: the softmax of block ph beside the MFMAs of the block
+        before it (P V, and unless do_s is false the scores of its next step). slots: {MFMA
+        index: [instructions after it]}. mask: the step is the last one and may hold keys past Lk."""
         slots = slots or {}
         if ph == 0:
             mb, kbuf, vbuf = 2, p, 1 - p
@@ -167,30 +184,37 @@ class Gen:
             mb, kbuf, vbuf = ph - 1, 1 - p, p
         mf = []
         for ks in range(4):
-            mf.append(self.mfma_s(mb, ks, kbuf))
+            if do_s:
+                mf.append(self.mfma_s(mb, ks, kbuf))
             ch, db = divmod(ks, 2)
             mf.append(self.mfma_pv(mb, ch, db, vbuf))
-        valu = self.softmax_valu(ph)
-        for s in pre:
-            self.emit(s)
-        # spread the VALU list over the 8 MFMA slots
-        n = len(valu)
+        valu = (self.mask_valu(ph) if mask else []) + self.softmax_valu(ph)
+        for x in pre:
+            self.emit(x)
+        # spread the VALU list over the MFMA slots
+        n, m = len(valu), len(mf)
         k = 0
-        for i in range(8):
+        for i in range(m):
             self.emit(mf[i])
-            for s in slots.get(i, []):
-                self.emit(s)
-            hi = (n * (i + 1)) // 8
+            for x in slots.get(i, []):
+                self.emit(x)
+            hi = (n * (i + 1)) // m
             while k < hi:
                 self.emit(valu[k])
                 k += 1
-        # check: sum > limit in any lane, or the forced first step -> rescale
-        label = f"R{ph}P{p}_%="
-        back = f"B{ph}P{p}_%="
+        # rescale when some lane's sum exceeded the limit (vcc, set by the compare above)
+        label = f"R{tag}_%="
+        back = f"B{tag}_%="
         self.emit(f"s_cbranch_vccnz {label}")
         self.emit(f"{back}:")
         self.emit(f"v_add_f32 {vr(LRUN(ph))}, {vr(LRUN(ph))}, {vr(U(ph))}")
         self.rare_block(ph, label, back)
+
+    def final_pv(self, vbuf):
+        """P V of block 2 of the last step (the loop leaves it to the next step's phase 0)."""
+        for ks in range(4):
+            ch, db = divmod(ks, 2)
+            self.emit(self.mfma_pv(2, ch, db, vbuf))
 
     def k_reads(self, p):
         """K(s+2) -> K buffer p: tile t+1, half p (base KADDR)."""
@@ -258,6 +282,7 @@ class Gen:
             for ks in range(4):
                 c = "0" if ks == 0 else vr(S(b), 16)
                 e(f"{self.mfma} {vr(S(b), 16)}, {ar(KB(0, ks), 4)}, {ar(Q(b, ks), 4)}, {c}")
+        e(f"v_mov_b32 {vr(NEGINF)}, 0xff800000")
         e(f"s_mov_b32 {S_LIMIT}, -1.0")
         e(f"s_mov_b32 {S_FLOOR}, 0xff800000")
         e(f"s_mov_b32 {S_IT}, 0")
@@ -281,15 +306,15 @@ class Gen:
         kr0, vr0 = self.k_reads(0), self.v_reads(0)
         kr1, vr1 = self.k_reads(1), self.v_reads(1)
         # step 2t (parity 0)
-        self.phase(0, 0)
-        self.phase(0, 1, pre=["s_waitcnt lgkmcnt(0)"], slots={3: kr0[:2], 4: kr0[2:]})
-        self.phase(0, 2, slots={1: vr0[0:2], 2: vr0[2:4], 3: vr0[4:6], 4: vr0[6:8]})
+        self.phase(0, 0, "0P0")
+        self.phase(0, 1, "1P0", pre=["s_waitcnt lgkmcnt(0)"], slots={3: kr0[:2], 4: kr0[2:]})
+        self.phase(0, 2, "2P0", slots={1: vr0[0:2], 2: vr0[2:4], 3: vr0[4:6], 4: vr0[6:8]})
         # step 2t+1 (parity 1): the forced first-step rescale is over
         e(f"s_mov_b32 {S_LIMIT}, {SUM_LIMIT}")
         e(f"s_mov_b32 {S_FLOOR}, 0")
-        self.phase(1, 0, pre=[w[0]], slots={0: w[1:], 1: ld, 2: adv})
-        self.phase(1, 1, pre=["s_waitcnt lgkmcnt(0)"], slots={3: kr1[:2], 4: kr1[2:]})
-        self.phase(1, 2, slots={1: vr1[0:2], 2: vr1[2:4], 3: vr1[4:6], 4: vr1[6:8]})
+        self.phase(1, 0, "0P1", pre=[w[0]], slots={0: w[1:], 1: ld, 2: adv})
+        self.phase(1, 1, "1P1", pre=["s_waitcnt lgkmcnt(0)"], slots={3: kr1[:2], 4: kr1[2:]})
+        self.phase(1, 2, "2P1", slots={1: vr1[0:2], 2: vr1[2:4], 3: vr1[4:6], 4: vr1[6:8]})
         e("s_waitcnt lgkmcnt(0)")
         e("s_barrier")
         e(f"s_add_u32 {S_IT}, {S_IT}, 1")
@@ -297,6 +322,43 @@ class Gen:
         e("s_cbranch_scc1 LLOOP_%=")
         e("LEND_%=:")
         e("s_waitcnt vmcnt(0) lgkmcnt(0)")
+        # ---- tail: the r = n_sub - 2 n remaining steps (0, 1 or 2; the last one masked) ----
+        # state: S(s_end) of blocks 0 and 1, P(s_end - 1) of block 2, K(s_end) and K(s_end + 1) in
+        # K buffers 0 and 1, V(s_end - 1) and V(s_end) in V buffers 1 and 0
+        e("s_cmp_eq_u32 %[r], 0")
+        e("s_cbranch_scc1 LT0_%=")
+        e("s_cmp_eq_u32 %[r], 1")
+        e("s_cbranch_scc1 LT1_%=")
+        # r = 2: step s_end (full), then step s_end + 1 (masked); V(s_end + 1) -> V buffer 1
+        e(f"s_and_b32 {S_TMP}, {S_IT}, 3")
+        e(f"s_mul_i32 {S_TMP}, {S_TMP}, {TILE_BYTES}")
+        e(f"v_add_u32 {vr(VADDRT)}, {S_TMP}, {vr(VLANE)}")
+        tvr = [x.replace(vr(VADDRA), vr(VADDRT)) for x in self.v_reads(0)]
+        self.phase(0, 0, "0T2")
+        self.phase(0, 1, "1T2", pre=["s_waitcnt lgkmcnt(0)"])
+        self.phase(0, 2, "2T2", slots={1: tvr[0:2], 2: tvr[2:4], 3: tvr[4:6], 4: tvr[6:8]})
+        e(f"s_mov_b32 {S_LIMIT}, {SUM_LIMIT}")
+        e(f"s_mov_b32 {S_FLOOR}, 0")
+        e("s_waitcnt lgkmcnt(0)")
+        self.phase(1, 0, "0T2b", mask=True)
+        self.phase(1, 1, "1T2b", do_s=False, mask=True)
+        self.phase(1, 2, "2T2b", do_s=False, mask=True)
+        self.final_pv(1)
+        e("s_branch LTEND_%=")
+        # r = 1: step s_end, masked
+        e("LT1_%=:")
+        self.phase(0, 0, "0T1", mask=True)
+        self.phase(0, 1, "1T1", pre=["s_waitcnt lgkmcnt(0)"], do_s=False, mask=True)
+        self.phase(0, 2, "2T1", do_s=False, mask=True)
+        self.final_pv(0)
+        e("s_branch LTEND_%=")
+        # r = 0: only block 2's last P V
+        e("LT0_%=:")
+        self.final_pv(1)
+        e("LTEND_%=:")
+        e("s_nop 7")
+        e("s_nop 7")
+        e("s_nop 7")
         e("s_branch LDONE_%=")
         self.out.extend(self.rare)
         e("LDONE_%=:")
