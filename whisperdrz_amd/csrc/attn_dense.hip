@@ -956,8 +956,9 @@ __global__ __launch_bounds__(kFThreads, 1) void dense_fwd_kernel(DenseArgs a) {
 // (B=16: 320 heads x 4 blocks = 5 x 256 workgroups).
 //
 // The C++ around the loop stages Q (pre-scaled by scale*log2(e)) into its operand registers,
-// the first two K/V tiles into LDS and the third into the staging registers, and after the loop
-// finishes the last (partial) steps, normalises and stores O through LDS as whole rows.
+// and the first two K/V tiles into LDS (the loop code requests the next ones itself); the loop
+// code also runs the last (partial) steps, and the C++ normalises and stores O through LDS as
+// whole rows.
 // ============================================================================================
 constexpr int kPWaves = 4;
 constexpr int kPThreads = kPWaves * 64;
@@ -993,16 +994,19 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
   "v91", "v92", "v93", "v94", "v95", "v96", "v97", "v98", "v99", "v100", "v101", "v102", "v103", "v104", \
   "v105", "v106", "v107", "v108", "v109", "v110", "v111", "v112", "v113", "v114", "v115", "v116", "v117", \
   "v118", "v119", "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127", "v128", "v129", "v130", \
-  "v131", "v132", "v133", "v134", "v135", "v152", "v153", "v154", "v155", "v159", "v168", "v169", "v170", \
-  "v171", "v172", "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180", "v181", "v182", "v183", \
-  "v184", "v185", "v186", "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195", "v196", \
-  "v197", "v198", "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "a144", "a145", \
-  "a146", "a147", "a148", "a149", "a150", "a151", "a152", "a153", "a154", "a155", "a156", "a157", "a158", \
-  "a159", "a160", "a161", "a162", "a163", "a164", "a165", "a166", "a167", "a168", "a169", "a170", "a171", \
-  "a172", "a173", "a174", "a175", "a176", "a177", "a178", "a179", "a180", "a181", "a182", "a183", "a184", \
-  "a185", "a186", "a187", "a188", "a189", "a190", "a191", "a192", "a193", "a194", "a195", "a196", "a197", \
-  "a198", "a199", "a200", "a201", "a202", "a203", "a204", "a205", "a206", "a207", "s70", "s71", "s72", "s73", \
-  "s74", "s75", "s76", "s77", "s78", "s79", "vcc", "scc", "memory"
+  "v131", "v132", "v133", "v134", "v135", "v136", "v137", "v138", "v139", "v140", "v141", "v142", "v143", \
+  "v144", "v145", "v146", "v147", "v148", "v149", "v150", "v151", "v152", "v153", "v154", "v155", "v159", \
+  "v168", "v169", "v170", "v171", "v172", "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180", \
+  "v181", "v182", "v183", "v184", "v185", "v186", "v187", "v188", "v189", "v190", "v191", "v192", "v193", \
+  "v194", "v195", "v196", "v197", "v198", "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", \
+  "v207", "v208", "v209", "v210", "v211", "v212", "v213", "v214", "v215", "v216", "v217", "v218", "v219", \
+  "v220", "v221", "v222", "v223", "a144", "a145", "a146", "a147", "a148", "a149", "a150", "a151", "a152", \
+  "a153", "a154", "a155", "a156", "a157", "a158", "a159", "a160", "a161", "a162", "a163", "a164", "a165", \
+  "a166", "a167", "a168", "a169", "a170", "a171", "a172", "a173", "a174", "a175", "a176", "a177", "a178", \
+  "a179", "a180", "a181", "a182", "a183", "a184", "a185", "a186", "a187", "a188", "a189", "a190", "a191", \
+  "a192", "a193", "a194", "a195", "a196", "a197", "a198", "a199", "a200", "a201", "a202", "a203", "a204", \
+  "a205", "a206", "a207", "s70", "s71", "s72", "s73", "s74", "s75", "s76", "s77", "s78", "s79", "vcc", "scc", \
+  "memory"
 
 template <typename T>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void dense_pipe_kernel(DenseArgs a) {
@@ -1057,7 +1061,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
   };
 
   // ---- Q: whole rows into LDS, then each wavefront's operand registers, pre-scaled by c ----
-  u32x4 t0[4], t1[4], stage[4];
+  u32x4 t0[4], t1[4];
   {
     u32x4 qc[kPBM / 32];
 #pragma unroll
@@ -1084,7 +1088,6 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
   __syncthreads();
   tile_store(0, t0);
   tile_store(1, t1);
-  tile_load(2, stage);
   __syncthreads();
 
   // ---- the hand-scheduled loop over pairs of 32-key steps (full tiles), then the remaining
@@ -1103,25 +1106,20 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
   lanes[1] = (uint32_t)((8 * (g16 >> 1) + (j16 >> 2)) * kPitchK + 16 * (g16 & 1) + 4 * (j16 & 3)) * 2;  // V^T reads
   lanes[2] = (uint32_t)st_off * 2;  // tile stores
   lanes[3] = 8 * hl;                // key offset of this lane half (masking)
-  // global byte offsets of this thread's rows in tile 3 (the first the loop requests)
+  // global byte offsets of this thread's rows in tile 2 (the first the loop code requests)
   u32x4 voff;
-  voff[0] = (3 * kBN + crow) * rs_k + cd0 * 2;
+  voff[0] = (2 * kBN + crow) * rs_k + cd0 * 2;
   voff[1] = voff[0] + 32 * rs_k;
-  voff[2] = (3 * kBN + crow) * rs_v + cd0 * 2;
+  voff[2] = (2 * kBN + crow) * rs_v + cd0 * 2;
   voff[3] = voff[2] + 32 * rs_v;
   const int tsk = kBN * rs_k, tsv = kBN * rs_v;
-  u32x16 stg;
-#pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) stg[4 * i + e] = stage[i][e];
 
   f32x16 acc_o[3][2];
   typedef float f32x3 __attribute__((ext_vector_type(3)));
   f32x3 lr;  // this lane's half of each block's row sum
 #define WDRZ_PIPE_OPERANDS                                                                                    \
   : "={a[0:15]}"(acc_o[0][0]), "={a[16:31]}"(acc_o[0][1]), "={a[32:47]}"(acc_o[1][0]), "={a[48:63]}"(acc_o[1][1]), \
-    "={a[64:79]}"(acc_o[2][0]), "={a[80:95]}"(acc_o[2][1]), "={v[156:158]}"(lr), "+{v[136:151]}"(stg),              \
+    "={a[64:79]}"(acc_o[2][0]), "={a[80:95]}"(acc_o[2][1]), "={v[156:158]}"(lr),                                    \
     "+{v[164:167]}"(voff)                                                                                         \
   : "{a[96:111]}"(q0), "{a[112:127]}"(q1), "{a[128:143]}"(q2), "{v[160:163]}"(lanes), "{s[80:83]}"(srd_k),        \
     "{s[84:87]}"(srd_v), [n] "s"(n_iter), [r] "s"(n_rest), [rem] "s"(rem), [tsk] "s"(tsk), [tsv] "s"(tsv)           \

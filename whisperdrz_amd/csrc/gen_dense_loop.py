@@ -24,8 +24,8 @@ wavefront as three 32-query blocks b = 0, 1, 2; 32 keys per step, 64-key LDS til
   * K and V operands for the MFMAs come from LDS one step ahead into double-buffered AGPRs
     (K through ds_read_b128 in the permuted key order that makes P^T the B operand without
     shuffles; V^T through ds_read_b64_tr_b16). Tiles of 64 keys are staged global -> VGPR ->
-    LDS through four LDS buffers: tile t+2 is written and tile t+3 requested during tile t,
-    one workgroup barrier per tile. Global loads are buffer loads bounded by the tensor's extent
+    LDS through four LDS buffers: tile t+2 is written and tile t+4 requested during tile t
+    (two register sets), one workgroup barrier per tile. Global loads are buffer loads bounded by the tensor's extent
     (rows past the last key read as zero; those keys are never used unmasked).
 
 Register map (the kernel passes these through "{v[..]}" / "{a[..]}" constraints):
@@ -36,6 +36,7 @@ Register map (the kernel passes these through "{v[..]}" / "{a[..]}" constraints)
   v160-163 lane bases: K read, V read, tile store, 8 * (lane >> 5)
   v164-167 global row offsets (K r, K r+32, V r, V r+32)   v168-171 per-tile addresses
   v172-183 rare-path temporaries   v184-207 row-sum temporaries (8 per block)
+  v208-223 second tile staging set
   a0-95 O[b][db] (16 each)   a96-143 Q[b][ks] (4 each)   a144-175 K buffers (2 x 16)
   a176-207 V buffers (2 x 16: [ch][db] operands of 4)
   s70-s79 loop state (clobbered: iteration, tile offsets, sum limit, rescale floor); the kernel
@@ -50,6 +51,7 @@ def CINIT(b): return 48 + 16 * b
 def P(b, ch=0): return 96 + 8 * b + 4 * ch
 T0 = 120
 STAGE = 136
+STAGE2 = 208  # the second staging set (208..223)
 def U(b): return 184 + 8 * b  # row-sum temporaries of block b (184..207)
 def MRUN(b): return 152 + b
 def LRUN(b): return 156 + b  # a 3-register tuple (even-aligned), an output of the loop
@@ -232,28 +234,66 @@ class Gen:
                 out.append(f"ds_read_b64_tr_b16 {ar(dst + 2, 2)}, {vr(base)} offset:{off + 4 * 144}")
         return out
 
-    def staging(self):
-        """Tile t+2 from the staging registers into LDS; tile t+3 requested into them."""
+    def staging(self, stage):
+        """Tile t+2 from staging registers `stage` into LDS; tile t+4 requested into them. The two
+        register sets alternate by iteration, so a tile's loads have two iterations to land: the
+        wait leaves the other set's four loads in flight."""
         w = [
-            "s_waitcnt vmcnt(0)",
-            f"ds_write_b128 {vr(STADDR)}, {vr(STAGE, 4)}",
-            f"ds_write_b128 {vr(STADDR)}, {vr(STAGE + 4, 4)} offset:{HALF_BYTES}",
-            f"ds_write_b128 {vr(STADDR)}, {vr(STAGE + 8, 4)} offset:{V_BASE}",
-            f"ds_write_b128 {vr(STADDR)}, {vr(STAGE + 12, 4)} offset:{V_BASE + HALF_BYTES}",
+            "s_waitcnt vmcnt(4)",
+            f"ds_write_b128 {vr(STADDR)}, {vr(stage, 4)}",
+            f"ds_write_b128 {vr(STADDR)}, {vr(stage + 4, 4)} offset:{HALF_BYTES}",
+            f"ds_write_b128 {vr(STADDR)}, {vr(stage + 8, 4)} offset:{V_BASE}",
+            f"ds_write_b128 {vr(STADDR)}, {vr(stage + 12, 4)} offset:{V_BASE + HALF_BYTES}",
         ]
-        ld = [
-            f"buffer_load_dwordx4 {vr(STAGE, 4)}, {vr(VOFF)}, {SRD_K}, 0 offen",
-            f"buffer_load_dwordx4 {vr(STAGE + 4, 4)}, {vr(VOFF + 1)}, {SRD_K}, 0 offen",
-            f"buffer_load_dwordx4 {vr(STAGE + 8, 4)}, {vr(VOFF + 2)}, {SRD_V}, 0 offen",
-            f"buffer_load_dwordx4 {vr(STAGE + 12, 4)}, {vr(VOFF + 3)}, {SRD_V}, 0 offen",
+        return w, self.tile_loads(stage), self.advance()
+
+    def tile_loads(self, stage):
+        return [
+            f"buffer_load_dwordx4 {vr(stage, 4)}, {vr(VOFF)}, {SRD_K}, 0 offen",
+            f"buffer_load_dwordx4 {vr(stage + 4, 4)}, {vr(VOFF + 1)}, {SRD_K}, 0 offen",
+            f"buffer_load_dwordx4 {vr(stage + 8, 4)}, {vr(VOFF + 2)}, {SRD_V}, 0 offen",
+            f"buffer_load_dwordx4 {vr(stage + 12, 4)}, {vr(VOFF + 3)}, {SRD_V}, 0 offen",
         ]
-        adv = [
+
+    def advance(self):
+        return [
             f"v_add_u32 {vr(VOFF)}, %[tsk], {vr(VOFF)}",
             f"v_add_u32 {vr(VOFF + 1)}, %[tsk], {vr(VOFF + 1)}",
             f"v_add_u32 {vr(VOFF + 2)}, %[tsv], {vr(VOFF + 2)}",
             f"v_add_u32 {vr(VOFF + 3)}, %[tsv], {vr(VOFF + 3)}",
         ]
-        return w, ld, adv
+
+    def iteration(self, stage, it):
+        """One tile: steps 2t and 2t+1, with tile t+2 staged from `stage` and tile t+4 requested."""
+        e = self.emit
+        e(f"s_and_b32 {S_TMP}, {S_IT}, 3")
+        e(f"s_mul_i32 {S_BUFA}, {S_TMP}, {TILE_BYTES}")
+        e(f"s_add_u32 {S_TMP}, {S_IT}, 1")
+        e(f"s_and_b32 {S_TMP}, {S_TMP}, 3")
+        e(f"s_mul_i32 {S_BUFB}, {S_TMP}, {TILE_BYTES}")
+        e(f"s_add_u32 {S_TMP}, {S_IT}, 2")
+        e(f"s_and_b32 {S_TMP}, {S_TMP}, 3")
+        e(f"s_mul_i32 {S_BUFC}, {S_TMP}, {TILE_BYTES}")
+        e(f"v_add_u32 {vr(KADDR)}, {S_BUFB}, {vr(KLANE)}")
+        e(f"v_add_u32 {vr(VADDRA)}, {S_BUFA}, {vr(VLANE)}")
+        e(f"v_add_u32 {vr(VADDRB)}, {S_BUFB}, {vr(VLANE)}")
+        e(f"v_add_u32 {vr(STADDR)}, {S_BUFC}, {vr(STLANE)}")
+        w, ld, adv = self.staging(stage)
+        kr0, vr0 = self.k_reads(0), self.v_reads(0)
+        kr1, vr1 = self.k_reads(1), self.v_reads(1)
+        # step 2t (parity 0)
+        self.phase(0, 0, f"0P0{it}")
+        self.phase(0, 1, f"1P0{it}", pre=["s_waitcnt lgkmcnt(0)"], slots={3: kr0[:2], 4: kr0[2:]})
+        self.phase(0, 2, f"2P0{it}", slots={1: vr0[0:2], 2: vr0[2:4], 3: vr0[4:6], 4: vr0[6:8]})
+        # step 2t+1 (parity 1): the forced first-step rescale is over
+        e(f"s_mov_b32 {S_LIMIT}, {SUM_LIMIT}")
+        e(f"s_mov_b32 {S_FLOOR}, 0")
+        self.phase(1, 0, f"0P1{it}", pre=[w[0]], slots={0: w[1:], 1: ld, 2: adv})
+        self.phase(1, 1, f"1P1{it}", pre=["s_waitcnt lgkmcnt(0)"], slots={3: kr1[:2], 4: kr1[2:]})
+        self.phase(1, 2, f"2P1{it}", slots={1: vr1[0:2], 2: vr1[2:4], 3: vr1[4:6], 4: vr1[6:8]})
+        e("s_waitcnt lgkmcnt(0)")
+        e("s_barrier")
+        e(f"s_add_u32 {S_IT}, {S_IT}, 1")
 
     def build(self):
         e = self.emit
@@ -282,42 +322,20 @@ class Gen:
             for ks in range(4):
                 c = "0" if ks == 0 else vr(S(b), 16)
                 e(f"{self.mfma} {vr(S(b), 16)}, {ar(KB(0, ks), 4)}, {ar(Q(b, ks), 4)}, {c}")
+        for x in self.tile_loads(STAGE) + self.advance() + self.tile_loads(STAGE2) + self.advance():
+            e(x)
         e(f"v_mov_b32 {vr(NEGINF)}, 0xff800000")
         e(f"s_mov_b32 {S_LIMIT}, -1.0")
         e(f"s_mov_b32 {S_FLOOR}, 0xff800000")
         e(f"s_mov_b32 {S_IT}, 0")
         e("s_cmp_eq_u32 %[n], 0")
         e("s_cbranch_scc1 LEND_%=")
-        # ---- loop over tiles ----
+        # ---- loop over tiles, two per trip (the staging register sets alternate) ----
         e("LLOOP_%=:")
-        e(f"s_and_b32 {S_TMP}, {S_IT}, 3")
-        e(f"s_mul_i32 {S_BUFA}, {S_TMP}, {TILE_BYTES}")
-        e(f"s_add_u32 {S_TMP}, {S_IT}, 1")
-        e(f"s_and_b32 {S_TMP}, {S_TMP}, 3")
-        e(f"s_mul_i32 {S_BUFB}, {S_TMP}, {TILE_BYTES}")
-        e(f"s_add_u32 {S_TMP}, {S_IT}, 2")
-        e(f"s_and_b32 {S_TMP}, {S_TMP}, 3")
-        e(f"s_mul_i32 {S_BUFC}, {S_TMP}, {TILE_BYTES}")
-        e(f"v_add_u32 {vr(KADDR)}, {S_BUFB}, {vr(KLANE)}")
-        e(f"v_add_u32 {vr(VADDRA)}, {S_BUFA}, {vr(VLANE)}")
-        e(f"v_add_u32 {vr(VADDRB)}, {S_BUFB}, {vr(VLANE)}")
-        e(f"v_add_u32 {vr(STADDR)}, {S_BUFC}, {vr(STLANE)}")
-        w, ld, adv = self.staging()
-        kr0, vr0 = self.k_reads(0), self.v_reads(0)
-        kr1, vr1 = self.k_reads(1), self.v_reads(1)
-        # step 2t (parity 0)
-        self.phase(0, 0, "0P0")
-        self.phase(0, 1, "1P0", pre=["s_waitcnt lgkmcnt(0)"], slots={3: kr0[:2], 4: kr0[2:]})
-        self.phase(0, 2, "2P0", slots={1: vr0[0:2], 2: vr0[2:4], 3: vr0[4:6], 4: vr0[6:8]})
-        # step 2t+1 (parity 1): the forced first-step rescale is over
-        e(f"s_mov_b32 {S_LIMIT}, {SUM_LIMIT}")
-        e(f"s_mov_b32 {S_FLOOR}, 0")
-        self.phase(1, 0, "0P1", pre=[w[0]], slots={0: w[1:], 1: ld, 2: adv})
-        self.phase(1, 1, "1P1", pre=["s_waitcnt lgkmcnt(0)"], slots={3: kr1[:2], 4: kr1[2:]})
-        self.phase(1, 2, "2P1", slots={1: vr1[0:2], 2: vr1[2:4], 3: vr1[4:6], 4: vr1[6:8]})
-        e("s_waitcnt lgkmcnt(0)")
-        e("s_barrier")
-        e(f"s_add_u32 {S_IT}, {S_IT}, 1")
+        self.iteration(STAGE, "A")
+        e(f"s_cmp_ge_u32 {S_IT}, %[n]")
+        e("s_cbranch_scc1 LEND_%=")
+        self.iteration(STAGE2, "B")
         e(f"s_cmp_lt_u32 {S_IT}, %[n]")
         e("s_cbranch_scc1 LLOOP_%=")
         e("LEND_%=:")
