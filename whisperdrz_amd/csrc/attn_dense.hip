@@ -965,6 +965,8 @@ constexpr int kPThreads = kPWaves * 64;
 constexpr int kPBM = 96 * kPWaves;  // queries per workgroup
 constexpr int kPTile = kBN * kPitchK;  // elements of one 64-key tile buffer
 constexpr int kPMinKeys = 64;         // the loop needs two tiles up front
+constexpr int kPQElems = kPBM * 64;   // the Q area: 384 rows of 64 elements (no pad; chunks swizzled)
+constexpr int kPQPieces = kPBM * 128 / kPThreads / 16;  // 1 KB prefetch pieces per wavefront (12)
 
 typedef float f32x32 __attribute__((ext_vector_type(32)));
 typedef uint32_t u32x32 __attribute__((ext_vector_type(32)));
@@ -1000,161 +1002,204 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
   "v181", "v182", "v183", "v184", "v185", "v186", "v187", "v188", "v189", "v190", "v191", "v192", "v193", \
   "v194", "v195", "v196", "v197", "v198", "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", \
   "v207", "v208", "v209", "v210", "v211", "v212", "v213", "v214", "v215", "v216", "v217", "v218", "v219", \
-  "v220", "v221", "v222", "v223", "a144", "a145", "a146", "a147", "a148", "a149", "a150", "a151", "a152", \
-  "a153", "a154", "a155", "a156", "a157", "a158", "a159", "a160", "a161", "a162", "a163", "a164", "a165", \
-  "a166", "a167", "a168", "a169", "a170", "a171", "a172", "a173", "a174", "a175", "a176", "a177", "a178", \
-  "a179", "a180", "a181", "a182", "a183", "a184", "a185", "a186", "a187", "a188", "a189", "a190", "a191", \
-  "a192", "a193", "a194", "a195", "a196", "a197", "a198", "a199", "a200", "a201", "a202", "a203", "a204", \
-  "a205", "a206", "a207", "s70", "s71", "s72", "s73", "s74", "s75", "s76", "s77", "s78", "s79", "vcc", "scc", \
-  "memory"
+  "v220", "v221", "v222", "v223", "v225", "a144", "a145", "a146", "a147", "a148", "a149", "a150", "a151", \
+  "a152", "a153", "a154", "a155", "a156", "a157", "a158", "a159", "a160", "a161", "a162", "a163", "a164", \
+  "a165", "a166", "a167", "a168", "a169", "a170", "a171", "a172", "a173", "a174", "a175", "a176", "a177", \
+  "a178", "a179", "a180", "a181", "a182", "a183", "a184", "a185", "a186", "a187", "a188", "a189", "a190", \
+  "a191", "a192", "a193", "a194", "a195", "a196", "a197", "a198", "a199", "a200", "a201", "a202", "a203", \
+  "a204", "a205", "a206", "a207", "s70", "s71", "s72", "s73", "s74", "s75", "s76", "s77", "s78", "s79", "m0", \
+  "vcc", "scc", "memory"
 
 template <typename T>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void dense_pipe_kernel(DenseArgs a) {
   typedef typename Mfma<T>::op_t op_t;
   typedef uint16_t e_t;
-  // four K tile buffers, then four V tile buffers, row-major [key][dim] with a 16-byte row pad;
-  // Q and O are staged through the same memory at the start and the end
-  __shared__ __attribute__((aligned(16))) e_t smem[8 * kPTile];
-  static_assert(kPBM * kPitchK <= 8 * kPTile, "Q/O staging must fit the tile buffers");
+  // [Q rows: 384 x 128 B, 16-byte chunks XOR-swizzled by the row] [four K tile buffers] [four V
+  // tile buffers] (tiles row-major [key][dim] with a 16-byte row pad); O is staged through the
+  // tile buffers at the end of each item
+  __shared__ __attribute__((aligned(16))) e_t smem[kPQElems + 8 * kPTile];
+  e_t* const tiles = smem + kPQElems;
+  static_assert(kPBM * kPitchK <= 8 * kPTile, "O staging must fit the tile buffers");
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int hl = lane >> 5;
   const int l32 = lane & 31;
-
-  const int n_qblk = (a.Lq + kPBM - 1) / kPBM;
-  const int tile_id = remap_xcd(blockIdx.x, gridDim.x);
-  const int qblk = tile_id % n_qblk;
-  const int bh = tile_id / n_qblk;
-  const int b = bh / a.H, h = bh % a.H;
-  const e_t* Q = reinterpret_cast<const e_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
-  const e_t* K = reinterpret_cast<const e_t*>(a.k) + b * a.ks[0] + h * a.ks[1];
-  const e_t* V = reinterpret_cast<const e_t*>(a.v) + b * a.vs[0] + h * a.vs[1];
-  e_t* O = reinterpret_cast<e_t*>(a.o) + b * a.os[0] + h * a.os[1];
-  const int q_blk0 = qblk * kPBM;
   const float c = a.c;
+  const int n_qblk = (a.Lq + kPBM - 1) / kPBM;
+  const int n_items = a.B * a.H * n_qblk;
 
   // Row-contiguous transfers: thread tid moves 16-byte chunk (tid & 7) of rows tid/8 + 32*i.
   const int crow = tid >> 3, cd0 = (tid & 7) * 8;
-  const int rs_k = (int)a.ks[2] * 2, rs_v = (int)a.vs[2] * 2;  // row strides in bytes
-  const i32x4 srd_k = buffer_rsrc(K, (uint32_t)((a.Lk - 1) * rs_k + 128));
-  const i32x4 srd_v = buffer_rsrc(V, (uint32_t)((a.Lk - 1) * rs_v + 128));
-  auto tile_load = [&](int kt, u32x4 (&st)[4]) __attribute__((always_inline)) {
+  const int rs_k = (int)a.ks[2] * 2, rs_v = (int)a.vs[2] * 2, rs_q = (int)a.qs[2] * 2;  // row strides, bytes
+  const int st_off = crow * kPitchK + cd0;  // elements
+
+  // The per-item pointers: item id (dispatch order) -> (b, h, query block), XCD-aware.
+  struct Item {
+    const e_t *q, *k, *v;
+    e_t* o;
+    int q0;
+  };
+  auto item_of = [&](int id) {
+    const int t = remap_xcd(id, n_items);
+    const int qblk = t % n_qblk, bh = t / n_qblk;
+    const int b = bh / a.H, h = bh % a.H;
+    Item it;
+    it.q = reinterpret_cast<const e_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
+    it.k = reinterpret_cast<const e_t*>(a.k) + b * a.ks[0] + h * a.ks[1];
+    it.v = reinterpret_cast<const e_t*>(a.v) + b * a.vs[0] + h * a.vs[1];
+    it.o = reinterpret_cast<e_t*>(a.o) + b * a.os[0] + h * a.os[1];
+    it.q0 = qblk * kPBM;
+    return it;
+  };
+  auto tile_load = [&](const Item& it, int kt, u32x4 (&st)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
       const int r = kt * kBN + crow + 32 * i;
       const bool in = r < a.Lk;
       const int rc = in ? r : a.Lk - 1;
-      st[i] = load16(K + (int64_t)rc * a.ks[2] + cd0);
-      st[2 + i] = load16(V + (int64_t)rc * a.vs[2] + cd0);
+      st[i] = load16(it.k + (int64_t)rc * a.ks[2] + cd0);
+      st[2 + i] = load16(it.v + (int64_t)rc * a.vs[2] + cd0);
       if (!in) st[i] = st[2 + i] = u32x4{0u, 0u, 0u, 0u};
     }
   };
-  const int st_off = crow * kPitchK + cd0;  // elements
   auto tile_store = [&](int buf, const u32x4 (&st)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      *reinterpret_cast<u32x4*>(&smem[buf * kPTile + st_off + 32 * i * kPitchK]) = st[i];
-      *reinterpret_cast<u32x4*>(&smem[(4 + buf) * kPTile + st_off + 32 * i * kPitchK]) = st[2 + i];
+      *reinterpret_cast<u32x4*>(&tiles[buf * kPTile + st_off + 32 * i * kPitchK]) = st[i];
+      *reinterpret_cast<u32x4*>(&tiles[(4 + buf) * kPTile + st_off + 32 * i * kPitchK]) = st[2 + i];
+    }
+  };
+  // Q rows through registers into the swizzled Q area (the first item; short keys)
+  auto q_load_sync = [&](const Item& it) __attribute__((always_inline)) {
+    u32x4 qc[kPBM / 32];
+#pragma unroll
+    for (int i = 0; i < kPBM / 32; ++i) qc[i] = load16(it.q + min(it.q0 + crow + 32 * i, a.Lq - 1) * a.qs[2] + cd0);
+#pragma unroll
+    for (int i = 0; i < kPBM / 32; ++i) {
+      const int row = crow + 32 * i;
+      *reinterpret_cast<u32x4*>(&smem[row * 64 + (((tid & 7) ^ (row & 7)) << 3)]) = qc[i];
     }
   };
 
-  // ---- Q: whole rows into LDS, then each wavefront's operand registers, pre-scaled by c ----
-  u32x4 t0[4], t1[4];
-  {
-    u32x4 qc[kPBM / 32];
-#pragma unroll
-    for (int i = 0; i < kPBM / 32; ++i) qc[i] = load16(Q + min(q_blk0 + crow + 32 * i, a.Lq - 1) * a.qs[2] + cd0);
-    tile_load(0, t0);
-    tile_load(1, t1);
-#pragma unroll
-    for (int i = 0; i < kPBM / 32; ++i) *reinterpret_cast<u32x4*>(&smem[(crow + 32 * i) * kPitchK + cd0]) = qc[i];
-  }
-  __syncthreads();
-  u32x16 q0, q1, q2;
-#pragma unroll
-  for (int qb = 0; qb < 3; ++qb)
-#pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
-      const u32x4 raw =
-          *reinterpret_cast<const u32x4*>(&smem[(wave * 96 + qb * 32 + l32) * kPitchK + ks * 16 + hl * 8]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t w = Mfma<T>::pack(Mfma<T>::widen_lo(raw[e]) * c, Mfma<T>::widen_hi(raw[e]) * c);
-        (qb == 0 ? q0 : qb == 1 ? q1 : q2)[ks * 4 + e] = w;
-      }
-    }
-  __syncthreads();
-  tile_store(0, t0);
-  tile_store(1, t1);
-  __syncthreads();
-
-  // ---- the hand-scheduled loop over pairs of 32-key steps (full tiles), then the remaining
-  // steps (the last one masked at Lk) and the last block's P V, all in the generated code ----
+  // ---- constants of the generated loop ----
   const int n_sub = (a.Lk + kBS - 1) / kBS;
   const int n_iter = (a.Lk / kBS) / 2;
-  const int n_rest = n_sub - 2 * n_iter;       // 0, 1 or 2
-  const int rem = a.Lk - kBS * (n_sub - 1);    // valid keys of the last step
+  const int n_rest = n_sub - 2 * n_iter;     // 0, 1 or 2
+  const int rem = a.Lk - kBS * (n_sub - 1);  // valid keys of the last step
+  // the next item's Q rows are requested by the loop code (one 1 KB piece per wavefront and
+  // iteration) when the loop has the iterations for it
+  const int n_pf = n_iter >= kPQPieces ? kPQPieces : 0;
   // LDS byte offsets of this lane's operand reads (the permuted K rows; V^T through the
   // transposing read), and of its tile stores
   const int pm = l32;
   const int pi_row = 16 * ((pm >> 3) >> 1) + 8 * ((pm >> 2) & 1) + 4 * ((pm >> 3) & 1) + (pm & 3);
   const int g16 = lane >> 4, j16 = lane & 15;
+  const uint32_t tbase = kPQElems * 2;  // byte offset of the tile buffers
   u32x4 lanes;
-  lanes[0] = (uint32_t)(pi_row * kPitchK + hl * 8) * 2;  // K reads
-  lanes[1] = (uint32_t)((8 * (g16 >> 1) + (j16 >> 2)) * kPitchK + 16 * (g16 & 1) + 4 * (j16 & 3)) * 2;  // V^T reads
-  lanes[2] = (uint32_t)st_off * 2;  // tile stores
-  lanes[3] = 8 * hl;                // key offset of this lane half (masking)
-  // global byte offsets of this thread's rows in tile 2 (the first the loop code requests)
-  u32x4 voff;
-  voff[0] = (2 * kBN + crow) * rs_k + cd0 * 2;
-  voff[1] = voff[0] + 32 * rs_k;
-  voff[2] = (2 * kBN + crow) * rs_v + cd0 * 2;
-  voff[3] = voff[2] + 32 * rs_v;
+  lanes[0] = tbase + (uint32_t)(pi_row * kPitchK + hl * 8) * 2;  // K reads
+  lanes[1] = tbase + (uint32_t)((8 * (g16 >> 1) + (j16 >> 2)) * kPitchK + 16 * (g16 & 1) + 4 * (j16 & 3)) * 2;
+  lanes[2] = tbase + (uint32_t)st_off * 2;  // tile stores
+  lanes[3] = 8 * hl;                        // key offset of this lane half (masking)
   const int tsk = kBN * rs_k, tsv = kBN * rs_v;
+  // the Q prefetch: this lane's piece of row 8j + lane/8 of its wavefront's 96, swizzled chunk
+  const uint32_t qvoff = (uint32_t)((wave * 96 + (lane >> 3)) * rs_q + (((lane & 7) ^ (lane >> 3)) << 4));
+  const int qlds = __builtin_amdgcn_readfirstlane(wave * 96 * 128), qstep = 8 * rs_q;
 
-  f32x16 acc_o[3][2];
-  typedef float f32x3 __attribute__((ext_vector_type(3)));
-  f32x3 lr;  // this lane's half of each block's row sum
+  // Persistent: each workgroup takes items id, id + G, ... (G = grid size, a multiple of 8 so an
+  // item stays on its XCD). While item k runs, item k+1's Q rows arrive in the Q area; its first
+  // two K/V tiles are requested before item k's output is written.
+  int id = blockIdx.x;
+  Item cur = item_of(id);
+  u32x4 t0[4], t1[4];
+  q_load_sync(cur);
+  tile_load(cur, 0, t0);
+  tile_load(cur, 1, t1);
+  for (;;) {
+    const int next_id = id + (int)gridDim.x;
+    const bool has_next = next_id < n_items;
+    const Item nxt = item_of(has_next ? next_id : id);
+    __syncthreads();  // the Q rows are in place; the previous item is done with the tile buffers
+    u32x16 q0, q1, q2;
+#pragma unroll
+    for (int qb = 0; qb < 3; ++qb)
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) {
+        const int row = wave * 96 + qb * 32 + l32;
+        const u32x4 raw = *reinterpret_cast<const u32x4*>(&smem[row * 64 + (((2 * ks + hl) ^ (row & 7)) << 3)]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t w = Mfma<T>::pack(Mfma<T>::widen_lo(raw[e]) * c, Mfma<T>::widen_hi(raw[e]) * c);
+          (qb == 0 ? q0 : qb == 1 ? q1 : q2)[ks * 4 + e] = w;
+        }
+      }
+    tile_store(0, t0);
+    tile_store(1, t1);
+    __syncthreads();  // tiles 0, 1 in place; every wavefront has its Q operands (the Q area is free)
+
+    // ---- the generated loop and the remaining steps (the last one masked at Lk) ----
+    const i32x4 srd_k = buffer_rsrc(cur.k, (uint32_t)((a.Lk - 1) * rs_k + 128));
+    const i32x4 srd_v = buffer_rsrc(cur.v, (uint32_t)((a.Lk - 1) * rs_v + 128));
+    const int nq_next = min(kPBM, a.Lq - nxt.q0);
+    const i32x4 srd_q = buffer_rsrc(nxt.q + (int64_t)nxt.q0 * a.qs[2], (uint32_t)((nq_next - 1) * rs_q + 128));
+    const int npf = has_next ? n_pf : 0;
+    // global byte offsets of this thread's rows in tile 2 (the first the loop code requests)
+    u32x4 voff;
+    voff[0] = (2 * kBN + crow) * rs_k + cd0 * 2;
+    voff[1] = voff[0] + 32 * rs_k;
+    voff[2] = (2 * kBN + crow) * rs_v + cd0 * 2;
+    voff[3] = voff[2] + 32 * rs_v;
+    f32x16 acc_o[3][2];
+    typedef float f32x3 __attribute__((ext_vector_type(3)));
+    f32x3 lr;  // this lane's half of each block's row sum
 #define WDRZ_PIPE_OPERANDS                                                                                    \
   : "={a[0:15]}"(acc_o[0][0]), "={a[16:31]}"(acc_o[0][1]), "={a[32:47]}"(acc_o[1][0]), "={a[48:63]}"(acc_o[1][1]), \
-    "={a[64:79]}"(acc_o[2][0]), "={a[80:95]}"(acc_o[2][1]), "={v[156:158]}"(lr),                                    \
-    "+{v[164:167]}"(voff)                                                                                         \
-  : "{a[96:111]}"(q0), "{a[112:127]}"(q1), "{a[128:143]}"(q2), "{v[160:163]}"(lanes), "{s[80:83]}"(srd_k),        \
-    "{s[84:87]}"(srd_v), [n] "s"(n_iter), [r] "s"(n_rest), [rem] "s"(rem), [tsk] "s"(tsk), [tsv] "s"(tsv)           \
+    "={a[64:79]}"(acc_o[2][0]), "={a[80:95]}"(acc_o[2][1]), "={v[156:158]}"(lr), "+{v[164:167]}"(voff)             \
+  : "{a[96:111]}"(q0), "{a[112:127]}"(q1), "{a[128:143]}"(q2), "{v[160:163]}"(lanes), "{v224}"(qvoff),            \
+    "{s[80:83]}"(srd_k), "{s[84:87]}"(srd_v), "{s[88:91]}"(srd_q), [n] "s"(n_iter), [r] "s"(n_rest),                \
+    [rem] "s"(rem), [tsk] "s"(tsk), [tsv] "s"(tsv), [npf] "s"(npf), [qlds] "s"(qlds), [qstep] "s"(qstep)          \
   : WDRZ_PIPE_CLOBBERS
-  __builtin_amdgcn_sched_barrier(0);
-  if constexpr (__is_same(T, Bf16))
-    asm volatile(WDRZ_DENSE_LOOP_BF16 WDRZ_PIPE_OPERANDS);
-  else
-    asm volatile(WDRZ_DENSE_LOOP_F16 WDRZ_PIPE_OPERANDS);
-  __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (__is_same(T, Bf16))
+      asm volatile(WDRZ_DENSE_LOOP_BF16 WDRZ_PIPE_OPERANDS);
+    else
+      asm volatile(WDRZ_DENSE_LOOP_F16 WDRZ_PIPE_OPERANDS);
+    __builtin_amdgcn_sched_barrier(0);
 #undef WDRZ_PIPE_OPERANDS
-  const float l_run[3] = {lr[0], lr[1], lr[2]};
 
-  // ---- normalise, stage O^T through LDS as [query][dim] rows, store whole rows ----
-  __syncthreads();  // every wavefront is done with the tiles
+    // the next item's first tiles, in flight while this item's output is written
+    if (has_next) {
+      tile_load(nxt, 0, t0);
+      tile_load(nxt, 1, t1);
+    }
+    // ---- normalise, stage O^T through the tile buffers as [query][dim] rows, store whole rows ----
+    __syncthreads();  // every wavefront is done with the tiles
 #pragma unroll
-  for (int qb = 0; qb < 3; ++qb) {
-    const float inv = 1.f / (l_run[qb] + __shfl_xor(l_run[qb], 32));
-    e_t* orow = &smem[(wave * 96 + qb * 32 + l32) * kPitchK];
+    for (int qb = 0; qb < 3; ++qb) {
+      const float inv = 1.f / (lr[qb] + __shfl_xor(lr[qb], 32));
+      e_t* orow = &tiles[(wave * 96 + qb * 32 + l32) * kPitchK];
 #pragma unroll
-    for (int db = 0; db < 2; ++db)
+      for (int db = 0; db < 2; ++db)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        u32x2 w;
-        w[0] = Mfma<T>::pack(acc_o[qb][db][i * 4 + 0] * inv, acc_o[qb][db][i * 4 + 1] * inv);
-        w[1] = Mfma<T>::pack(acc_o[qb][db][i * 4 + 2] * inv, acc_o[qb][db][i * 4 + 3] * inv);
-        *reinterpret_cast<u32x2*>(orow + db * 32 + i * 8 + hl * 4) = w;
-      }
-  }
-  __syncthreads();
+        for (int i = 0; i < 4; ++i) {
+          u32x2 w;
+          w[0] = Mfma<T>::pack(acc_o[qb][db][i * 4 + 0] * inv, acc_o[qb][db][i * 4 + 1] * inv);
+          w[1] = Mfma<T>::pack(acc_o[qb][db][i * 4 + 2] * inv, acc_o[qb][db][i * 4 + 3] * inv);
+          *reinterpret_cast<u32x2*>(orow + db * 32 + i * 8 + hl * 4) = w;
+        }
+    }
+    __syncthreads();
 #pragma unroll
-  for (int i = 0; i < kPBM / 32; ++i) {
-    const int qi = q_blk0 + crow + 32 * i;
-    if (qi < a.Lq)
-      store16(O + qi * a.os[2] + cd0, *reinterpret_cast<const u32x4*>(&smem[(crow + 32 * i) * kPitchK + cd0]));
+    for (int i = 0; i < kPBM / 32; ++i) {
+      const int qi = cur.q0 + crow + 32 * i;
+      if (qi < a.Lq)
+        store16(cur.o + qi * a.os[2] + cd0, *reinterpret_cast<const u32x4*>(&tiles[(crow + 32 * i) * kPitchK + cd0]));
+    }
+    if (!has_next) break;
+    if (npf == 0) q_load_sync(nxt);  // (too few iterations to request it during the loop)
+    id = next_id;
+    cur = nxt;
   }
 }
 
@@ -1669,7 +1714,8 @@ hipError_t launch_typed(const DenseArgs& a, hipStream_t stream) {
     // the hand-scheduled 384-query kernel when its grid fills the chip
     const int64_t np = bh * ((a.Lq + kPBM - 1) / kPBM);
     if (a.Lk >= kPMinKeys && np >= kNumCus && np <= 0x7fffffff) {
-      hipLaunchKernelGGL((dense_pipe_kernel<T>), dim3((unsigned)np), dim3(kPThreads), 0, stream, a);
+      // persistent: one workgroup per CU, each taking every 256th item
+      hipLaunchKernelGGL((dense_pipe_kernel<T>), dim3((unsigned)kNumCus), dim3(kPThreads), 0, stream, a);
       return hipGetLastError();
     }
     const int64_t bh_main = (n / kNumCus) * kNumCus / qf;  // heads filling whole rounds

@@ -27,6 +27,8 @@ wavefront as three 32-query blocks b = 0, 1, 2; 32 keys per step, 64-key LDS til
     LDS through four LDS buffers: tile t+2 is written and tile t+4 requested during tile t
     (two register sets), one workgroup barrier per tile. Global loads are buffer loads bounded by the tensor's extent
     (rows past the last key read as zero; those keys are never used unmasked).
+  * The kernel is persistent; during the first 12 iterations of an item each wavefront also
+    requests one 1 KB piece of the next item's Q rows straight into LDS (buffer loads to LDS).
 
 Register map (the kernel passes these through "{v[..]}" / "{a[..]}" constraints):
   v0-47 S[b] (16 each)   v48-95 cinit[b]   v96-119 P[b] (8 each: two 16-key chunks)
@@ -36,11 +38,11 @@ Register map (the kernel passes these through "{v[..]}" / "{a[..]}" constraints)
   v160-163 lane bases: K read, V read, tile store, 8 * (lane >> 5)
   v164-167 global row offsets (K r, K r+32, V r, V r+32)   v168-171 per-tile addresses
   v172-183 rare-path temporaries   v184-207 row-sum temporaries (8 per block)
-  v208-223 second tile staging set
+  v208-223 second tile staging set   v224 Q prefetch lane offset   v225 its address
   a0-95 O[b][db] (16 each)   a96-143 Q[b][ks] (4 each)   a144-175 K buffers (2 x 16)
   a176-207 V buffers (2 x 16: [ch][db] operands of 4)
   s70-s79 loop state (clobbered: iteration, tile offsets, sum limit, rescale floor); the kernel
-  passes the buffer resources in s[80:83], s[84:87].
+  passes the buffer resources of K, V and the next item's Q rows in s[80:83], s[84:87], s[88:91].
 """
 import sys
 from pathlib import Path
@@ -52,6 +54,7 @@ def P(b, ch=0): return 96 + 8 * b + 4 * ch
 T0 = 120
 STAGE = 136
 STAGE2 = 208  # the second staging set (208..223)
+QVOFF, QV = 224, 225  # the Q prefetch: this lane's row offset, and the piece's address
 def U(b): return 184 + 8 * b  # row-sum temporaries of block b (184..207)
 def MRUN(b): return 152 + b
 def LRUN(b): return 156 + b  # a 3-register tuple (even-aligned), an output of the loop
@@ -69,7 +72,7 @@ def VB(p, ch, db): return 176 + 16 * p + 8 * ch + 4 * db
 S_N = None  # the iteration count comes in through an operand: %[n]
 S_IT, S_BUFA, S_BUFB, S_BUFC, S_TMP = "s70", "s71", "s72", "s73", "s74"
 S_LIMIT, S_FLOOR = "s76", "s78"
-SRD_K, SRD_V = "s[80:83]", "s[84:87]"
+SRD_K, SRD_V, SRD_Q = "s[80:83]", "s[84:87]", "s[88:91]"
 
 TILE_BYTES = 64 * 72 * 2   # one 64-key tile of K (or V): 64 rows x 72 elements (16-byte pad)
 HALF_BYTES = 32 * 72 * 2   # 32 key rows
@@ -288,7 +291,22 @@ class Gen:
         # step 2t+1 (parity 1): the forced first-step rescale is over
         e(f"s_mov_b32 {S_LIMIT}, {SUM_LIMIT}")
         e(f"s_mov_b32 {S_FLOOR}, 0")
-        self.phase(1, 0, f"0P1{it}", pre=[w[0]], slots={0: w[1:], 1: ld, 2: adv})
+        # the next item's Q rows: piece S_IT of this wavefront's 12 (1 KB each), straight into
+        # the Q area (LDS DMA at m0), requested before the tile loads so that the staging waits
+        # (vmcnt(4)) keep their meaning
+        pf = [
+            f"s_cmp_lt_u32 {S_IT}, %[npf]",
+            f"s_cbranch_scc0 LNQ{it}_%=",
+            f"s_lshl_b32 {S_TMP}, {S_IT}, 10",
+            f"s_add_u32 {S_TMP}, {S_TMP}, %[qlds]",
+            f"s_mov_b32 m0, {S_TMP}",
+            f"s_mul_i32 {S_TMP}, {S_IT}, %[qstep]",
+            f"v_add_u32 {vr(QV)}, {S_TMP}, {vr(QVOFF)}",
+            "s_nop 0",
+            f"buffer_load_dwordx4 {vr(QV)}, {SRD_Q}, 0 offen lds",
+            f"LNQ{it}_%=:",
+        ]
+        self.phase(1, 0, f"0P1{it}", pre=[w[0]], slots={0: w[1:], 1: pf + ld, 2: adv})
         self.phase(1, 1, f"1P1{it}", pre=["s_waitcnt lgkmcnt(0)"], slots={3: kr1[:2], 4: kr1[2:]})
         self.phase(1, 2, f"2P1{it}", slots={1: vr1[0:2], 2: vr1[2:4], 3: vr1[4:6], 4: vr1[6:8]})
         e("s_waitcnt lgkmcnt(0)")
