@@ -402,6 +402,29 @@ class Gen:
         return self.out
 
 
+def _vregs(ops):
+    out = set()
+    for o in ops:
+        o = o.rstrip(",")
+        if o.startswith("v["):
+            lo, hi = o[2:-1].split(":")
+            out |= set(range(int(lo), int(hi) + 1))
+        elif o[:1] == "v" and o[1:].isdigit():
+            out.add(int(o[1:]))
+    return out
+
+
+def check_trans_hazards(body):
+    """A transcendental's result is not forwarded: the VALU instruction right after a v_exp must
+    not read it (one wait state)."""
+    for i in range(len(body) - 1):
+        if body[i].startswith("v_exp"):
+            dst = _vregs(body[i].split()[1:2])
+            nxt = body[i + 1].split()
+            if nxt and nxt[0].startswith("v_") and dst & _vregs(nxt[2:]):
+                raise AssertionError(f"trans hazard: {body[i]!r} -> {body[i + 1]!r}")
+
+
 def render() -> str:
     lines = [
         "// Generated by gen_dense_loop.py -- do not edit; edit the generator and rebuild.",
@@ -411,6 +434,7 @@ def render() -> str:
     ]
     for dtype in ("bf16", "f16"):
         body = Gen(dtype).build()
+        check_trans_hazards(body)
         lines.append(f"#define WDRZ_DENSE_LOOP_{dtype.upper()} \\")
         for s in body:
             lines.append(f'  "{s}\\n" \\')
