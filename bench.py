@@ -139,9 +139,9 @@ def bench_encoder(dev, steps: int, warmup: int) -> dict:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": measured_traffic("dense_fwd_kernel<wdrz::Bf16>"),
+            "traffic": measured_traffic("dense_pipe_kernel<wdrz::Bf16>"),
             "traffic_source": "profiles/pmc_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE passes)",
-            "kernel": "dense_fwd_kernel<Bf16>",
+            "kernel": "dense_pipe_kernel<Bf16>",
             "flop_per_launch": flop_layer,
             "ms_per_launch": ms_launch,
             # softmax exponentials per layer (B*H*L^2) and their rate: the VALU side of the kernel
@@ -1046,6 +1046,74 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
     }
 
 
+# Algorithmic HBM bytes per launch of each kernel at the pmc_sample shapes (what the kernel must
+# read and write at least), against which the measured traffic is compared.
+_ALG_BYTES = {
+    "dense_pipe_kernel<wdrz::Bf16>": 4 * 16 * 1500 * 20 * 64 * 2,  # Q + K + V + O
+    "kv_attn_kernel<wdrz::Bf16, 1, true>": 68526592,
+    "kv_attn_kernel<wdrz::Bf16, 1, false>": 491847936,
+    "kv_mq_kernel<wdrz::Bf16, true, 8>": 75279872,
+    "kv_mq_kernel<wdrz::Bf16, false, 8>": 493158656,
+    "dtw_rowcol_kernel<6>": 430080000,
+    "dtw_seg_kernel": 430080000 + 43008000,
+    "dtw_qk_kernel<wdrz::Bf16>": 430080000 + 2 * 16 * 10 * (448 + 1500) * 64,
+    "kv_fill_kernel": 2 * 2 * 16 * 1500 * 1280 * 2,
+    "median_filter_kernel<3>": 2 * 16 * 10 * 448 * 1500 * 4,
+    "dtw_qk_rowcol_kernel<wdrz::Bf16>": 2 * 16 * 10 * (448 + 1500) * 64 + 16 * 10 * 448 * 8 + 16 * 10 * 4 * 1500 * 8,
+    "dtw_qk_band_kernel<wdrz::Bf16, 3>": 2 * 16 * 10 * (448 + 1500) * 64 + 16 * 10 * (448 + 1500) * 8
+    + 16 * 448 * 1500 * 4,
+    "dense_f32_kernel<false>": 4 * 1500 * 20 * 64 * 4,
+    "dense_split4_kernel<wdrz::Bf16>": 4 * 1500 * 20 * 64 * 2,
+    "linear_act_kernel<wdrz::Bf16, 1, 2, 2, false>": 5120 * 1280 * 2 + 64 * 1280 * 2 + 5120 * 2 + 64 * 5120 * 2,
+    "linear_act_kernel<wdrz::Bf16, 0, 2, 2, true>": 1280 * 5120 * 2 + 64 * 5120 * 2 + 4 * 64 * 1280 * 4,
+    "kv_prefill_kernel<wdrz::Bf16, true>": 6 * 64 * 224 * 20 * 64 * 2,
+}
+
+
+def pmc_table(fetch_csv: str, write_csv: str) -> None:
+    """Writes profiles/pmc_traffic.json (and prints its markdown table) from the counter CSVs of
+    two `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` runs of `bench.py --pmc-sample`. Both
+    counters are scaled by what they read for the 1 GiB calibration copy (1 GiB read, 1 GiB
+    written)."""
+    import collections
+    import csv
+    import re
+
+    def load(path, ctr):
+        d = collections.defaultdict(list)
+        with open(path) as f:
+            for r in csv.DictReader(f):
+                if r["Counter_Name"] == ctr:
+                    d[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+        return d
+
+    fe, wr = load(fetch_csv, "FETCH_SIZE"), load(write_csv, "WRITE_SIZE")
+    cf, cw = max(fe["__amd_rocclr_copyBuffer"]), max(wr["__amd_rocclr_copyBuffer"])
+    ff, wf = (1 << 20) / cf, (1 << 20) / cw
+    out = {"calibration": {"copy_bytes_read": 1 << 30, "copy_bytes_written": 1 << 30, "fetch_size_KiB": cf,
+                           "write_size_KiB": cw, "fetch_factor": round(ff, 4), "write_factor": round(wf, 4)},
+           "kernels": {}}
+    rows = []
+    for name in fe:
+        m = re.match(r"(?:void )?wdrz::\(anonymous namespace\)::(\w+(?:<[^()]*>)?)\(", name)
+        if not m or name not in wr:
+            continue
+        k = m.group(1)
+        f, w = sum(fe[name]) / len(fe[name]), sum(wr[name]) / len(wr[name])
+        rb, wb = int(f * 1024 * ff), int(w * 1024 * wf)
+        alg = _ALG_BYTES.get(k)
+        out["kernels"][k] = {"fetch_KiB_raw": round(f, 1), "write_KiB_raw": round(w, 1), "hbm_read_bytes": rb,
+                             "hbm_write_bytes": wb, "traffic_bytes": rb + wb, "algorithmic_bytes": alg,
+                             "traffic_over_algorithmic": round((rb + wb) / alg, 4) if alg else None}
+        ratio = f"{(rb + wb) / alg:.3f}" if alg else "n/a"
+        alg_mb = f"{alg / 1e6:.1f}" if alg else "n/a"
+        rows.append(f"| `{k}` | {f:.0f} | {w:.0f} | {(rb + wb) / 1e6:.1f} | {alg_mb} | {ratio} |")
+    with open(_TRAFFIC_FILE, "w") as f:
+        json.dump(out, f, indent=1)
+    print(f"calibration fetch {cf:.0f} KiB write {cw:.0f} KiB -> factors {ff:.4f} {wf:.4f}")
+    print("\n".join(sorted(rows)))
+
+
 def pmc_sample(dev) -> None:
     """A short, fixed kernel sequence for hardware-counter passes (rocprofv3 --pmc):
     a calibration copy of 1 GiB (known HBM bytes), then 3 launches of the encoder kernel, of
@@ -1175,7 +1243,12 @@ def main() -> int:
     ap.add_argument("--only", choices=["enc", "dec", "dtw", "mel", "step", "fill"], default=None)
     ap.add_argument("--pmc-sample", action="store_true",
                     help="run the short fixed kernel sequence used for rocprofv3 --pmc passes and exit")
+    ap.add_argument("--pmc-table", nargs=2, metavar=("FETCH_CSV", "WRITE_CSV"),
+                    help="summarise two --pmc-sample counter passes into profiles/pmc_traffic.json and exit")
     args = ap.parse_args()
+    if args.pmc_table:
+        pmc_table(*args.pmc_table)
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print(
             "bench.py measures one GPU: the attention hot path shards by independent windows/slots "
