@@ -166,17 +166,17 @@ def test_qkv_attention_helper(cuda):
 
 
 PIPE_SHAPES = [
-    # (B, H, Lq, Lk): grids of >= 256 workgroups of 384 queries route to dense_pipe_kernel;
-    # Lk covers an even / odd number of full 32-key steps, with and without a partial last step,
-    # and the loop's minimum of two tiles
-    (4, 64, 100, 64),
-    (4, 64, 100, 96),
-    (4, 64, 100, 100),
-    (4, 64, 100, 127),
-    (4, 64, 100, 160),
-    (2, 64, 400, 333),
-    (1, 128, 800, 1500),
-    (2, 128, 300, 2001),
+    # (B, H, Lq, Lk): grids of >= 256 items of 384 queries whose last query block is mostly full
+    # route to dense_pipe_kernel; Lk covers an even / odd number of full 32-key steps, with and
+    # without a partial last step, and the loop's minimum of two tiles; Lq partial query blocks
+    (4, 64, 340, 64),
+    (4, 64, 340, 96),
+    (4, 64, 340, 100),
+    (4, 64, 340, 127),
+    (4, 64, 340, 160),
+    (2, 64, 720, 333),
+    (1, 128, 1100, 1500),
+    (2, 128, 350, 2001),
 ]
 
 

@@ -1711,9 +1711,12 @@ hipError_t launch_typed(const DenseArgs& a, hipStream_t stream) {
       split(a, bh);
       return hipGetLastError();
     }
-    // the hand-scheduled 384-query kernel when its grid fills the chip
+    // the hand-scheduled 384-query kernel when its items fill the chip and its query blocks
+    // are mostly full (padding <= 15% of the rows: the encoder's 1500 in 4 x 384; the DTW
+    // decoder's 448 would compute 768 and runs faster on the 512-query kernel + key split)
     const int64_t np = bh * ((a.Lq + kPBM - 1) / kPBM);
-    if (a.Lk >= kPMinKeys && np >= kNumCus && np <= 0x7fffffff) {
+    const bool full = (a.Lq + kPBM - 1) / kPBM * kPBM * 100 <= (int64_t)a.Lq * 115;
+    if (a.Lk >= kPMinKeys && full && np >= kNumCus && np <= 0x7fffffff) {
       // persistent: one workgroup per CU, each taking every 256th item
       hipLaunchKernelGGL((dense_pipe_kernel<T>), dim3((unsigned)kNumCus), dim3(kPThreads), 0, stream, a);
       return hipGetLastError();
