@@ -151,6 +151,10 @@ class Gen:
         # still zero there, and exp2(-delta) = inf would turn them into NaN
         r.append(f"v_min_f32 {vr(al)}, 1.0, {vr(al)}")
         r.append(f"v_mul_f32 {vr(LRUN(b))}, {vr(LRUN(b))}, {vr(al)}")
+        # O is still zero in the forced first step (its floor register is -inf then): no rescale
+        skip = label.replace("R", "N", 1)
+        r.append(f"s_cmp_eq_u32 {S_FLOOR}, 0xff800000")
+        r.append(f"s_cbranch_scc1 {skip}")
         tmp = [RT + 4 + i for i in range(8)]
         for i0 in range(0, 32, 8):
             for i in range(8):
@@ -159,6 +163,7 @@ class Gen:
                 r.append(f"v_mul_f32 {vr(tmp[i])}, {vr(al)}, {vr(tmp[i])}")
             for i in range(8):
                 r.append(f"v_accvgpr_write_b32 {ar(O(b, 0) + i0 + i)}, {vr(tmp[i])}")
+        r.append(f"{skip}:")
         for i in range(16):
             r.append(f"v_sub_f32 {vr(CINIT(b) + i)}, 0, {vr(MRUN(b))}")
         for i in range(16):
