@@ -985,6 +985,14 @@ __device__ __forceinline__ i32x4 buffer_rsrc(const void* base, uint32_t bytes) {
   return r;
 }
 
+// The same resource for the buffer load / store builtins (stores past the end are dropped).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_res(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+
 // Registers the generated loop uses beyond its operands (gen_dense_loop.py has the map).
 #define WDRZ_PIPE_CLOBBERS \
   "v0", "v1", "v2", "v3", "v4", "v5", "v6", "v7", "v8", "v9", "v10", "v11", "v12", "v13", "v14", "v15", \
@@ -1053,15 +1061,16 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
     it.q0 = qblk * kPBM;
     return it;
   };
+  // Global transfers through buffer resources bounded by the tensor (32-bit offsets, no
+  // per-row 64-bit address arithmetic; rows past the end load as zero, stores there are dropped)
+  const uint32_t k_bytes = (uint32_t)((a.Lk - 1) * rs_k + 128), v_bytes = (uint32_t)((a.Lk - 1) * rs_v + 128);
   auto tile_load = [&](const Item& it, int kt, u32x4 (&st)[4]) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t rk = buffer_res(it.k, k_bytes), rv = buffer_res(it.v, v_bytes);
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int r = kt * kBN + crow + 32 * i;
-      const bool in = r < a.Lk;
-      const int rc = in ? r : a.Lk - 1;
-      st[i] = load16(it.k + (int64_t)rc * a.ks[2] + cd0);
-      st[2 + i] = load16(it.v + (int64_t)rc * a.vs[2] + cd0);
-      if (!in) st[i] = st[2 + i] = u32x4{0u, 0u, 0u, 0u};
+      const uint32_t r = (uint32_t)(kt * kBN + crow + 32 * i);
+      st[i] = buf_load16(rk, r * rs_k + cd0 * 2);
+      st[2 + i] = buf_load16(rv, r * rs_v + cd0 * 2);
     }
   };
   auto tile_store = [&](int buf, const u32x4 (&st)[4]) __attribute__((always_inline)) {
@@ -1074,8 +1083,10 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
   // Q rows through registers into the swizzled Q area (the first item; short keys)
   auto q_load_sync = [&](const Item& it) __attribute__((always_inline)) {
     u32x4 qc[kPBM / 32];
+    const __amdgpu_buffer_rsrc_t rq =
+        buffer_res(it.q + (int64_t)it.q0 * a.qs[2], (uint32_t)((min(kPBM, a.Lq - it.q0) - 1) * rs_q + 128));
 #pragma unroll
-    for (int i = 0; i < kPBM / 32; ++i) qc[i] = load16(it.q + min(it.q0 + crow + 32 * i, a.Lq - 1) * a.qs[2] + cd0);
+    for (int i = 0; i < kPBM / 32; ++i) qc[i] = buf_load16(rq, (uint32_t)(crow + 32 * i) * rs_q + cd0 * 2);
 #pragma unroll
     for (int i = 0; i < kPBM / 32; ++i) {
       const int row = crow + 32 * i;
@@ -1190,12 +1201,15 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
         }
     }
     __syncthreads();
+    const int rs_o = (int)a.os[2] * 2;
+    const __amdgpu_buffer_rsrc_t ro =
+        buffer_res(cur.o + (int64_t)cur.q0 * a.os[2], (uint32_t)((min(kPBM, a.Lq - cur.q0) - 1) * rs_o + 128));
 #pragma unroll
-    for (int i = 0; i < kPBM / 32; ++i) {
-      const int qi = cur.q0 + crow + 32 * i;
-      if (qi < a.Lq)
-        store16(cur.o + qi * a.os[2] + cd0, *reinterpret_cast<const u32x4*>(&tiles[(crow + 32 * i) * kPitchK + cd0]));
-    }
+    for (int i = 0; i < kPBM / 32; ++i)
+      __builtin_amdgcn_raw_buffer_store_b128(
+          __builtin_bit_cast(__attribute__((ext_vector_type(4))) unsigned int,
+                             *reinterpret_cast<const u32x4*>(&tiles[(crow + 32 * i) * kPitchK + cd0])),
+          ro, (uint32_t)(crow + 32 * i) * rs_o + cd0 * 2, 0, 0);
     if (!has_next) break;
     if (npf == 0) q_load_sync(nxt);  // (too few iterations to request it during the loop)
     id = next_id;
@@ -1716,7 +1730,11 @@ hipError_t launch_typed(const DenseArgs& a, hipStream_t stream) {
     // decoder's 448 would compute 768 and runs faster on the 512-query kernel + key split)
     const int64_t np = bh * ((a.Lq + kPBM - 1) / kPBM);
     const bool full = (a.Lq + kPBM - 1) / kPBM * kPBM * 100 <= (int64_t)a.Lq * 115;
-    if (a.Lk >= kPMinKeys && full && np >= kNumCus && np <= 0x7fffffff) {
+    // its global transfers use 32-bit byte offsets within one head's rows
+    const int64_t lim = 0x7fffffff;
+    const bool offs32 = (int64_t)a.Lk * a.ks[2] * 2 < lim && (int64_t)a.Lk * a.vs[2] * 2 < lim &&
+                        (int64_t)a.Lq * a.qs[2] * 2 < lim && (int64_t)a.Lq * a.os[2] * 2 < lim;
+    if (a.Lk >= kPMinKeys && full && offs32 && np >= kNumCus && np <= 0x7fffffff) {
       // persistent: one workgroup per CU, each taking every 256th item
       hipLaunchKernelGGL((dense_pipe_kernel<T>), dim3((unsigned)kNumCus), dim3(kPThreads), 0, stream, a);
       return hipGetLastError();
