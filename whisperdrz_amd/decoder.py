@@ -130,13 +130,16 @@ class MultiHeadAttention(nn.Module):
                            project_out: bool = True) -> Tensor:
         """``forward_flash`` with the step's metadata computed once by the caller (the gathered
         ``cache_seqlens`` and the int32 slot map) and, for self-attention, the query / key /
-        value projections as one GEMM (``decode_ops.linear`` when K % 128 == 0). Same arithmetic
-        per output element. ``project_out=False`` returns the attention output before ``out``
-        (the caller applies it, fused with the residual add)."""
+        value projections as one GEMM (``decode_ops.linear`` when K % 128 == 0, as is the
+        cross-attention's query projection). Same arithmetic per output element.
+        ``project_out=False`` returns the attention output before ``out`` (the caller applies it,
+        fused with the residual add)."""
         B, seq_len, _ = x.shape
         d = self.n_state // self.n_head
         if is_cross_attn:
-            q = self.query(x).view(B, seq_len, self.n_head, d)
+            # the query projection on the same 64-row kernel as the others (K % 128 == 0)
+            q = linear(x, self.query.weight, self.query.bias) if self.n_state % 128 == 0 else self.query(x)
+            q = q.view(B, seq_len, self.n_head, d)
             o = self.attn_kvcache(q, kv_cache.k_cache, kv_cache.v_cache, cache_batch_idx=batch_idx,
                                   softmax_scale=d ** -0.5, causal=False)
         else:
