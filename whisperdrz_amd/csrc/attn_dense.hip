@@ -963,7 +963,7 @@ __global__ __launch_bounds__(kFThreads, 1) void dense_fwd_kernel(DenseArgs a) {
 constexpr int kPWaves = 4;
 constexpr int kPThreads = kPWaves * 64;
 constexpr int kPBM = 96 * kPWaves;  // queries per workgroup
-constexpr int kPTile = kBN * kPitchK;  // elements of one 64-key tile buffer
+constexpr int kPTile = kBN * 64;  // elements of one 64-key tile buffer (unpadded 128-byte rows, swizzled)
 constexpr int kPMinKeys = 64;         // the loop needs two tiles up front
 constexpr int kPQElems = kPBM * 64;   // the Q area: 384 rows of 64 elements (no pad; chunks swizzled)
 constexpr int kPQPieces = kPBM * 128 / kPThreads / 16;  // 1 KB prefetch pieces per wavefront (12)
@@ -1004,19 +1004,17 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
   "v91", "v92", "v93", "v94", "v95", "v96", "v97", "v98", "v99", "v100", "v101", "v102", "v103", "v104", \
   "v105", "v106", "v107", "v108", "v109", "v110", "v111", "v112", "v113", "v114", "v115", "v116", "v117", \
   "v118", "v119", "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127", "v128", "v129", "v130", \
-  "v131", "v132", "v133", "v134", "v135", "v136", "v137", "v138", "v139", "v140", "v141", "v142", "v143", \
-  "v144", "v145", "v146", "v147", "v148", "v149", "v150", "v151", "v152", "v153", "v154", "v155", "v159", \
+  "v131", "v132", "v133", "v134", "v135", "v148", "v149", "v150", "v151", "v152", "v153", "v154", "v159", \
   "v168", "v169", "v170", "v171", "v172", "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180", \
   "v181", "v182", "v183", "v184", "v185", "v186", "v187", "v188", "v189", "v190", "v191", "v192", "v193", \
   "v194", "v195", "v196", "v197", "v198", "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", \
-  "v207", "v208", "v209", "v210", "v211", "v212", "v213", "v214", "v215", "v216", "v217", "v218", "v219", \
-  "v220", "v221", "v222", "v223", "v225", "a144", "a145", "a146", "a147", "a148", "a149", "a150", "a151", \
-  "a152", "a153", "a154", "a155", "a156", "a157", "a158", "a159", "a160", "a161", "a162", "a163", "a164", \
-  "a165", "a166", "a167", "a168", "a169", "a170", "a171", "a172", "a173", "a174", "a175", "a176", "a177", \
-  "a178", "a179", "a180", "a181", "a182", "a183", "a184", "a185", "a186", "a187", "a188", "a189", "a190", \
-  "a191", "a192", "a193", "a194", "a195", "a196", "a197", "a198", "a199", "a200", "a201", "a202", "a203", \
-  "a204", "a205", "a206", "a207", "s70", "s71", "s72", "s73", "s74", "s75", "s76", "s77", "s78", "s79", "m0", \
-  "vcc", "scc", "memory"
+  "v207", "v208", "v209", "v210", "v211", "v212", "v213", "v214", "v215", "v225", "a144", "a145", "a146", \
+  "a147", "a148", "a149", "a150", "a151", "a152", "a153", "a154", "a155", "a156", "a157", "a158", "a159", \
+  "a160", "a161", "a162", "a163", "a164", "a165", "a166", "a167", "a168", "a169", "a170", "a171", "a172", \
+  "a173", "a174", "a175", "a176", "a177", "a178", "a179", "a180", "a181", "a182", "a183", "a184", "a185", \
+  "a186", "a187", "a188", "a189", "a190", "a191", "a192", "a193", "a194", "a195", "a196", "a197", "a198", \
+  "a199", "a200", "a201", "a202", "a203", "a204", "a205", "a206", "a207", "s70", "s71", "s72", "s73", "s74", \
+  "s75", "s76", "s77", "s78", "s79", "m0", "vcc", "scc", "memory"
 
 template <typename T>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void dense_pipe_kernel(DenseArgs a) {
@@ -1041,7 +1039,6 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
   // Row-contiguous transfers: thread tid moves 16-byte chunk (tid & 7) of rows tid/8 + 32*i.
   const int crow = tid >> 3, cd0 = (tid & 7) * 8;
   const int rs_k = (int)a.ks[2] * 2, rs_v = (int)a.vs[2] * 2, rs_q = (int)a.qs[2] * 2;  // row strides, bytes
-  const int st_off = crow * kPitchK + cd0;  // elements
 
   // The per-item pointers: item id (dispatch order) -> (b, h, query block), XCD-aware.
   struct Item {
@@ -1073,11 +1070,15 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
       st[2 + i] = buf_load16(rv, r * rs_v + cd0 * 2);
     }
   };
+  // tile layout: chunk c (16 bytes) of row r at element 64 r + 8 (c ^ ((r >> 1) & 7)) (the
+  // operand reads of 16 lanes then touch 16 distinct 16-byte bank groups)
   auto tile_store = [&](int buf, const u32x4 (&st)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      *reinterpret_cast<u32x4*>(&tiles[buf * kPTile + st_off + 32 * i * kPitchK]) = st[i];
-      *reinterpret_cast<u32x4*>(&tiles[(4 + buf) * kPTile + st_off + 32 * i * kPitchK]) = st[2 + i];
+      const int row = crow + 32 * i;
+      const int off = row * 64 + (((tid & 7) ^ ((row >> 1) & 7)) << 3);
+      *reinterpret_cast<u32x4*>(&tiles[buf * kPTile + off]) = st[i];
+      *reinterpret_cast<u32x4*>(&tiles[(4 + buf) * kPTile + off]) = st[2 + i];
     }
   };
   // Q rows through registers into the swizzled Q area (the first item; short keys)
@@ -1102,17 +1103,33 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
   // the next item's Q rows are requested by the loop code (one 1 KB piece per wavefront and
   // iteration) when the loop has the iterations for it
   const int n_pf = n_iter >= kPQPieces ? kPQPieces : 0;
-  // LDS byte offsets of this lane's operand reads (the permuted K rows; V^T through the
-  // transposing read), and of its tile stores
+  // LDS byte offsets of this lane's operand reads in the swizzled tiles: the permuted K rows,
+  // one base per 16-key chunk ks; V^T through the transposing read, one base per 32-dim half db
+  // and 4-row offset s (their chunk positions differ)
   const int pm = l32;
   const int pi_row = 16 * ((pm >> 3) >> 1) + 8 * ((pm >> 2) & 1) + 4 * ((pm >> 3) & 1) + (pm & 3);
   const int g16 = lane >> 4, j16 = lane & 15;
   const uint32_t tbase = kPQElems * 2;  // byte offset of the tile buffers
-  u32x4 lanes;
-  lanes[0] = tbase + (uint32_t)(pi_row * kPitchK + hl * 8) * 2;  // K reads
-  lanes[1] = tbase + (uint32_t)((8 * (g16 >> 1) + (j16 >> 2)) * kPitchK + 16 * (g16 & 1) + 4 * (j16 & 3)) * 2;
-  lanes[2] = tbase + (uint32_t)st_off * 2;  // tile stores
-  lanes[3] = 8 * hl;                        // key offset of this lane half (masking)
+  u32x4 kl;
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) kl[ks] = tbase + pi_row * 128 + (((2 * ks + hl) ^ ((pi_row >> 1) & 7)) << 4);
+  typedef uint32_t u32x8v __attribute__((ext_vector_type(8)));
+  u32x8v vl;
+#pragma unroll
+  for (int db = 0; db < 2; ++db)
+#pragma unroll
+    for (int sr = 0; sr < 2; ++sr) {
+      const int r = 8 * (g16 >> 1) + (j16 >> 2) + 4 * sr;
+      const int cc = 2 * (g16 & 1) + ((j16 & 3) >> 1) + 4 * db;
+      vl[2 * db + sr] = tbase + r * 128 + ((cc ^ ((r >> 1) & 7)) << 4) + 8 * (j16 & 1);
+    }
+  const uint32_t hl8 = 8 * hl;  // key offset of this lane half (masking)
+  // the loop's LDS DMA: wavefront w requests rows 16 w .. 16 w + 15 of each K and V tile in two
+  // 8-row pieces, lane l writing position l % 8 of row l / 8 of a piece and so fetching the
+  // global chunk the swizzle puts there
+  const int dmab = __builtin_amdgcn_readfirstlane(tbase + wave * 16 * 128);
+  const uint32_t swz0 = (uint32_t)(((lane & 7) ^ (lane >> 4)) << 4);        // rows 16 w + l / 8
+  const uint32_t swz1 = (uint32_t)(((lane & 7) ^ (4 + (lane >> 4))) << 4);  // rows 16 w + 8 + l / 8
   const int tsk = kBN * rs_k, tsv = kBN * rs_v;
   // the Q prefetch: this lane's piece of row 8j + lane/8 of its wavefront's 96, swizzled chunk
   const uint32_t qvoff = (uint32_t)((wave * 96 + (lane >> 3)) * rs_q + (((lane & 7) ^ (lane >> 3)) << 4));
@@ -1155,21 +1172,22 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
     const int nq_next = min(kPBM, a.Lq - nxt.q0);
     const i32x4 srd_q = buffer_rsrc(nxt.q + (int64_t)nxt.q0 * a.qs[2], (uint32_t)((nq_next - 1) * rs_q + 128));
     const int npf = has_next ? n_pf : 0;
-    // global byte offsets of this thread's rows in tile 2 (the first the loop code requests)
+    // global byte offsets of this lane's rows of tile 2 (the first the loop code requests)
     u32x4 voff;
-    voff[0] = (2 * kBN + crow) * rs_k + cd0 * 2;
-    voff[1] = voff[0] + 32 * rs_k;
-    voff[2] = (2 * kBN + crow) * rs_v + cd0 * 2;
-    voff[3] = voff[2] + 32 * rs_v;
+    voff[0] = (2 * kBN + wave * 16 + (lane >> 3)) * rs_k + swz0;
+    voff[1] = (2 * kBN + wave * 16 + 8 + (lane >> 3)) * rs_k + swz1;
+    voff[2] = (2 * kBN + wave * 16 + (lane >> 3)) * rs_v + swz0;
+    voff[3] = (2 * kBN + wave * 16 + 8 + (lane >> 3)) * rs_v + swz1;
     f32x16 acc_o[3][2];
     typedef float f32x3 __attribute__((ext_vector_type(3)));
     f32x3 lr;  // this lane's half of each block's row sum
 #define WDRZ_PIPE_OPERANDS                                                                                    \
   : "={a[0:15]}"(acc_o[0][0]), "={a[16:31]}"(acc_o[0][1]), "={a[32:47]}"(acc_o[1][0]), "={a[48:63]}"(acc_o[1][1]), \
     "={a[64:79]}"(acc_o[2][0]), "={a[80:95]}"(acc_o[2][1]), "={v[156:158]}"(lr), "+{v[164:167]}"(voff)             \
-  : "{a[96:111]}"(q0), "{a[112:127]}"(q1), "{a[128:143]}"(q2), "{v[160:163]}"(lanes), "{v224}"(qvoff),            \
-    "{s[80:83]}"(srd_k), "{s[84:87]}"(srd_v), "{s[88:91]}"(srd_q), [n] "s"(n_iter), [r] "s"(n_rest),                \
-    [rem] "s"(rem), [tsk] "s"(tsk), [tsv] "s"(tsv), [npf] "s"(npf), [qlds] "s"(qlds), [qstep] "s"(qstep)          \
+  : "{a[96:111]}"(q0), "{a[112:127]}"(q1), "{a[128:143]}"(q2), "{v[136:139]}"(kl), "{v[140:147]}"(vl),              \
+    "{v163}"(hl8), "{v224}"(qvoff), "{s[80:83]}"(srd_k), "{s[84:87]}"(srd_v), "{s[88:91]}"(srd_q), [n] "s"(n_iter),  \
+    [r] "s"(n_rest), [rem] "s"(rem), [tsk] "s"(tsk), [tsv] "s"(tsv), [npf] "s"(npf), [qlds] "s"(qlds),               \
+    [qstep] "s"(qstep), [dmab] "s"(dmab)                                                                          \
   : WDRZ_PIPE_CLOBBERS
     __builtin_amdgcn_sched_barrier(0);
     if constexpr (__is_same(T, Bf16))

@@ -23,22 +23,23 @@ wavefront as three 32-query blocks b = 0, 1, 2; 32 keys per step, 64-key LDS til
     written stalls the in-order wavefront).
   * K and V operands for the MFMAs come from LDS one step ahead into double-buffered AGPRs
     (K through ds_read_b128 in the permuted key order that makes P^T the B operand without
-    shuffles; V^T through ds_read_b64_tr_b16). Tiles of 64 keys are staged global -> VGPR ->
-    LDS through four LDS buffers: tile t+2 is written and tile t+4 requested during tile t
-    (two register sets), one workgroup barrier per tile. Global loads are buffer loads bounded by the tensor's extent
-    (rows past the last key read as zero; those keys are never used unmasked).
+    shuffles; V^T through ds_read_b64_tr_b16). Tiles of 64 keys go global -> LDS directly (buffer
+    loads to LDS, 1 KB = 8 rows per instruction) through four LDS buffers of unpadded 128-byte rows
+    whose 16-byte chunks are XOR-swizzled by (row / 2) % 8 (a lane fetches the global chunk that
+    the swizzle puts at its LDS position); tile t+3 is requested during tile t and tile t+2 must have
+    landed by tile t's barrier (one workgroup barrier per tile). The loads are bounded by the
+    tensor's extent (rows past the last key read as zero; those keys are never used unmasked).
   * The kernel is persistent; during the first 12 iterations of an item each wavefront also
     requests one 1 KB piece of the next item's Q rows straight into LDS (buffer loads to LDS).
 
 Register map (the kernel passes these through "{v[..]}" / "{a[..]}" constraints):
   v0-47 S[b] (16 each)   v48-95 cinit[b]   v96-119 P[b] (8 each: two 16-key chunks)
-  v120-135 exp temps     v136-151 tile staging (K rows r, r+32, V rows r, r+32)
-  v152-154 m_run[b]      v155 tail V address   v156-158 l_run[b] (this lane's half of the row sum)
-  v159 -inf
-  v160-163 lane bases: K read, V read, tile store, 8 * (lane >> 5)
-  v164-167 global row offsets (K r, K r+32, V r, V r+32)   v168-171 per-tile addresses
+  v120-135 exp temps     v136-139 K read lane bases   v140-147 V^T read lane bases   v148-151 K reads
+  v152-154 m_run[b]      v156-158 l_run[b] (this lane's half of the row sum)   v159 -inf
+  v163 8 * (lane >> 5)   v164-167 global byte offsets of this lane's tile rows (K r, r+8, V r, r+8)
+  v168-171 V^T reads of tile t
   v172-183 rare-path temporaries   v184-207 row-sum temporaries (8 per block)
-  v208-223 second tile staging set   v224 Q prefetch lane offset   v225 its address
+  v208-211 V^T reads of tile t+1   v212-215 the tail's   v224 Q prefetch lane offset   v225 its address
   a0-95 O[b][db] (16 each)   a96-143 Q[b][ks] (4 each)   a144-175 K buffers (2 x 16)
   a176-207 V buffers (2 x 16: [ch][db] operands of 4)
   s70-s79 loop state (clobbered: iteration, tile offsets, sum limit, rescale floor); the kernel
@@ -52,17 +53,19 @@ def S(b): return 16 * b
 def CINIT(b): return 48 + 16 * b
 def P(b, ch=0): return 96 + 8 * b + 4 * ch
 T0 = 120
-STAGE = 136
-STAGE2 = 208  # the second staging set (208..223)
+KL = 136   # 136..139 K read lane bases, one per 16-key chunk ks (the layout is XOR-swizzled)
+VL = 140   # 140..147 V^T read lane bases [db][s]: dims 32 db.., rows +4 s
 QVOFF, QV = 224, 225  # the Q prefetch: this lane's row offset, and the piece's address
 def U(b): return 184 + 8 * b  # row-sum temporaries of block b (184..207)
 def MRUN(b): return 152 + b
 def LRUN(b): return 156 + b  # a 3-register tuple (even-aligned), an output of the loop
-KLANE, VLANE, STLANE, HL8 = 160, 161, 162, 163  # HL8: 8 * (lane >> 5), the masking's key offset
-VOFF = 164  # 164..167 (a 4-register tuple: even-aligned)
-KADDR, VADDRA, VADDRB, STADDR = 168, 169, 170, 171
+HL8 = 163  # 8 * (lane >> 5), the masking's key offset
+VOFF = 164  # 164..167 global byte offsets of this lane's tile rows (K r, K r+8, V r, V r+8)
+KADDR = 148   # 148..151 the K read addresses of an iteration (per ks)
+VADDRA = 168  # 168..171 the V^T read addresses of tile t ([db][s])
+VADDRB = 208  # 208..211 the same for tile t+1
+VADDRT = 212  # 212..215 the same for the tail
 RT = 172  # rare-path temporaries 172..183
-VADDRT = 155  # the tail's V read address
 NEGINF = 159  # -inf (the masked score)
 def O(b, db): return 32 * b + 16 * db
 def Q(b, ks): return 96 + 16 * b + 4 * ks
@@ -74,8 +77,9 @@ S_IT, S_BUFA, S_BUFB, S_BUFC, S_TMP = "s70", "s71", "s72", "s73", "s74"
 S_LIMIT, S_FLOOR = "s76", "s78"
 SRD_K, SRD_V, SRD_Q = "s[80:83]", "s[84:87]", "s[88:91]"
 
-TILE_BYTES = 64 * 72 * 2   # one 64-key tile of K (or V): 64 rows x 72 elements (16-byte pad)
-HALF_BYTES = 32 * 72 * 2   # 32 key rows
+TILE_BYTES = 64 * 128      # one 64-key tile of K (or V): 64 rows of 128 bytes, 16-byte chunks
+HALF_BYTES = 32 * 128      # XOR-swizzled (chunk c of row r at byte 16 (c ^ ((r >> 1) & 7)))
+ROW_BYTES = 128
 V_BASE = 4 * TILE_BYTES    # the V tiles follow the four K tiles
 SUM_LIMIT = "0x44800000"   # 1024.0f
 
@@ -228,40 +232,32 @@ class Gen:
 
     def k_reads(self, p):
         """K(s+2) -> K buffer p: tile t+1, half p (base KADDR)."""
-        return [f"ds_read_b128 {ar(KB(p, ks), 4)}, {vr(KADDR)} offset:{p * HALF_BYTES + ks * 32}" for ks in range(4)]
+        return [f"ds_read_b128 {ar(KB(p, ks), 4)}, {vr(KADDR + ks)} offset:{p * HALF_BYTES}" for ks in range(4)]
 
-    def v_reads(self, p):
+    def v_reads(self, p, base=None):
         """V(s+1) -> V buffer 1-p: step 2t: tile t half 1 (VADDRA); step 2t+1: tile t+1 half 0 (VADDRB)."""
-        base, half = (VADDRA, 1) if p == 0 else (VADDRB, 0)
+        b0, half = (VADDRA, 1) if p == 0 else (VADDRB, 0)
+        base = b0 if base is None else base
         out = []
         for ch in range(2):
             for db in range(2):
-                off = V_BASE + half * HALF_BYTES + ch * 16 * 144 + db * 64
+                off = V_BASE + half * HALF_BYTES + ch * 16 * ROW_BYTES
                 dst = VB(1 - p, ch, db)
-                out.append(f"ds_read_b64_tr_b16 {ar(dst, 2)}, {vr(base)} offset:{off}")
-                out.append(f"ds_read_b64_tr_b16 {ar(dst + 2, 2)}, {vr(base)} offset:{off + 4 * 144}")
+                out.append(f"ds_read_b64_tr_b16 {ar(dst, 2)}, {vr(base + 2 * db)} offset:{off}")
+                out.append(f"ds_read_b64_tr_b16 {ar(dst + 2, 2)}, {vr(base + 2 * db + 1)} offset:{off}")
         return out
 
-    def staging(self, stage):
-        """Tile t+2 from staging registers `stage` into LDS; tile t+4 requested into them. The two
-        register sets alternate by iteration, so a tile's loads have two iterations to land: the
-        wait leaves the other set's four loads in flight."""
-        w = [
-            "s_waitcnt vmcnt(4)",
-            f"ds_write_b128 {vr(STADDR)}, {vr(stage, 4)}",
-            f"ds_write_b128 {vr(STADDR)}, {vr(stage + 4, 4)} offset:{HALF_BYTES}",
-            f"ds_write_b128 {vr(STADDR)}, {vr(stage + 8, 4)} offset:{V_BASE}",
-            f"ds_write_b128 {vr(STADDR)}, {vr(stage + 12, 4)} offset:{V_BASE + HALF_BYTES}",
-        ]
-        return w, self.tile_loads(stage), self.advance()
-
-    def tile_loads(self, stage):
-        return [
-            f"buffer_load_dwordx4 {vr(stage, 4)}, {vr(VOFF)}, {SRD_K}, 0 offen",
-            f"buffer_load_dwordx4 {vr(stage + 4, 4)}, {vr(VOFF + 1)}, {SRD_K}, 0 offen",
-            f"buffer_load_dwordx4 {vr(stage + 8, 4)}, {vr(VOFF + 2)}, {SRD_V}, 0 offen",
-            f"buffer_load_dwordx4 {vr(stage + 12, 4)}, {vr(VOFF + 3)}, {SRD_V}, 0 offen",
-        ]
+    def tile_dma(self):
+        """This wavefront's 16 rows of K and of V of one tile (four 1 KB pieces of 8 rows) straight
+        into the LDS buffer at S_BUFC (LDS DMA at m0): lane l fetches the global chunk that the
+        swizzle puts at position l % 8 of row l / 8 (the C++ side sets VOFF so)."""
+        out = [f"s_add_u32 {S_TMP}, {S_BUFC}, %[dmab]"]
+        for i, (srd, off) in enumerate(((SRD_K, 0), (SRD_K, 8 * ROW_BYTES), (SRD_V, V_BASE),
+                                         (SRD_V, V_BASE + 8 * ROW_BYTES))):
+            out.append(f"s_add_u32 m0, {S_TMP}, {off}" if off else f"s_mov_b32 m0, {S_TMP}")
+            out.append("s_nop 0")
+            out.append(f"buffer_load_dwordx4 {vr(VOFF + i)}, {srd}, 0 offen lds")
+        return out
 
     def advance(self):
         return [
@@ -271,22 +267,25 @@ class Gen:
             f"v_add_u32 {vr(VOFF + 3)}, %[tsv], {vr(VOFF + 3)}",
         ]
 
-    def iteration(self, stage, it):
-        """One tile: steps 2t and 2t+1, with tile t+2 staged from `stage` and tile t+4 requested."""
+    def iteration(self, it):
+        """One tile t: steps 2t and 2t+1, with tile t+3 requested (LDS DMA) into the buffer that
+        tile t-1 held; tile t+2 (requested during tile t-1) must have landed by the barrier."""
         e = self.emit
         e(f"s_and_b32 {S_TMP}, {S_IT}, 3")
         e(f"s_mul_i32 {S_BUFA}, {S_TMP}, {TILE_BYTES}")
         e(f"s_add_u32 {S_TMP}, {S_IT}, 1")
         e(f"s_and_b32 {S_TMP}, {S_TMP}, 3")
         e(f"s_mul_i32 {S_BUFB}, {S_TMP}, {TILE_BYTES}")
-        e(f"s_add_u32 {S_TMP}, {S_IT}, 2")
+        e(f"s_add_u32 {S_TMP}, {S_IT}, 3")
         e(f"s_and_b32 {S_TMP}, {S_TMP}, 3")
         e(f"s_mul_i32 {S_BUFC}, {S_TMP}, {TILE_BYTES}")
-        e(f"v_add_u32 {vr(KADDR)}, {S_BUFB}, {vr(KLANE)}")
-        e(f"v_add_u32 {vr(VADDRA)}, {S_BUFA}, {vr(VLANE)}")
-        e(f"v_add_u32 {vr(VADDRB)}, {S_BUFB}, {vr(VLANE)}")
-        e(f"v_add_u32 {vr(STADDR)}, {S_BUFC}, {vr(STLANE)}")
-        w, ld, adv = self.staging(stage)
+        for i in range(4):
+            e(f"v_add_u32 {vr(KADDR + i)}, {S_BUFB}, {vr(KL + i)}")
+        for i in range(4):
+            e(f"v_add_u32 {vr(VADDRA + i)}, {S_BUFA}, {vr(VL + i)}")
+        for i in range(4):
+            e(f"v_add_u32 {vr(VADDRB + i)}, {S_BUFB}, {vr(VL + i)}")
+        ld, adv = self.tile_dma(), self.advance()
         kr0, vr0 = self.k_reads(0), self.v_reads(0)
         kr1, vr1 = self.k_reads(1), self.v_reads(1)
         # step 2t (parity 0)
@@ -297,8 +296,8 @@ class Gen:
         e(f"s_mov_b32 {S_LIMIT}, {SUM_LIMIT}")
         e(f"s_mov_b32 {S_FLOOR}, 0")
         # the next item's Q rows: piece S_IT of this wavefront's 12 (1 KB each), straight into
-        # the Q area (LDS DMA at m0), requested before the tile loads so that the staging waits
-        # (vmcnt(4)) keep their meaning
+        # the Q area (LDS DMA at m0), requested before the tile's pieces so that the wait at the
+        # barrier (vmcnt(4)) leaves exactly those in flight
         pf = [
             f"s_cmp_lt_u32 {S_IT}, %[npf]",
             f"s_cbranch_scc0 LNQ{it}_%=",
@@ -311,10 +310,10 @@ class Gen:
             f"buffer_load_dwordx4 {vr(QV)}, {SRD_Q}, 0 offen lds",
             f"LNQ{it}_%=:",
         ]
-        self.phase(1, 0, f"0P1{it}", pre=[w[0]], slots={0: w[1:], 1: pf + ld, 2: adv})
+        self.phase(1, 0, f"0P1{it}", slots={1: pf + ld, 2: adv})
         self.phase(1, 1, f"1P1{it}", pre=["s_waitcnt lgkmcnt(0)"], slots={3: kr1[:2], 4: kr1[2:]})
         self.phase(1, 2, f"2P1{it}", slots={1: vr1[0:2], 2: vr1[2:4], 3: vr1[4:6], 4: vr1[6:8]})
-        e("s_waitcnt lgkmcnt(0)")
+        e("s_waitcnt vmcnt(4) lgkmcnt(0)")  # tile t+2 in LDS (and this wavefront's reads done)
         e("s_barrier")
         e(f"s_add_u32 {S_IT}, {S_IT}, 1")
 
@@ -322,13 +321,13 @@ class Gen:
         e = self.emit
         # ---- prologue: first operands, zero state, scores of step 0 for blocks 0 and 1 ----
         for ks in range(4):
-            e(f"ds_read_b128 {ar(KB(0, ks), 4)}, {vr(KLANE)} offset:{ks * 32}")
-            e(f"ds_read_b128 {ar(KB(1, ks), 4)}, {vr(KLANE)} offset:{HALF_BYTES + ks * 32}")
+            e(f"ds_read_b128 {ar(KB(0, ks), 4)}, {vr(KL + ks)}")
+            e(f"ds_read_b128 {ar(KB(1, ks), 4)}, {vr(KL + ks)} offset:{HALF_BYTES}")
         for ch in range(2):
             for db in range(2):
-                off = V_BASE + ch * 16 * 144 + db * 64
-                e(f"ds_read_b64_tr_b16 {ar(VB(0, ch, db), 2)}, {vr(VLANE)} offset:{off}")
-                e(f"ds_read_b64_tr_b16 {ar(VB(0, ch, db) + 2, 2)}, {vr(VLANE)} offset:{off + 4 * 144}")
+                off = V_BASE + ch * 16 * ROW_BYTES
+                e(f"ds_read_b64_tr_b16 {ar(VB(0, ch, db), 2)}, {vr(VL + 2 * db)} offset:{off}")
+                e(f"ds_read_b64_tr_b16 {ar(VB(0, ch, db) + 2, 2)}, {vr(VL + 2 * db + 1)} offset:{off}")
         for i in range(16):
             e(f"v_accvgpr_write_b32 {ar(VB(1, 0, 0) + i)}, 0")
         for i in range(8):
@@ -345,7 +344,9 @@ class Gen:
             for ks in range(4):
                 c = "0" if ks == 0 else vr(S(b), 16)
                 e(f"{self.mfma} {vr(S(b), 16)}, {ar(KB(0, ks), 4)}, {ar(Q(b, ks), 4)}, {c}")
-        for x in self.tile_loads(STAGE) + self.advance() + self.tile_loads(STAGE2) + self.advance():
+        # tile 2 requested (tile t+3 is requested during tile t)
+        e(f"s_mov_b32 {S_BUFC}, {2 * TILE_BYTES}")
+        for x in self.tile_dma() + self.advance():
             e(x)
         e(f"v_mov_b32 {vr(NEGINF)}, 0xff800000")
         e(f"s_mov_b32 {S_LIMIT}, -1.0")
@@ -353,12 +354,12 @@ class Gen:
         e(f"s_mov_b32 {S_IT}, 0")
         e("s_cmp_eq_u32 %[n], 0")
         e("s_cbranch_scc1 LEND_%=")
-        # ---- loop over tiles, two per trip (the staging register sets alternate) ----
+        # ---- loop over tiles, two per trip ----
         e("LLOOP_%=:")
-        self.iteration(STAGE, "A")
+        self.iteration("A")
         e(f"s_cmp_ge_u32 {S_IT}, %[n]")
         e("s_cbranch_scc1 LEND_%=")
-        self.iteration(STAGE2, "B")
+        self.iteration("B")
         e(f"s_cmp_lt_u32 {S_IT}, %[n]")
         e("s_cbranch_scc1 LLOOP_%=")
         e("LEND_%=:")
@@ -373,8 +374,9 @@ class Gen:
         # r = 2: step s_end (full), then step s_end + 1 (masked); V(s_end + 1) -> V buffer 1
         e(f"s_and_b32 {S_TMP}, {S_IT}, 3")
         e(f"s_mul_i32 {S_TMP}, {S_TMP}, {TILE_BYTES}")
-        e(f"v_add_u32 {vr(VADDRT)}, {S_TMP}, {vr(VLANE)}")
-        tvr = [x.replace(vr(VADDRA), vr(VADDRT)) for x in self.v_reads(0)]
+        for i in range(4):
+            e(f"v_add_u32 {vr(VADDRT + i)}, {S_TMP}, {vr(VL + i)}")
+        tvr = self.v_reads(0, base=VADDRT)
         self.phase(0, 0, "0T2")
         self.phase(0, 1, "1T2", pre=["s_waitcnt lgkmcnt(0)"])
         self.phase(0, 2, "2T2", slots={1: tvr[0:2], 2: tvr[2:4], 3: tvr[4:6], 4: tvr[6:8]})
