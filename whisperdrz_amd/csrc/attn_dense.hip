@@ -145,7 +145,10 @@ __global__ __launch_bounds__(NW * 64) void dense_mfma_kernel(DenseArgs a) {
   e_t* O = reinterpret_cast<e_t*>(a.o) + b * a.os[0] + h * a.os[1];
 
   const int q_wg = qblk * kBM;
-  const int q_wave = q_wg + wave * 32 * QB;
+  // Causal: the two wavefronts that share a SIMD (w and w + 4) take query blocks s and 7 - s, so
+  // every SIMD gets the same number of key steps under the mask (1 + 8, 2 + 7, ...)
+  const int wblk = (CAUSAL && NW == 8) ? (wave < 4 ? wave : 11 - wave) : wave;
+  const int q_wave = q_wg + wblk * 32 * QB;
   const float c = a.c;
 
   // Q operand (B of S^T = K Q^T), pre-scaled by c: lane holds query q_wave + qb*32 + l32,
