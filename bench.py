@@ -554,7 +554,7 @@ def bench_dtw_decoder_attention(dev, steps: int, warmup: int) -> dict:
         "causal_self_us_per_layer": round(us_self, 2),
         "causal_self_roofline": roof(t_self, "dense_mfma_kernel<Bf16, true>"),
         "cross_us_per_layer": round(us_cross, 2),
-        "cross_roofline": roof(t_cross, "dense_fwd_kernel<Bf16> (256 heads) + dense_split4_kernel<Bf16> (64 heads)"),
+        "cross_roofline": roof(t_cross, "dense_pipe_kernel<Bf16, 2> (256-query items)"),
     }
 
 

@@ -177,13 +177,20 @@ PIPE_SHAPES = [
     (2, 64, 720, 333),
     (1, 128, 1100, 1500),
     (2, 128, 350, 2001),
+    # 256-query items (two 32-query blocks per wavefront): query counts that 384 would pad by
+    # more than 15% (the DTW decoder's 448 x 1500 cross pass, a prompt's 224)
+    (2, 80, 448, 64),
+    (2, 80, 448, 127),
+    (2, 80, 448, 1500),
+    (4, 64, 224, 333),
+    (1, 128, 480, 160),
 ]
 
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("B,H,Lq,Lk", PIPE_SHAPES)
 def test_pipe_kernel_shapes(cuda, dtype, B, H, Lq, Lk):
-    """The hand-scheduled 384-query kernel on every head against a float64 evaluation on the
+    """The hand-scheduled kernel (384- and 256-query items) on every head against a float64 evaluation on the
     device, and a few heads against the float64 numpy oracle; 2e-2 max-abs."""
     print(f"pipe dtype={dtype} B={B} H={H} Lq={Lq} Lk={Lk}", flush=True)
     from whisperdrz_amd import scaled_dot_product_attention
@@ -207,8 +214,9 @@ def test_pipe_kernel_shapes(cuda, dtype, B, H, Lq, Lk):
         assert_close(out[b : b + 1, h : h + 1], ref, dtype, f"pipe b={b} h={h}")
 
 
+@pytest.mark.parametrize("Lq", [384, 448])
 @pytest.mark.parametrize("case", ["growing", "shrinking", "bump", "flat_x6", "negative"])
-def test_pipe_kernel_large_scores(cuda, case):
+def test_pipe_kernel_large_scores(cuda, case, Lq):
     """Scores far above the running max of earlier keys, so that the rare rescale runs in every
     block and many steps (growing key norms, a bump of large keys, flat large scores), scores
     whose first step holds the max (shrinking), and rows whose scores are all very negative (the
@@ -219,8 +227,8 @@ def test_pipe_kernel_large_scores(cuda, case):
     P in peaked rows (the previous kernel gives the same outputs bit for bit); bound 3e-2."""
     from whisperdrz_amd import scaled_dot_product_attention
 
-    B, H, Lq, Lk, D = 2, 128, 384, 700, 64
-    print(f"pipe large scores: {case}", flush=True)
+    B, H, Lk, D = 2, 128, 700, 64  # Lq 384: three blocks per wavefront; 448: two
+    print(f"pipe large scores: {case} Lq={Lq}", flush=True)
     q = randn((B, Lq, H, D), 5, torch.bfloat16).to(cuda)
     k = randn((B, Lk, H, D), 6, torch.bfloat16).to(cuda)
     v = randn((B, Lk, H, D), 7, torch.bfloat16).to(cuda)

@@ -965,11 +965,8 @@ __global__ __launch_bounds__(kFThreads, 1) void dense_fwd_kernel(DenseArgs a) {
 // ============================================================================================
 constexpr int kPWaves = 4;
 constexpr int kPThreads = kPWaves * 64;
-constexpr int kPBM = 96 * kPWaves;  // queries per workgroup
 constexpr int kPTile = kBN * 64;  // elements of one 64-key tile buffer (unpadded 128-byte rows, swizzled)
 constexpr int kPMinKeys = 64;         // the loop needs two tiles up front
-constexpr int kPQElems = kPBM * 64;   // the Q area: 384 rows of 64 elements (no pad; chunks swizzled)
-constexpr int kPQPieces = kPBM * 128 / kPThreads / 16;  // 1 KB prefetch pieces per wavefront (12)
 
 typedef float f32x32 __attribute__((ext_vector_type(32)));
 typedef uint32_t u32x32 __attribute__((ext_vector_type(32)));
@@ -1019,13 +1016,20 @@ __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, uint32_t o
   "a199", "a200", "a201", "a202", "a203", "a204", "a205", "a206", "a207", "s70", "s71", "s72", "s73", "s74", \
   "s75", "s76", "s77", "s78", "s79", "m0", "vcc", "scc", "memory"
 
-template <typename T>
+// NB: 32-query blocks per wavefront (3: 384-query items; 2: 256-query items for query counts
+// that 384 would pad by more than 15%, such as the DTW decoder's 448 and a prompt's 224).
+template <typename T, int NB>
 __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void dense_pipe_kernel(DenseArgs a) {
   typedef typename Mfma<T>::op_t op_t;
   typedef uint16_t e_t;
-  // [Q rows: 384 x 128 B, 16-byte chunks XOR-swizzled by the row] [four K tile buffers] [four V
-  // tile buffers] (tiles row-major [key][dim] with a 16-byte row pad); O is staged through the
-  // tile buffers at the end of each item
+  static_assert(NB == 2 || NB == 3, "two or three blocks per wavefront");
+  constexpr int kPBM = 32 * NB * kPWaves;   // queries per item
+  constexpr int kPQElems = kPBM * 64;       // the Q area: kPBM rows of 64 elements
+  constexpr int kPQPieces = kPBM * 128 / kPThreads / 16;  // 1 KB Q prefetch pieces per wavefront
+  constexpr int kWQ = 32 * NB;              // queries per wavefront
+  // [Q rows: kPBM x 128 B, 16-byte chunks XOR-swizzled by the row] [four K tile buffers] [four V
+  // tile buffers] (tiles row-major [key][dim], 128-byte rows, chunks XOR-swizzled); O is staged
+  // through the tile buffers at the end of each item
   __shared__ __attribute__((aligned(16))) e_t smem[kPQElems + 8 * kPTile];
   e_t* const tiles = smem + kPQElems;
   static_assert(kPBM * kPitchK <= 8 * kPTile, "O staging must fit the tile buffers");
@@ -1134,9 +1138,9 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
   const uint32_t swz0 = (uint32_t)(((lane & 7) ^ (lane >> 4)) << 4);        // rows 16 w + l / 8
   const uint32_t swz1 = (uint32_t)(((lane & 7) ^ (4 + (lane >> 4))) << 4);  // rows 16 w + 8 + l / 8
   const int tsk = kBN * rs_k, tsv = kBN * rs_v;
-  // the Q prefetch: this lane's piece of row 8j + lane/8 of its wavefront's 96, swizzled chunk
-  const uint32_t qvoff = (uint32_t)((wave * 96 + (lane >> 3)) * rs_q + (((lane & 7) ^ (lane >> 3)) << 4));
-  const int qlds = __builtin_amdgcn_readfirstlane(wave * 96 * 128), qstep = 8 * rs_q;
+  // the Q prefetch: this lane's piece of row 8j + lane/8 of its wavefront's rows, swizzled chunk
+  const uint32_t qvoff = (uint32_t)((wave * kWQ + (lane >> 3)) * rs_q + (((lane & 7) ^ (lane >> 3)) << 4));
+  const int qlds = __builtin_amdgcn_readfirstlane(wave * kWQ * 128), qstep = 8 * rs_q;
 
   // Persistent: each workgroup takes items id, id + G, ... (G = grid size, a multiple of 8 so an
   // item stays on its XCD). While item k runs, item k+1's Q rows arrive in the Q area; its first
@@ -1152,12 +1156,12 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
     const bool has_next = next_id < n_items;
     const Item nxt = item_of(has_next ? next_id : id);
     __syncthreads();  // the Q rows are in place; the previous item is done with the tile buffers
-    u32x16 q0, q1, q2;
+    u32x16 q0, q1, q2 = u32x16{};
 #pragma unroll
-    for (int qb = 0; qb < 3; ++qb)
+    for (int qb = 0; qb < NB; ++qb)
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
-        const int row = wave * 96 + qb * 32 + l32;
+        const int row = wave * kWQ + qb * 32 + l32;
         const u32x4 raw = *reinterpret_cast<const u32x4*>(&smem[row * 64 + (((2 * ks + hl) ^ (row & 7)) << 3)]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -1193,10 +1197,14 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
     [qstep] "s"(qstep), [dmab] "s"(dmab)                                                                          \
   : WDRZ_PIPE_CLOBBERS
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (__is_same(T, Bf16))
+    if constexpr (__is_same(T, Bf16) && NB == 3)
       asm volatile(WDRZ_DENSE_LOOP_BF16 WDRZ_PIPE_OPERANDS);
-    else
+    else if constexpr (__is_same(T, Bf16))
+      asm volatile(WDRZ_DENSE_LOOP_BF16_NB2 WDRZ_PIPE_OPERANDS);
+    else if constexpr (NB == 3)
       asm volatile(WDRZ_DENSE_LOOP_F16 WDRZ_PIPE_OPERANDS);
+    else
+      asm volatile(WDRZ_DENSE_LOOP_F16_NB2 WDRZ_PIPE_OPERANDS);
     __builtin_amdgcn_sched_barrier(0);
 #undef WDRZ_PIPE_OPERANDS
 
@@ -1208,9 +1216,9 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
     // ---- normalise, stage O^T through the tile buffers as [query][dim] rows, store whole rows ----
     __syncthreads();  // every wavefront is done with the tiles
 #pragma unroll
-    for (int qb = 0; qb < 3; ++qb) {
+    for (int qb = 0; qb < NB; ++qb) {
       const float inv = 1.f / (lr[qb] + __shfl_xor(lr[qb], 32));
-      e_t* orow = &tiles[(wave * 96 + qb * 32 + l32) * kPitchK];
+      e_t* orow = &tiles[(wave * kWQ + qb * 32 + l32) * kPitchK];
 #pragma unroll
       for (int db = 0; db < 2; ++db)
 #pragma unroll
@@ -1746,18 +1754,23 @@ hipError_t launch_typed(const DenseArgs& a, hipStream_t stream) {
       split(a, bh);
       return hipGetLastError();
     }
-    // the hand-scheduled 384-query kernel when its items fill the chip and its query blocks
-    // are mostly full (padding <= 15% of the rows: the encoder's 1500 in 4 x 384; the DTW
-    // decoder's 448 would compute 768 and runs faster on the 512-query kernel + key split)
-    const int64_t np = bh * ((a.Lq + kPBM - 1) / kPBM);
-    const bool full = (a.Lq + kPBM - 1) / kPBM * kPBM * 100 <= (int64_t)a.Lq * 115;
-    // its global transfers use 32-bit byte offsets within one head's rows
+    // the hand-scheduled kernel when its items fill the chip and its query blocks are mostly full
+    // (padding <= 15% of the rows): 384-query items (the encoder's 1500 = 4 x 384 - 36), else
+    // 256-query items (the DTW decoder's 448, a prompt's 224)
     const int64_t lim = 0x7fffffff;
     const bool offs32 = (int64_t)a.Lk * a.ks[2] * 2 < lim && (int64_t)a.Lk * a.vs[2] * 2 < lim &&
                         (int64_t)a.Lq * a.qs[2] * 2 < lim && (int64_t)a.Lq * a.os[2] * 2 < lim;
-    if (a.Lk >= kPMinKeys && full && offs32 && np >= kNumCus && np <= 0x7fffffff) {
+    auto fits = [&](int64_t bm) {
+      const int64_t items = bh * ((a.Lq + bm - 1) / bm);
+      return (a.Lq + bm - 1) / bm * bm * 100 <= (int64_t)a.Lq * 115 && items >= kNumCus && items <= lim;
+    };
+    if (a.Lk >= kPMinKeys && offs32 && fits(32 * 3 * kPWaves)) {
       // persistent: one workgroup per CU, each taking every 256th item
-      hipLaunchKernelGGL((dense_pipe_kernel<T>), dim3((unsigned)kNumCus), dim3(kPThreads), 0, stream, a);
+      hipLaunchKernelGGL((dense_pipe_kernel<T, 3>), dim3((unsigned)kNumCus), dim3(kPThreads), 0, stream, a);
+      return hipGetLastError();
+    }
+    if (a.Lk >= kPMinKeys && offs32 && fits(32 * 2 * kPWaves)) {
+      hipLaunchKernelGGL((dense_pipe_kernel<T, 2>), dim3((unsigned)kNumCus), dim3(kPThreads), 0, stream, a);
       return hipGetLastError();
     }
     const int64_t bh_main = (n / kNumCus) * kNumCus / qf;  // heads filling whole rounds

@@ -93,7 +93,8 @@ def ar(lo, n=1):
 
 
 class Gen:
-    def __init__(self, dtype):
+    def __init__(self, dtype, nb=3):
+        self.nb = nb  # 32-query blocks per wavefront (3: 96 queries, 2: 64)
         self.mfma = "v_mfma_f32_32x32x16_bf16" if dtype == "bf16" else "v_mfma_f32_32x32x16_f16"
         self.cvt = "v_cvt_pk_bf16_f32" if dtype == "bf16" else "v_cvt_pk_f16_f32"
         self.out = []
@@ -193,7 +194,7 @@ class Gen:
         index: [instructions after it]}. mask: the step is the last one and may hold keys past Lk."""
         slots = slots or {}
         if ph == 0:
-            mb, kbuf, vbuf = 2, p, 1 - p
+            mb, kbuf, vbuf = self.nb - 1, p, 1 - p
         else:
             mb, kbuf, vbuf = ph - 1, 1 - p, p
         mf = []
@@ -225,10 +226,17 @@ class Gen:
         self.rare_block(ph, label, back)
 
     def final_pv(self, vbuf):
-        """P V of block 2 of the last step (the loop leaves it to the next step's phase 0)."""
+        """P V of the last block of the last step (the loop leaves it to the next step's phase 0)."""
         for ks in range(4):
             ch, db = divmod(ks, 2)
-            self.emit(self.mfma_pv(2, ch, db, vbuf))
+            self.emit(self.mfma_pv(self.nb - 1, ch, db, vbuf))
+
+    def read_slots(self, kr, vrd):
+        """The slots of a step's last phases that take the K reads (after the scores' MFMAs that
+        use the other K buffer) and the V^T reads (once phase 0's P V is issued)."""
+        if self.nb == 3:
+            return {3: kr[:2], 4: kr[2:]}, {1: vrd[0:2], 2: vrd[2:4], 3: vrd[4:6], 4: vrd[6:8]}
+        return {}, {1: vrd[0:2], 2: vrd[2:4], 3: kr[:2] + vrd[4:6], 4: kr[2:] + vrd[6:8]}
 
     def k_reads(self, p):
         """K(s+2) -> K buffer p: tile t+1, half p (base KADDR)."""
@@ -289,9 +297,15 @@ class Gen:
         kr0, vr0 = self.k_reads(0), self.v_reads(0)
         kr1, vr1 = self.k_reads(1), self.v_reads(1)
         # step 2t (parity 0)
+        last = self.nb - 1
+        ks0, vs0 = self.read_slots(kr0, vr0)
+        ks1, vs1 = self.read_slots(kr1, vr1)
         self.phase(0, 0, f"0P0{it}")
-        self.phase(0, 1, f"1P0{it}", pre=["s_waitcnt lgkmcnt(0)"], slots={3: kr0[:2], 4: kr0[2:]})
-        self.phase(0, 2, f"2P0{it}", slots={1: vr0[0:2], 2: vr0[2:4], 3: vr0[4:6], 4: vr0[6:8]})
+        if self.nb == 3:
+            self.phase(0, 1, f"1P0{it}", pre=["s_waitcnt lgkmcnt(0)"], slots=ks0)
+            self.phase(0, 2, f"2P0{it}", slots=vs0)
+        else:
+            self.phase(0, 1, f"1P0{it}", pre=["s_waitcnt lgkmcnt(0)"], slots=vs0)
         # step 2t+1 (parity 1): the forced first-step rescale is over
         e(f"s_mov_b32 {S_LIMIT}, {SUM_LIMIT}")
         e(f"s_mov_b32 {S_FLOOR}, 0")
@@ -311,8 +325,11 @@ class Gen:
             f"LNQ{it}_%=:",
         ]
         self.phase(1, 0, f"0P1{it}", slots={1: pf + ld, 2: adv})
-        self.phase(1, 1, f"1P1{it}", pre=["s_waitcnt lgkmcnt(0)"], slots={3: kr1[:2], 4: kr1[2:]})
-        self.phase(1, 2, f"2P1{it}", slots={1: vr1[0:2], 2: vr1[2:4], 3: vr1[4:6], 4: vr1[6:8]})
+        if self.nb == 3:
+            self.phase(1, 1, f"1P1{it}", pre=["s_waitcnt lgkmcnt(0)"], slots=ks1)
+            self.phase(1, 2, f"2P1{it}", slots=vs1)
+        else:
+            self.phase(1, 1, f"1P1{it}", pre=["s_waitcnt lgkmcnt(0)"], slots=vs1)
         e("s_waitcnt vmcnt(4) lgkmcnt(0)")  # tile t+2 in LDS (and this wavefront's reads done)
         e("s_barrier")
         e(f"s_add_u32 {S_IT}, {S_IT}, 1")
@@ -331,16 +348,16 @@ class Gen:
         for i in range(16):
             e(f"v_accvgpr_write_b32 {ar(VB(1, 0, 0) + i)}, 0")
         for i in range(8):
-            e(f"v_mov_b32 {vr(P(2) + i)}, 0")
+            e(f"v_mov_b32 {vr(P(self.nb - 1) + i)}, 0")
         for i in range(48):
             e(f"v_mov_b32 {vr(CINIT(0) + i)}, 0")
         for i in range(96):
             e(f"v_accvgpr_write_b32 {ar(i)}, 0")
-        for b in range(3):
+        for b in range(self.nb):
             e(f"v_mov_b32 {vr(MRUN(b))}, 0")
             e(f"v_mov_b32 {vr(LRUN(b))}, 0")
         e("s_waitcnt lgkmcnt(0)")
-        for b in range(2):
+        for b in range(self.nb - 1):
             for ks in range(4):
                 c = "0" if ks == 0 else vr(S(b), 16)
                 e(f"{self.mfma} {vr(S(b), 16)}, {ar(KB(0, ks), 4)}, {ar(Q(b, ks), 4)}, {c}")
@@ -377,25 +394,26 @@ class Gen:
         for i in range(4):
             e(f"v_add_u32 {vr(VADDRT + i)}, {S_TMP}, {vr(VL + i)}")
         tvr = self.v_reads(0, base=VADDRT)
-        self.phase(0, 0, "0T2")
-        self.phase(0, 1, "1T2", pre=["s_waitcnt lgkmcnt(0)"])
-        self.phase(0, 2, "2T2", slots={1: tvr[0:2], 2: tvr[2:4], 3: tvr[4:6], 4: tvr[6:8]})
+        tslots = {1: tvr[0:2], 2: tvr[2:4], 3: tvr[4:6], 4: tvr[6:8]}
+        nb = self.nb
+        for ph in range(nb):
+            pre = ["s_waitcnt lgkmcnt(0)"] if ph == 1 else []
+            self.phase(0, ph, f"{ph}T2", pre=pre, slots=tslots if ph == nb - 1 else None)
         e(f"s_mov_b32 {S_LIMIT}, {SUM_LIMIT}")
         e(f"s_mov_b32 {S_FLOOR}, 0")
         e("s_waitcnt lgkmcnt(0)")
-        self.phase(1, 0, "0T2b", mask=True)
-        self.phase(1, 1, "1T2b", do_s=False, mask=True)
-        self.phase(1, 2, "2T2b", do_s=False, mask=True)
+        for ph in range(nb):
+            self.phase(1, ph, f"{ph}T2b", do_s=ph == 0, mask=True)
         self.final_pv(1)
         e("s_branch LTEND_%=")
         # r = 1: step s_end, masked
         e("LT1_%=:")
-        self.phase(0, 0, "0T1", mask=True)
-        self.phase(0, 1, "1T1", pre=["s_waitcnt lgkmcnt(0)"], do_s=False, mask=True)
-        self.phase(0, 2, "2T1", do_s=False, mask=True)
+        for ph in range(nb):
+            pre = ["s_waitcnt lgkmcnt(0)"] if ph == 1 else []
+            self.phase(0, ph, f"{ph}T1", pre=pre, do_s=ph == 0, mask=True)
         self.final_pv(0)
         e("s_branch LTEND_%=")
-        # r = 0: only block 2's last P V
+        # r = 0: only the last block's last P V
         e("LT0_%=:")
         self.final_pv(1)
         e("LTEND_%=:")
@@ -440,13 +458,15 @@ def render() -> str:
         "",
     ]
     for dtype in ("bf16", "f16"):
-        body = Gen(dtype).build()
-        check_trans_hazards(body)
-        lines.append(f"#define WDRZ_DENSE_LOOP_{dtype.upper()} \\")
-        for s in body:
-            lines.append(f'  "{s}\\n" \\')
-        lines.append('  ""')
-        lines.append("")
+        for nb in (3, 2):
+            body = Gen(dtype, nb).build()
+            check_trans_hazards(body)
+            suffix = "" if nb == 3 else "_NB2"
+            lines.append(f"#define WDRZ_DENSE_LOOP_{dtype.upper()}{suffix} \\")
+            for s in body:
+                lines.append(f'  "{s}\\n" \\')
+            lines.append('  ""')
+            lines.append("")
     return "\n".join(lines) + "\n"
 
 
