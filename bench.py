@@ -365,7 +365,7 @@ def bench_decode(dev, steps: int, warmup: int) -> dict:
     bytes_p = 6 * Bs * sqp * H * D * E  # Q, new K and V read, K and V appended, O written
     res["prefill_self_sq224"] = {
         "workload": "64 streams append a 224-token prompt to empty 448-row self caches (causal), bf16; "
-                    "kv_prefill_kernel in 256-query blocks",
+                    "dense_pipe_kernel<Bf16, 2> through the slot map (256-query items)",
         "us_per_layer": round(us_p, 2), "tflops": round(flop_p / us_p / 1e6, 2),
         "roofline": {"bound": "hbm", "achieved": round(bytes_p / us_p / 1e3, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(bytes_p / us_p / 1e3 / PEAK_HBM_GBS, 4),
@@ -386,7 +386,7 @@ def bench_decode(dev, steps: int, warmup: int) -> dict:
         f"{bytes_c / us_c / 1e3:.0f} GB/s")
     res["prefill_cross_sq224"] = {
         "workload": f"64 streams, {sqp} prompt queries over {Lcross} cross rows (non-causal), bf16; "
-                    "kv_prefill_kernel in 256-query blocks",
+                    "dense_pipe_kernel<Bf16, 2> through the slot map (256-query items)",
         "us_per_layer": round(us_c, 2), "tflops": round(flop_c / us_c / 1e6, 2),
         "roofline": {"bound": "hbm", "achieved": round(bytes_c / us_c / 1e3, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(bytes_c / us_c / 1e3 / PEAK_HBM_GBS, 4), "traffic": None,

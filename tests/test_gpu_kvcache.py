@@ -321,3 +321,36 @@ def test_many_rows_need_no_workspace(cuda, dtype, self_attn):
                                   to_np(v) if self_attn else None, cs if self_attn else None, bidx_np, 0.125)
     assert_close(out, ref, dtype, "sq=40 without workspace")
     assert np.array_equal(to_np(kc), kref) and np.array_equal(to_np(vc), vref)
+
+
+@pytest.mark.parametrize("layout", ["head_major", "slot_major"])
+def test_prefill_cross_dense_route_slots(cuda, layout):
+    """A prompt's cross-attention with enough (row, head) pairs takes the dense hand-scheduled
+    kernel through the slot map: a permuted slot map gives the rows of the identity call
+    permuted, bit for bit; an out-of-range slot id gives that row NaN and leaves the others
+    unchanged; a few rows against the oracle."""
+    from whisperdrz_amd import flash_attn_with_kvcache
+
+    B, sq, H, Lmax = 16, 224, 20, 700
+    print(f"prefill cross dense route: {layout}", flush=True)
+    kc, vc = make_cache(B + 2, Lmax, H, D, torch.bfloat16, cuda, layout, 81)
+    q = randn((B, sq, H, D), 82, torch.bfloat16).to(cuda)
+    ident = torch.arange(B, dtype=torch.int32, device=cuda)
+    perm = torch.from_numpy(np.random.default_rng(83).permutation(B).astype(np.int32)).to(cuda)
+    base = flash_attn_with_kvcache(q, kc, vc, cache_batch_idx=ident, softmax_scale=0.125)
+    # row i of q against slot perm[i]: equal to the identity call on q with row perm[i]
+    qp = torch.empty_like(q)
+    qp[torch.arange(B, device=cuda).long()] = q[perm.long()]
+    outp = flash_attn_with_kvcache(qp, kc, vc, cache_batch_idx=perm, softmax_scale=0.125)
+    bad = perm.clone()
+    bad[3] = B + 2  # outside the pool
+    outb = flash_attn_with_kvcache(qp, kc, vc, cache_batch_idx=bad, softmax_scale=0.125)
+    torch.cuda.synchronize()
+    assert torch.equal(outp, base[perm.long()])
+    assert torch.isnan(outb[3].float()).all()
+    keep = [i for i in range(B) if i != 3]
+    assert torch.equal(outb[keep], outp[keep])
+    kc_np, vc_np = to_np(kc), to_np(vc)
+    for i in (0, 7, B - 1):
+        ref = kvcache_ref(to_np(q[i : i + 1]), kc_np, vc_np, None, None, None, np.array([i], np.int32), 0.125)[0]
+        assert_close(base[i : i + 1], ref, torch.bfloat16, f"prefill cross row {i}")

@@ -1052,15 +1052,19 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
     const e_t *q, *k, *v;
     e_t* o;
     int q0;
+    bool bad;  // the row's slot is outside the cache: NaN output
   };
   auto item_of = [&](int id) {
     const int t = remap_xcd(id, n_items);
     const int qblk = t % n_qblk, bh = t / n_qblk;
     const int b = bh / a.H, h = bh % a.H;
+    const int sl = a.slot ? a.slot[b] : b;
     Item it;
+    it.bad = a.slot && (sl < 0 || sl >= a.n_slots);
+    const int bk = it.bad ? 0 : sl;
     it.q = reinterpret_cast<const e_t*>(a.q) + b * a.qs[0] + h * a.qs[1];
-    it.k = reinterpret_cast<const e_t*>(a.k) + b * a.ks[0] + h * a.ks[1];
-    it.v = reinterpret_cast<const e_t*>(a.v) + b * a.vs[0] + h * a.vs[1];
+    it.k = reinterpret_cast<const e_t*>(a.k) + bk * a.ks[0] + h * a.ks[1];
+    it.v = reinterpret_cast<const e_t*>(a.v) + bk * a.vs[0] + h * a.vs[1];
     it.o = reinterpret_cast<e_t*>(a.o) + b * a.os[0] + h * a.os[1];
     it.q0 = qblk * kPBM;
     return it;
@@ -1217,7 +1221,7 @@ __global__ __launch_bounds__(kPThreads) __attribute__((amdgpu_waves_per_eu(1, 1)
     __syncthreads();  // every wavefront is done with the tiles
 #pragma unroll
     for (int qb = 0; qb < NB; ++qb) {
-      const float inv = 1.f / (lr[qb] + __shfl_xor(lr[qb], 32));
+      const float inv = cur.bad ? __uint_as_float(0x7fc00000u) : 1.f / (lr[qb] + __shfl_xor(lr[qb], 32));
       e_t* orow = &tiles[(wave * kWQ + qb * 32 + l32) * kPitchK];
 #pragma unroll
       for (int db = 0; db < 2; ++db)
@@ -1730,6 +1734,32 @@ __global__ __launch_bounds__(1024) void dense_split4_kernel(DenseArgs a) {
 constexpr int kQB = 1;
 constexpr int kNW = 8;
 
+// The hand-scheduled kernel when its items fill the chip and its query blocks are mostly full
+// (padding <= 15% of the rows): 384-query items (the encoder's 1500 = 4 x 384 - 36), else
+// 256-query items (the DTW decoder's 448, a prompt's 224). Non-causal, 16-bit. Returns whether it
+// launched.
+template <typename T>
+bool launch_pipe(const DenseArgs& a, hipStream_t stream) {
+  const int64_t lim = 0x7fffffff, bh = (int64_t)a.B * a.H;
+  const bool offs32 = (int64_t)a.Lk * a.ks[2] * 2 < lim && (int64_t)a.Lk * a.vs[2] * 2 < lim &&
+                      (int64_t)a.Lq * a.qs[2] * 2 < lim && (int64_t)a.Lq * a.os[2] * 2 < lim;
+  auto fits = [&](int64_t bm) {
+    const int64_t items = bh * ((a.Lq + bm - 1) / bm);
+    return (a.Lq + bm - 1) / bm * bm * 100 <= (int64_t)a.Lq * 115 && items >= kNumCus && items <= lim;
+  };
+  if (a.causal || a.Lk < kPMinKeys || !offs32) return false;
+  if (fits(32 * 3 * kPWaves)) {
+    // persistent: one workgroup per CU, each taking every 256th item
+    hipLaunchKernelGGL((dense_pipe_kernel<T, 3>), dim3((unsigned)kNumCus), dim3(kPThreads), 0, stream, a);
+    return true;
+  }
+  if (fits(32 * 2 * kPWaves)) {
+    hipLaunchKernelGGL((dense_pipe_kernel<T, 2>), dim3((unsigned)kNumCus), dim3(kPThreads), 0, stream, a);
+    return true;
+  }
+  return false;
+}
+
 template <typename T>
 hipError_t launch_typed(const DenseArgs& a, hipStream_t stream) {
   if (!a.causal) {
@@ -1754,25 +1784,7 @@ hipError_t launch_typed(const DenseArgs& a, hipStream_t stream) {
       split(a, bh);
       return hipGetLastError();
     }
-    // the hand-scheduled kernel when its items fill the chip and its query blocks are mostly full
-    // (padding <= 15% of the rows): 384-query items (the encoder's 1500 = 4 x 384 - 36), else
-    // 256-query items (the DTW decoder's 448, a prompt's 224)
-    const int64_t lim = 0x7fffffff;
-    const bool offs32 = (int64_t)a.Lk * a.ks[2] * 2 < lim && (int64_t)a.Lk * a.vs[2] * 2 < lim &&
-                        (int64_t)a.Lq * a.qs[2] * 2 < lim && (int64_t)a.Lq * a.os[2] * 2 < lim;
-    auto fits = [&](int64_t bm) {
-      const int64_t items = bh * ((a.Lq + bm - 1) / bm);
-      return (a.Lq + bm - 1) / bm * bm * 100 <= (int64_t)a.Lq * 115 && items >= kNumCus && items <= lim;
-    };
-    if (a.Lk >= kPMinKeys && offs32 && fits(32 * 3 * kPWaves)) {
-      // persistent: one workgroup per CU, each taking every 256th item
-      hipLaunchKernelGGL((dense_pipe_kernel<T, 3>), dim3((unsigned)kNumCus), dim3(kPThreads), 0, stream, a);
-      return hipGetLastError();
-    }
-    if (a.Lk >= kPMinKeys && offs32 && fits(32 * 2 * kPWaves)) {
-      hipLaunchKernelGGL((dense_pipe_kernel<T, 2>), dim3((unsigned)kNumCus), dim3(kPThreads), 0, stream, a);
-      return hipGetLastError();
-    }
+    if (launch_pipe<T>(a, stream)) return hipGetLastError();
     const int64_t bh_main = (n / kNumCus) * kNumCus / qf;  // heads filling whole rounds
     const int64_t bh_rest = bh - bh_main;
     if (bh_main > 0 && bh_rest > 0 && bh_rest * q2 <= kNumCus && bh_rest * qf * 2 <= kNumCus) {
@@ -1800,6 +1812,36 @@ hipError_t launch_typed(const DenseArgs& a, hipStream_t stream) {
 }  // namespace
 
 hipError_t launch_kv_prefill(int dtype, const KvArgs& a, hipStream_t stream) {
+  if (a.kn == nullptr && (dtype == 1 || dtype == 2)) {
+    // cross-attention over whole cache rows: the dense hand-scheduled kernel with the slot map
+    // (strides here in elements: DenseArgs orders them b, h, row)
+    DenseArgs d{};
+    d.q = a.q;
+    d.k = a.kc;
+    d.v = a.vc;
+    d.o = a.o;
+    d.B = a.B;
+    d.H = a.H;
+    d.Lq = a.sq;
+    d.Lk = a.Lk;
+    d.causal = 0;
+    d.bh0 = 0;
+    const int64_t qs[3] = {a.qs[0], a.qs[2], a.qs[1]}, ks[3] = {a.kcs[0], a.kcs[2], a.kcs[1]};
+    const int64_t vs[3] = {a.vcs[0], a.vcs[2], a.vcs[1]}, os[3] = {a.os[0], a.os[2], a.os[1]};
+    bool aligned = true;
+    for (int i = 0; i < 3; ++i) {
+      aligned = aligned && qs[i] % 2 == 0 && ks[i] % 2 == 0 && vs[i] % 2 == 0 && os[i] % 2 == 0;
+      d.qs[i] = qs[i] / 2;
+      d.ks[i] = ks[i] / 2;
+      d.vs[i] = vs[i] / 2;
+      d.os[i] = os[i] / 2;
+    }
+    d.c = a.c;
+    d.slot = a.bidx;
+    d.n_slots = a.n_slots;
+    const bool ok = aligned && (dtype == 2 ? launch_pipe<Bf16>(d, stream) : launch_pipe<F16>(d, stream));
+    if (ok) return hipGetLastError();
+  }
   const int n_qblk = (a.sq + 255) / 256;
   const dim3 grid((unsigned)(a.B * n_qblk), (unsigned)a.H);
   const bool has_new = a.kn != nullptr;

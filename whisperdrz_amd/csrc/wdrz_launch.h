@@ -54,6 +54,10 @@ struct DenseArgs {
   int bh0;                             // first (b * H + h) of a dense_split_kernel launch
   int64_t qs[3], ks[3], vs[3], os[3];  // b, h, l strides
   float c;                             // softmax scale * log2(e)
+  // dense_pipe_kernel only: K/V of batch row b at slot slot[b] (nullptr: b); a slot outside
+  // [0, n_slots) gives that row's output as NaN, as the cached-attention kernels do
+  const int32_t* slot = nullptr;
+  int n_slots = 0;
 };
 hipError_t launch_dense_mfma(int dtype, const DenseArgs& a, hipStream_t stream);
 // The same on the fp32 matrix cores (fp32 inputs and output; causal = top-left).
