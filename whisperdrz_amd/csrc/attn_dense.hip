@@ -949,24 +949,24 @@ __global__ __launch_bounds__(kFThreads, 1) void dense_fwd_kernel(DenseArgs a) {
 }
 
 // ============================================================================================
-// Non-causal kernel with a hand-scheduled main loop (the encoder shape): 256-thread workgroups,
-// one wavefront per SIMD, 96 queries per wavefront (three 32-query blocks), 384 queries per
-// workgroup. With two wavefronts per SIMD (dense_fwd_kernel above) the softmax VALU work and the
-// MFMAs of the two largely serialise; here a single instruction stream per SIMD interleaves them
-// explicitly: while the VALU runs block b's softmax the matrix pipe runs the MFMAs of the block
-// before it, whose inputs are all a phase old (gen_dense_loop.py, which emits the loop, gives
-// the schedule and the register map). 384-query blocks also make the encoder launch whole rounds
-// (B=16: 320 heads x 4 blocks = 5 x 256 workgroups).
+// Non-causal kernel with a hand-scheduled main loop (the encoder shape): persistent, one
+// 256-thread workgroup per CU, one wavefront per SIMD; an item is (b, h, query block) of 384
+// queries (three 32-query blocks per wavefront) or 256 (two). With two wavefronts per SIMD
+// (dense_fwd_kernel above) the softmax VALU work and the MFMAs of the two largely serialise; here
+// a single instruction stream per SIMD interleaves them explicitly: while the VALU runs block b's
+// softmax the matrix pipe runs the MFMAs of the block before it, whose inputs are all a phase old
+// (gen_dense_loop.py, which emits the loop, gives the schedule and the register map). 384-query
+// items also make the encoder launch whole rounds (B=16: 320 heads x 4 blocks = 5 x 256 items).
 //
-// The C++ around the loop stages Q (pre-scaled by scale*log2(e)) into its operand registers,
-// and the first two K/V tiles into LDS (the loop code requests the next ones itself); the loop
-// code also runs the last (partial) steps, and the C++ normalises and stores O through LDS as
-// whole rows.
+// The C++ around the loop turns the item's Q rows (in LDS, requested by the previous item's loop)
+// into operand registers pre-scaled by scale*log2(e) and stores the first two K/V tiles into LDS
+// (the loop requests the next ones itself, straight into LDS); the loop code also runs the last
+// (partial) steps, and the C++ normalises and stores O through LDS as whole rows.
 // ============================================================================================
 constexpr int kPWaves = 4;
 constexpr int kPThreads = kPWaves * 64;
 constexpr int kPTile = kBN * 64;  // elements of one 64-key tile buffer (unpadded 128-byte rows, swizzled)
-constexpr int kPMinKeys = 64;         // the loop needs two tiles up front
+constexpr int kPMinKeys = 64;     // the loop needs two tiles up front
 
 typedef float f32x32 __attribute__((ext_vector_type(32)));
 typedef uint32_t u32x32 __attribute__((ext_vector_type(32)));
