@@ -2,9 +2,11 @@
 
 Usage: python gen_dense_loop.py [out_path]   (whisperdrz_amd/build.py runs it before compiling)
 
-The loop is one inline-asm statement per element type (bf16 / fp16) over physical registers that
-the kernel binds with register constraints. Design (one wavefront per SIMD, 96 queries per
-wavefront as three 32-query blocks b = 0, 1, 2; 32 keys per step, 64-key LDS tiles):
+The loop is one inline-asm statement per element type (bf16 / fp16) and form over physical
+registers that the kernel binds with register constraints. Design (one wavefront per SIMD, 96
+queries per wavefront as three 32-query blocks b = 0, 1, 2 -- or, in the two-block form, 64 as
+blocks 0, 1 with two phases per step, block 1 in the role of block 2 below; 32 keys per step,
+64-key LDS tiles):
 
   * Each step s runs three phases. Phase b runs the online softmax of block b's scores S(s)[b]
     on the VALU (exp2, bf16/fp16 packs of P, row sums, the rescale check) while the matrix pipe
