@@ -139,9 +139,9 @@ def bench_encoder(dev, steps: int, warmup: int) -> dict:
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-            "traffic": measured_traffic("dense_pipe_kernel<wdrz::Bf16>"),
+            "traffic": measured_traffic("dense_pipe_kernel<wdrz::Bf16, 3>"),
             "traffic_source": "profiles/pmc_traffic.json (rocprofv3 FETCH_SIZE/WRITE_SIZE passes)",
-            "kernel": "dense_pipe_kernel<Bf16>",
+            "kernel": "dense_pipe_kernel<Bf16, 3>",
             "flop_per_launch": flop_layer,
             "ms_per_launch": ms_launch,
             # softmax exponentials per layer (B*H*L^2) and their rate: the VALU side of the kernel
@@ -365,7 +365,7 @@ def bench_decode(dev, steps: int, warmup: int) -> dict:
     bytes_p = 6 * Bs * sqp * H * D * E  # Q, new K and V read, K and V appended, O written
     res["prefill_self_sq224"] = {
         "workload": "64 streams append a 224-token prompt to empty 448-row self caches (causal), bf16; "
-                    "dense_pipe_kernel<Bf16, 2> through the slot map (256-query items)",
+                    "kv_prefill_kernel in 256-query blocks",
         "us_per_layer": round(us_p, 2), "tflops": round(flop_p / us_p / 1e6, 2),
         "roofline": {"bound": "hbm", "achieved": round(bytes_p / us_p / 1e3, 1), "peak": PEAK_HBM_GBS,
                      "unit": "GB/s", "frac": round(bytes_p / us_p / 1e3 / PEAK_HBM_GBS, 4),
@@ -1049,7 +1049,7 @@ def cpu_baseline(budget_s: float = 12.0) -> dict:
 # Algorithmic HBM bytes per launch of each kernel at the pmc_sample shapes (what the kernel must
 # read and write at least), against which the measured traffic is compared.
 _ALG_BYTES = {
-    "dense_pipe_kernel<wdrz::Bf16>": 4 * 16 * 1500 * 20 * 64 * 2,  # Q + K + V + O
+    "dense_pipe_kernel<wdrz::Bf16, 3>": 4 * 16 * 1500 * 20 * 64 * 2,  # Q + K + V + O
     "kv_attn_kernel<wdrz::Bf16, 1, true>": 68526592,
     "kv_attn_kernel<wdrz::Bf16, 1, false>": 491847936,
     "kv_mq_kernel<wdrz::Bf16, true, 8>": 75279872,
