@@ -214,9 +214,58 @@ def test_pipe_kernel_shapes(cuda, dtype, B, H, Lq, Lk):
         assert_close(out[b : b + 1, h : h + 1], ref, dtype, f"pipe b={b} h={h}")
 
 
-@pytest.mark.parametrize("Lq", [384, 448])
+CAUSAL_SHAPES = [
+    # (B, H, Lq, Lk): causal 16-bit launches (dense_mfma_kernel, top-left mask as torch's
+    # is_causal): the DTW decoder's 448 x 448 self pass at full shape, a partial last 32-key
+    # step, Lq < Lk and Lq > Lk (rows past Lk see every key), many query blocks per head
+    (16, 20, 448, 448),
+    (2, 128, 224, 224),
+    (1, 256, 250, 250),
+    (2, 64, 480, 480),
+    (1, 128, 448, 1500),
+    (1, 128, 700, 300),
+    (2, 64, 1000, 1000),
+]
+
+
+def _masked_ref(qb, kb, vb, causal):
+    s = qb @ kb.transpose(1, 2) * 0.125
+    if causal:
+        Lq, Lk = s.shape[-2:]
+        keep = torch.ones(Lq, Lk, dtype=torch.bool, device=s.device).tril()
+        s = s.masked_fill(~keep, float("-inf"))
+    return torch.softmax(s, dim=-1) @ vb
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("B,H,Lq,Lk", CAUSAL_SHAPES)
+def test_dense_causal_shapes(cuda, dtype, B, H, Lq, Lk):
+    """Causal launches on every head against a float64 evaluation on the device (top-left mask,
+    as torch's is_causal), and a few heads against the float64 numpy oracle; 2e-2 max-abs."""
+    print(f"dense causal dtype={dtype} B={B} H={H} Lq={Lq} Lk={Lk}", flush=True)
+    from whisperdrz_amd import scaled_dot_product_attention
+
+    D = 64
+    q = randn((B, Lq, H, D), 41 + Lk, dtype).to(cuda)
+    k = randn((B, Lk, H, D), 42 + Lk, dtype).to(cuda)
+    v = randn((B, Lk, H, D), 43 + Lk, dtype).to(cuda)
+    out = scaled_dot_product_attention(q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3),
+                                       is_causal=True, scale=0.125)
+    torch.cuda.synchronize()
+    for b in range(B):
+        qb, kb, vb = (x[b].permute(1, 0, 2).double() for x in (q, k, v))
+        err = (out[b].double() - _masked_ref(qb, kb, vb, True)).abs().max().item()
+        assert err <= 2e-2, f"b={b}: max|diff|={err:.3e}"
+    for b, h in ((0, 0), (B - 1, H - 1), (B // 2, H // 3)):
+        ref = sdpa_ref(to_np(q[b : b + 1, :, h : h + 1].permute(0, 2, 1, 3)),
+                       to_np(k[b : b + 1, :, h : h + 1].permute(0, 2, 1, 3)),
+                       to_np(v[b : b + 1, :, h : h + 1].permute(0, 2, 1, 3)), scale=0.125, causal=True)
+        assert_close(out[b : b + 1, h : h + 1], ref, dtype, f"causal b={b} h={h}")
+
+
+@pytest.mark.parametrize("Lq,causal", [(384, False), (448, False), (448, True)])
 @pytest.mark.parametrize("case", ["growing", "shrinking", "bump", "flat_x6", "negative"])
-def test_pipe_kernel_large_scores(cuda, case, Lq):
+def test_pipe_kernel_large_scores(cuda, case, Lq, causal):
     """Scores far above the running max of earlier keys, so that the rare rescale runs in every
     block and many steps (growing key norms, a bump of large keys, flat large scores), scores
     whose first step holds the max (shrinking), and rows whose scores are all very negative (the
@@ -224,11 +273,12 @@ def test_pipe_kernel_large_scores(cuda, case, Lq):
     16-bit type; at these score magnitudes that rounding alone moves the output by more than the
     N(0,1) tolerance, so the float64 reference here uses the same rounded Q: what is checked is
     the online softmax, the rescaling and the merge. The remaining error is the 16-bit rounding of
-    P in peaked rows (the previous kernel gives the same outputs bit for bit); bound 3e-2."""
+    P in peaked rows (the previous kernel gives the same outputs bit for bit); bound 3e-2. The
+    causal cases run on dense_mfma_kernel, whose lazy rescale checks each step's max instead."""
     from whisperdrz_amd import scaled_dot_product_attention
 
-    B, H, Lk, D = 2, 128, 700, 64  # Lq 384: three blocks per wavefront; 448: two
-    print(f"pipe large scores: {case} Lq={Lq}", flush=True)
+    B, H, Lk, D = 2, 128, 700, 64  # Lq 384: three blocks per wavefront; 448: two; causal: the causal kernel
+    print(f"pipe large scores: {case} Lq={Lq} causal={causal}", flush=True)
     q = randn((B, Lq, H, D), 5, torch.bfloat16).to(cuda)
     k = randn((B, Lk, H, D), 6, torch.bfloat16).to(cuda)
     v = randn((B, Lk, H, D), 7, torch.bfloat16).to(cuda)
@@ -239,14 +289,14 @@ def test_pipe_kernel_large_scores(cuda, case, Lq):
     if case == "negative":
         q[:, :, ::7] = (q[:, :, ::7].float() * -40.0).to(torch.bfloat16)
     out = scaled_dot_product_attention(q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3),
-                                       scale=0.125)
+                                       is_causal=causal, scale=0.125)
     torch.cuda.synchronize()
     c = 0.125 * 1.4426950408889634
     q_eff = (q.float() * c).to(torch.bfloat16).double() / c  # Q as the kernel holds it
     for b in range(B):
         qb = q_eff[b].permute(1, 0, 2)
         kb, vb = (x[b].permute(1, 0, 2).double() for x in (k, v))
-        ref = torch.softmax(qb @ kb.transpose(1, 2) * 0.125, dim=-1) @ vb
+        ref = _masked_ref(qb, kb, vb, causal)
         assert torch.isfinite(out[b]).all()
         err = (out[b].double() - ref).abs().max().item()
         assert err <= 3e-2, f"b={b}: max|diff|={err:.3e}"
