@@ -19,8 +19,9 @@ blocks 0, 1 with two phases per step, block 1 in the role of block 2 below; 32 k
   * The running max is subtracted inside the MFMA: every score chain starts from cinit[b] =
     -m_run[b]. The rescale check runs on the step's row sum (a lane's 16 P values summing above
     1024 means a score exceeded the max by more than 6 in log2 units); the rare rescale takes
-    the true max, rescales O (AGPRs), l and cinit, and redoes the block's softmax. The first
-    step always takes it (its limit register is -1), which establishes the max. The compare is
+    the true max, rescales O (AGPRs), l and cinit, and redoes the block's softmax. The running
+    max starts at the true max of the first step: the prologue computes every block's step-0
+    scores and takes their row max before the loop. The compare is
     placed a few instructions before the phase's branch (a branch on a VCC the VALU has only just
     written stalls the in-order wavefront).
   * K and V operands for the MFMAs come from LDS one step ahead into double-buffered AGPRs
@@ -76,7 +77,7 @@ def VB(p, ch, db): return 176 + 16 * p + 8 * ch + 4 * db
 
 S_N = None  # the iteration count comes in through an operand: %[n]
 S_IT, S_BUFA, S_BUFB, S_BUFC, S_TMP = "s70", "s71", "s72", "s73", "s74"
-S_LIMIT, S_FLOOR = "s76", "s78"
+S_LIMIT = "s76"
 SRD_K, SRD_V, SRD_Q = "s[80:83]", "s[84:87]", "s[88:91]"
 
 TILE_BYTES = 64 * 128      # one 64-key tile of K (or V): 64 rows of 128 bytes, 16-byte chunks
@@ -128,40 +129,39 @@ class Gen:
         v.append(f"v_add_f32 {vr(U(b) + 4)}, {vr(U(b) + 4)}, {vr(U(b) + 6)}")
         v.append(f"v_add_f32 {vr(U(b))}, {vr(U(b))}, {vr(U(b) + 4)}")
         if check:
-            # sum > limit in any lane -> rescale; the limit register is -1 in the first step, so
-            # that step always takes the true max
+            # sum > limit in any lane -> rescale
             v.append(f"v_cmp_lt_f32 vcc, {S_LIMIT}, {vr(U(b))}")
         for j in range(8):
             v.append(f"{self.cvt} {vr(P(b) + j)}, {vr(T0 + 2 * j)}, {vr(T0 + 2 * j + 1)}")
         return v
 
+    def row_max(self, b, mx):
+        """mx = the max of block b's scores over the row (this lane's 16 and its partner lane's
+        l ^ 32); uses mx + 1."""
+        s0 = S(b)
+        v = [f"v_max3_f32 {vr(mx)}, {vr(s0)}, {vr(s0 + 1)}, {vr(s0 + 2)}"]
+        for i in range(3, 15, 2):
+            v.append(f"v_max3_f32 {vr(mx)}, {vr(mx)}, {vr(s0 + i)}, {vr(s0 + i + 1)}")
+        v.append(f"v_max_f32 {vr(mx)}, {vr(mx)}, {vr(s0 + 15)}")
+        v.append(f"v_mov_b32 {vr(mx + 1)}, {vr(mx)}")
+        v.append("s_nop 1")
+        v.append(f"v_permlane32_swap_b32 {vr(mx)}, {vr(mx + 1)}")
+        v.append(f"v_max_f32 {vr(mx)}, {vr(mx)}, {vr(mx + 1)}")
+        return v
+
     def rare_block(self, b, label, back):
-        """Rescale of block b (rare): true max, O / l / cinit rescaled, softmax redone."""
+        """Rescale of block b (rare): the step's true max, O / l / cinit rescaled, softmax redone."""
         r = self.rare
         r.append(f"{label}:")
         r.append("s_nop 7")
         r.append("s_nop 7")
-        mx, mx2, dl, al = RT, RT + 1, RT + 2, RT + 3
-        s0 = S(b)
-        r.append(f"v_max3_f32 {vr(mx)}, {vr(s0)}, {vr(s0 + 1)}, {vr(s0 + 2)}")
-        for i in range(3, 15, 2):
-            r.append(f"v_max3_f32 {vr(mx)}, {vr(mx)}, {vr(s0 + i)}, {vr(s0 + i + 1)}")
-        r.append(f"v_max_f32 {vr(mx)}, {vr(mx)}, {vr(s0 + 15)}")
-        r.append(f"v_mov_b32 {vr(mx2)}, {vr(mx)}")
-        r.append("s_nop 1")
-        r.append(f"v_permlane32_swap_b32 {vr(mx)}, {vr(mx2)}")
-        r.append(f"v_max3_f32 {vr(dl)}, {vr(mx)}, {vr(mx2)}, {S_FLOOR}")  # delta (>= 0 except forced)
+        mx, dl, al = RT, RT + 2, RT + 3
+        r.extend(self.row_max(b, mx))
+        r.append(f"v_max_f32 {vr(dl)}, 0, {vr(mx)}")  # delta >= 0: the max only grows
         r.append(f"v_add_f32 {vr(MRUN(b))}, {vr(MRUN(b))}, {vr(dl)}")
         r.append(f"v_exp_f32_e64 {vr(al)}, -{vr(dl)}")
         r.append("s_nop 1")  # a transcendental's result is not forwarded to the next VALU instruction
-        # alpha <= 1: in the forced first step delta may be any negative number, but O and l are
-        # still zero there, and exp2(-delta) = inf would turn them into NaN
-        r.append(f"v_min_f32 {vr(al)}, 1.0, {vr(al)}")
         r.append(f"v_mul_f32 {vr(LRUN(b))}, {vr(LRUN(b))}, {vr(al)}")
-        # O is still zero in the forced first step (its floor register is -inf then): no rescale
-        skip = label.replace("R", "N", 1)
-        r.append(f"s_cmp_eq_u32 {S_FLOOR}, 0xff800000")
-        r.append(f"s_cbranch_scc1 {skip}")
         tmp = [RT + 4 + i for i in range(8)]
         for i0 in range(0, 32, 8):
             for i in range(8):
@@ -170,7 +170,6 @@ class Gen:
                 r.append(f"v_mul_f32 {vr(tmp[i])}, {vr(al)}, {vr(tmp[i])}")
             for i in range(8):
                 r.append(f"v_accvgpr_write_b32 {ar(O(b, 0) + i0 + i)}, {vr(tmp[i])}")
-        r.append(f"{skip}:")
         for i in range(16):
             r.append(f"v_sub_f32 {vr(CINIT(b) + i)}, 0, {vr(MRUN(b))}")
         for i in range(16):
@@ -308,9 +307,7 @@ class Gen:
             self.phase(0, 2, f"2P0{it}", slots=vs0)
         else:
             self.phase(0, 1, f"1P0{it}", pre=["s_waitcnt lgkmcnt(0)"], slots=vs0)
-        # step 2t+1 (parity 1): the forced first-step rescale is over
-        e(f"s_mov_b32 {S_LIMIT}, {SUM_LIMIT}")
-        e(f"s_mov_b32 {S_FLOOR}, 0")
+        # step 2t+1 (parity 1)
         # the next item's Q rows: piece S_IT of this wavefront's 12 (1 KB each), straight into
         # the Q area (LDS DMA at m0), requested before the tile's pieces so that the wait at the
         # barrier (vmcnt(4)) leaves exactly those in flight
@@ -338,7 +335,8 @@ class Gen:
 
     def build(self):
         e = self.emit
-        # ---- prologue: first operands, zero state, scores of step 0 for blocks 0 and 1 ----
+        # ---- prologue: first operands, zero state, scores of step 0 for every block and the
+        # running max taken from them ----
         for ks in range(4):
             e(f"ds_read_b128 {ar(KB(0, ks), 4)}, {vr(KL + ks)}")
             e(f"ds_read_b128 {ar(KB(1, ks), 4)}, {vr(KL + ks)} offset:{HALF_BYTES}")
@@ -351,15 +349,12 @@ class Gen:
             e(f"v_accvgpr_write_b32 {ar(VB(1, 0, 0) + i)}, 0")
         for i in range(8):
             e(f"v_mov_b32 {vr(P(self.nb - 1) + i)}, 0")
-        for i in range(48):
-            e(f"v_mov_b32 {vr(CINIT(0) + i)}, 0")
         for i in range(96):
             e(f"v_accvgpr_write_b32 {ar(i)}, 0")
         for b in range(self.nb):
-            e(f"v_mov_b32 {vr(MRUN(b))}, 0")
             e(f"v_mov_b32 {vr(LRUN(b))}, 0")
         e("s_waitcnt lgkmcnt(0)")
-        for b in range(self.nb - 1):
+        for b in range(self.nb):
             for ks in range(4):
                 c = "0" if ks == 0 else vr(S(b), 16)
                 e(f"{self.mfma} {vr(S(b), 16)}, {ar(KB(0, ks), 4)}, {ar(Q(b, ks), 4)}, {c}")
@@ -368,8 +363,22 @@ class Gen:
         for x in self.tile_dma() + self.advance():
             e(x)
         e(f"v_mov_b32 {vr(NEGINF)}, 0xff800000")
-        e(f"s_mov_b32 {S_LIMIT}, -1.0")
-        e(f"s_mov_b32 {S_FLOOR}, 0xff800000")
+        # the running max of each block = the true max of its step-0 scores: the score chains
+        # start from -max; the scores of blocks 0 .. nb-2 are shifted here, those of the last
+        # block are computed again by step 0's first phase from the new chain start
+        for b in range(self.nb):
+            if b in (0, self.nb - 1):
+                e("s_nop 7")  # (the scores' MFMAs were issued just before)
+                e("s_nop 7")
+            for x in self.row_max(b, RT):
+                e(x)
+            e(f"v_mov_b32 {vr(MRUN(b))}, {vr(RT)}")
+            for i in range(16):
+                e(f"v_sub_f32 {vr(CINIT(b) + i)}, 0, {vr(RT)}")
+            if b < self.nb - 1:
+                for i in range(16):
+                    e(f"v_sub_f32 {vr(S(b) + i)}, {vr(S(b) + i)}, {vr(RT)}")
+        e(f"s_mov_b32 {S_LIMIT}, {SUM_LIMIT}")
         e(f"s_mov_b32 {S_IT}, 0")
         e("s_cmp_eq_u32 %[n], 0")
         e("s_cbranch_scc1 LEND_%=")
@@ -401,8 +410,6 @@ class Gen:
         for ph in range(nb):
             pre = ["s_waitcnt lgkmcnt(0)"] if ph == 1 else []
             self.phase(0, ph, f"{ph}T2", pre=pre, slots=tslots if ph == nb - 1 else None)
-        e(f"s_mov_b32 {S_LIMIT}, {SUM_LIMIT}")
-        e(f"s_mov_b32 {S_FLOOR}, 0")
         e("s_waitcnt lgkmcnt(0)")
         for ph in range(nb):
             self.phase(1, ph, f"{ph}T2b", do_s=ph == 0, mask=True)
