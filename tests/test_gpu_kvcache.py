@@ -354,3 +354,34 @@ def test_prefill_cross_dense_route_slots(cuda, layout):
     for i in (0, 7, B - 1):
         ref = kvcache_ref(to_np(q[i : i + 1]), kc_np, vc_np, None, None, None, np.array([i], np.int32), 0.125)[0]
         assert_close(base[i : i + 1], ref, torch.bfloat16, f"prefill cross row {i}")
+
+
+@pytest.mark.parametrize("sq", [1, 5, 40])
+def test_causal_flag_is_ignored_as_in_the_reference(cuda, sq):
+    """The reference fallback (model.py:20-76) never reads `causal`: new rows are always masked
+    bottom-right causally and cross calls never are. Same here: causal=False with new rows gives
+    the causal result, and causal=True on a cross call changes nothing (bit for bit)."""
+    from whisperdrz_amd import flash_attn_with_kvcache
+
+    print(f"causal flag sq={sq}", flush=True)
+    B, H, n_slots, Lmax = 4, 3, 6, 448
+    q = randn((B, sq, H, D), 900 + sq, torch.bfloat16).to(cuda)
+    k = randn((B, sq, H, D), 901 + sq, torch.bfloat16).to(cuda)
+    v = randn((B, sq, H, D), 902 + sq, torch.bfloat16).to(cuda)
+    bidx = torch.tensor([3, 0, 5, 1], dtype=torch.int32, device=cuda)
+    cs = torch.tensor([0, 17, Lmax - sq, 200], dtype=torch.int32, device=cuda)
+    outs = {}
+    for causal in (True, False):
+        kc, vc = make_cache(n_slots, Lmax, H, D, torch.bfloat16, cuda, "head_major", 77)
+        outs[causal] = flash_attn_with_kvcache(q, kc, vc, k=k, v=v, cache_seqlens=cs, cache_batch_idx=bidx,
+                                               softmax_scale=0.125, causal=causal)
+    torch.cuda.synchronize()
+    assert torch.equal(outs[True], outs[False])
+    kc, vc = make_cache(n_slots, Lmax, H, D, torch.bfloat16, cuda, "head_major", 77)
+    ref, _, _ = kvcache_ref(to_np(q), to_np(kc), to_np(vc), to_np(k), to_np(v), cs.cpu().numpy(), bidx.cpu().numpy(),
+                            0.125)
+    assert_close(outs[False], ref, torch.bfloat16, "self, causal=False")
+    cross = [flash_attn_with_kvcache(q, kc, vc, cache_batch_idx=bidx, softmax_scale=0.125, causal=c)
+             for c in (False, True)]
+    torch.cuda.synchronize()
+    assert torch.equal(cross[0], cross[1])
