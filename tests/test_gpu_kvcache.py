@@ -385,3 +385,22 @@ def test_causal_flag_is_ignored_as_in_the_reference(cuda, sq):
              for c in (False, True)]
     torch.cuda.synchronize()
     assert torch.equal(cross[0], cross[1])
+
+
+def test_default_scale_is_head_dim_power(cuda):
+    """softmax_scale=None means SDPA's default 1/sqrt(head_dim) (model.py:69-75 passes it to
+    F.scaled_dot_product_attention): bit-identical to an explicit 0.125 at head_dim 64."""
+    from whisperdrz_amd import flash_attn_with_kvcache, scaled_dot_product_attention
+
+    q = randn((3, 2, 4, D), 31, torch.bfloat16).to(cuda)
+    kc, vc = make_cache(5, 300, 4, D, torch.bfloat16, cuda, "head_major", 32)
+    bidx = torch.tensor([4, 1, 2], dtype=torch.int32, device=cuda)
+    a = flash_attn_with_kvcache(q, kc, vc, cache_batch_idx=bidx)
+    b = flash_attn_with_kvcache(q, kc, vc, cache_batch_idx=bidx, softmax_scale=0.125)
+    qd = randn((2, 4, 300, D), 33, torch.bfloat16).to(cuda)
+    kd = randn((2, 4, 300, D), 34, torch.bfloat16).to(cuda)
+    vd = randn((2, 4, 300, D), 35, torch.bfloat16).to(cuda)
+    c = scaled_dot_product_attention(qd, kd, vd)
+    d = scaled_dot_product_attention(qd, kd, vd, scale=0.125)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b) and torch.equal(c, d)
